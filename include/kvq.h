@@ -1,0 +1,175 @@
+/*
+ * kvq.h - C ABI of libkvq.so, the MI355X (gfx950) paged-KV GQA decode attention library.
+ *
+ * The reference (pawaryd/kvq-decode, package `bpt`) runs this path as three Triton kernels
+ * launched from Python by `paged_decode_attention_triton` (src/bpt/triton_fp16.py:183-247).
+ * Each entry point below replaces one of those launches, or the whole wrapper, and says
+ * which. Signatures use plain pointers, element strides and sizes only.
+ *
+ * Conventions
+ *  - Every function returns a kvq_status (0 = KVQ_OK, negative = error). Argument checks
+ *    run on the host from the arguments alone, before any HIP call, and never read device
+ *    memory, so a failed check has no side effects and needs no GPU.
+ *  - Launches are asynchronous on `stream` (a hipStream_t; NULL = the null stream). No
+ *    entry point synchronizes, allocates or frees device memory; the caller owns every
+ *    buffer, including the split-KV workspace. Calls are re-entrant.
+ *  - Strides are in elements of the tensor they describe (fp16 elements for fp16
+ *    tensors, bytes for uint8 code tensors). The innermost dimension of q, out and the
+ *    caches is contiguous.
+ *  - Layout (vLLM style, reference src/bpt/reference.py:3-9):
+ *        q            [batch, q_heads, head_dim]                 fp16
+ *        k/v cache    [num_blocks, block_size, kv_heads, head_dim] fp16, or codes (below)
+ *        block_table  [batch, max_blocks] int32
+ *        seq_lens     [batch] int32
+ *        out          [batch, q_heads, head_dim]                 fp16
+ *  - Every seq_len must be >= 1 (reference asserts it, triton_fp16.py:201). The library
+ *    does not read seq_lens on the host; a seq_len < 1 yields a zero output row, and a
+ *    seq_len above max_blocks * block_size is clamped to it. Block-table entries are
+ *    clamped to [0, num_blocks) on the device so a bad table cannot address memory
+ *    outside the cache.
+ */
+#ifndef KVQ_H
+#define KVQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* kvq_stream_t; /* the same type as hipStream_t */
+
+typedef enum kvq_status {
+    KVQ_OK = 0,
+    KVQ_ERR_NULL_POINTER = -1,  /* a required pointer is NULL */
+    KVQ_ERR_SHAPE = -2,         /* sizes inconsistent (e.g. q_heads % kv_heads != 0) */
+    KVQ_ERR_UNSUPPORTED = -3,   /* valid for the reference, not built here (e.g. head_dim 512) */
+    KVQ_ERR_ALIGNMENT = -4,     /* pointer or stride breaks the 16-byte vector-load alignment */
+    KVQ_ERR_SPLITS = -5,        /* num_splits / pages_per_split inconsistent with max_blocks */
+    KVQ_ERR_FORMAT = -6,        /* unknown kv_format or missing scale/zero tensors */
+    KVQ_ERR_HIP = -7            /* a HIP launch failed (hipGetLastError) */
+} kvq_status;
+
+/* KV cache storage formats. F16 is the reference's format; the quantized ones follow the
+ * KIVI-style spec the reference's byte model assumes (src/bpt/roofline.py:6-9, 22-31):
+ * asymmetric fp16 scale + zero, K per channel over groups of k_group tokens, V per token.
+ *   INT8      codes uint8 [nb, bs, Hkv, D],     x = c * s + z, z = min, s = (max-min)/255
+ *   FP8_E4M3  codes uint8 [nb, bs, Hkv, D],     OCP e4m3fn bits, x = f(c) * s + z,
+ *                                               z = (max+min)/2, s = (max-min)/896
+ *   INT4      codes uint8 [nb, bs, Hkv, D/2],   two codes per byte (low nibble = even
+ *                                               channel), z = min, s = (max-min)/15
+ *   k_scale, k_zero  fp16 [nb, Hkv, D]: group g of sequence b lives in block
+ *                    block_table[b][g * k_group / block_size]
+ *   v_scale, v_zero  fp16 [nb, Hkv, block_size]: one pair per token slot           */
+typedef enum kvq_kv_format {
+    KVQ_KV_F16 = 0,
+    KVQ_KV_INT8 = 1,
+    KVQ_KV_FP8_E4M3 = 2,
+    KVQ_KV_INT4 = 3
+} kvq_kv_format;
+
+/* Everything that describes one decode call's inputs and output. Mirrors the arguments of
+ * paged_decode_attention_triton (triton_fp16.py:183-191) and the strides its launches pass
+ * (triton_fp16.py:221-230, 237-247). */
+typedef struct kvq_decode_args {
+    const void* q;            /* fp16 [batch, q_heads, head_dim] */
+    int64_t q_stride_b, q_stride_h;
+    const void* k_cache;      /* [num_blocks, block_size, kv_heads, head_dim or head_dim/2] */
+    int64_t k_stride_blk, k_stride_tok, k_stride_head;
+    const void* v_cache;
+    int64_t v_stride_blk, v_stride_tok, v_stride_head;
+    const int32_t* block_table; /* [batch, max_blocks] */
+    int64_t bt_stride_b;
+    const int32_t* seq_lens;    /* [batch] */
+    void* out;                /* fp16 [batch, q_heads, head_dim] */
+    int64_t o_stride_b, o_stride_h;
+    int32_t batch, q_heads, kv_heads, head_dim, block_size, max_blocks, num_blocks;
+    float scale;              /* softmax scale; the reference defaults to 1/sqrt(head_dim) */
+    int32_t kv_format;        /* kvq_kv_format */
+    int32_t k_group;          /* tokens per K scale group (quantized formats; 128) */
+    const void* k_scale;      /* fp16 [num_blocks, kv_heads, head_dim], contiguous */
+    const void* k_zero;
+    const void* v_scale;      /* fp16 [num_blocks, kv_heads, block_size], contiguous */
+    const void* v_zero;
+    int32_t waves_per_group;  /* tuning: waves per (kv head, split) workgroup, one of
+                                 1, 2, 4, 8, 16; 0 = the library's choice */
+    int32_t pipeline;         /* tuning: 1 = one chunk of loads per wave at a time (higher
+                                 occupancy), 2 = next chunk's loads in flight during compute;
+                                 0 = the library's choice */
+} kvq_decode_args;
+
+/* Library version string, e.g. "kvq 0.1.0 gfx950". */
+const char* kvq_version(void);
+
+/* Human-readable name of a kvq_status. */
+const char* kvq_status_string(int status);
+
+/* Split-count heuristic, triton_fp16.py:175-180 (choose_num_splits):
+ *   S = max(1, min(next_pow2(cdiv(target_per_cu * cu_count, batch * kv_heads)),
+ *                  max_pages / max(1, min_tokens_per_split / block_size)))
+ * The reference's constants are target_per_cu = 8, min_tokens_per_split = 512
+ * (triton_fp16.py:166-167). Returns S >= 1, or a negative kvq_status. */
+int kvq_choose_num_splits(int32_t batch, int32_t kv_heads, int32_t block_size,
+                          int32_t max_pages, int32_t cu_count, int32_t target_per_cu,
+                          int32_t min_tokens_per_split);
+
+/* Split normalization, triton_fp16.py:211-217: clamps num_splits to [1, max_pages], then
+ * pages_per_split = cdiv(max_pages, S) and S = cdiv(max_pages, pages_per_split).
+ * Writes both; returns KVQ_OK or an error. */
+int kvq_normalize_splits(int32_t num_splits, int32_t max_pages, int32_t* splits_out,
+                         int32_t* pages_per_split_out);
+
+/* Stage 1 of split-KV; replaces the _split_kernel launch (triton_fp16.py:219-230, kernel
+ * :83-144). Grid (kv_heads, num_splits, batch). Split s of sequence b covers pages
+ * [s*pps, min((s+1)*pps, cdiv(seq_len, block_size))) and writes the normalized partial
+ * output and its natural-log LSE:
+ *   o_part fp32 [batch, q_heads, num_splits, head_dim], lse fp32 [batch, q_heads, num_splits]
+ * An empty split writes o = 0, lse = -inf (triton_fp16.py:138-141). */
+int kvq_decode_split(const kvq_decode_args* args, int32_t num_splits, int32_t pages_per_split,
+                     float* o_part, float* lse, kvq_stream_t stream);
+
+/* Stage 2; replaces the _merge_kernel launch (triton_fp16.py:231-234, kernel :147-163):
+ * out[b, h] = sum_s w_s o_part[b, h, s] / sum_s w_s, w_s = exp(lse_s - max_s lse_s).
+ * out is fp16 with the given strides. */
+int kvq_decode_merge(const float* o_part, const float* lse, void* out, int64_t o_stride_b,
+                     int64_t o_stride_h, int32_t batch, int32_t q_heads, int32_t head_dim,
+                     int32_t num_splits, kvq_stream_t stream);
+
+/* Single pass; replaces the _paged_decode_kernel launch (triton_fp16.py:237-247, kernel
+ * :25-80). Grid (kv_heads, 1, batch); writes args->out directly. */
+int kvq_decode_single(const kvq_decode_args* args, kvq_stream_t stream);
+
+/* The whole op after split selection (triton_fp16.py:207-247 minus the heuristic):
+ * normalizes num_splits as kvq_normalize_splits does; if the result is 1, runs the single
+ * pass, otherwise stage 1 then stage 2. o_part and lse must hold
+ * batch*q_heads*S*head_dim and batch*q_heads*S floats for the normalized S (NULL allowed
+ * when S == 1). */
+int kvq_paged_decode(const kvq_decode_args* args, int32_t num_splits, float* o_part,
+                     float* lse, kvq_stream_t stream);
+
+/* Bulk KIVI quantization of fp16 paged caches (no reference counterpart: the reference's
+ * quantized KV is "not started", README.md:16; its byte model is roofline.py:6-9).
+ * For each sequence b and kv head, writes codes for the seq_lens[b] valid token slots of
+ * both caches, K scales/zeros per channel per k_group tokens (stored in the group's first
+ * block) and V scales/zeros per token. Slots past a sequence's length are not written.
+ * k_src/v_src: fp16 caches with the strides in args (args->k_cache / v_cache are the
+ * destination code caches, args->kv_format the target format). */
+int kvq_quantize_cache(const kvq_decode_args* args, const void* k_src, const void* v_src,
+                       int64_t src_stride_blk, int64_t src_stride_tok,
+                       int64_t src_stride_head, kvq_stream_t stream);
+
+/* Quantize-on-append (no reference counterpart; KIVI write path). For each sequence b,
+ * the token at position p = seq_lens[b] - 1 is new: k_new/v_new fp16 [batch, kv_heads,
+ * head_dim] hold it. V is quantized per token into its slot immediately. K is written
+ * to the fp16 residual k_resid [batch, kv_heads, k_group, head_dim] at row p % k_group,
+ * and the group containing p is (re)quantized from the residual rows 0..p%k_group, so
+ * the cache always equals kvq_quantize_cache of all tokens so far.
+ * args->seq_lens must already count the new token. */
+int kvq_quantize_append(const kvq_decode_args* args, const void* k_new, const void* v_new,
+                        void* k_resid, kvq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVQ_H */

@@ -1,0 +1,66 @@
+"""Build libkvq.so (the HIP kernels + C ABI) in-tree for gfx950.
+
+    python -m kvq_decode_amd.build          # or: python kvq_decode_amd/build.py
+
+Compiles csrc/*.hip and csrc/*.cpp with hipcc into kvq_decode_amd/libkvq.so. Always
+recompiles (the build check runs it on every call); a failed compile raises.
+"""
+import os
+import subprocess
+import sys
+import time
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+CSRC = os.path.join(PKG_DIR, "csrc")
+INCLUDE = os.path.join(REPO_DIR, "include")
+LIB_PATH = os.path.join(PKG_DIR, "libkvq.so")
+
+ARCH = "gfx950"
+SOURCES = ["capi.cpp", "decode.hip", "quant.hip"]
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    # Packed fp32 VALU ops (v_pk_{add,mul,fma}_f32) stay off: hipcc would otherwise form
+    # them from ordinary float code. The host pass warns that it does not know the feature.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the softmax rescale works on them with VALU ops, which
+    # would otherwise copy them out of and back into AGPRs every chunk.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
+    # No -ffast-math: fp32 division stays correctly rounded (the quantizer's codes must be
+    # bit-exact with its float32 spec; quant.hip also turns fp contraction off).
+]
+
+
+def hipcc():
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    return os.environ.get("HIPCC", os.path.join(rocm, "bin", "hipcc"))
+
+
+def build(verbose=False):
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    tmp = LIB_PATH + ".tmp"
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *srcs, "-o", tmp]
+    t0 = time.time()
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    noise = ("packed-fp32-ops", "is not a recognized feature")
+    msgs = [ln for ln in (proc.stdout + proc.stderr).splitlines()
+            if not any(n in ln for n in noise)]
+    if proc.returncode != 0:
+        raise RuntimeError("hipcc failed (%d):\n%s\ncommand: %s"
+                           % (proc.returncode, "\n".join(msgs), " ".join(cmd)))
+    os.replace(tmp, LIB_PATH)
+    if verbose:
+        for m in msgs:
+            print(m)
+        print(f"built {LIB_PATH} in {time.time() - t0:.1f}s")
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build(verbose=True)
+    sys.exit(0)

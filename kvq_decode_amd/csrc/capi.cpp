@@ -1,0 +1,265 @@
+// C ABI of libkvq.so (declared in include/kvq.h): argument validation and dispatch.
+// Every check here reads only the arguments - never device memory - and runs before
+// any HIP call, so a rejected call has no side effects and needs no GPU.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kvq.h"
+#include "kvq_internal.h"
+
+namespace {
+
+constexpr int kMaxGroup = 16;     // q heads per kv head served by one MFMA column block
+constexpr int kLdsBudget = 64 * 1024;
+
+bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+int ilog2(int64_t x) {
+    int r = 0;
+    while ((int64_t(1) << r) < x) ++r;
+    return r;
+}
+
+int cdiv(int64_t a, int64_t b) { return int((a + b - 1) / b); }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Checks shared by every entry point that reads the caches. `need_out` is false for
+// stage 1, which writes the workspace instead of args->out.
+int check_decode_args(const kvq_decode_args* a, bool need_out) {
+    if (!a) return KVQ_ERR_NULL_POINTER;
+    if (!a->q || !a->k_cache || !a->v_cache || !a->block_table || !a->seq_lens)
+        return KVQ_ERR_NULL_POINTER;
+    if (need_out && !a->out) return KVQ_ERR_NULL_POINTER;
+    if (a->batch < 1 || a->q_heads < 1 || a->kv_heads < 1 || a->max_blocks < 1 ||
+        a->num_blocks < 1)
+        return KVQ_ERR_SHAPE;
+    if (a->batch > 65535 || a->kv_heads > 65535) return KVQ_ERR_UNSUPPORTED;
+    if (a->q_heads % a->kv_heads != 0) return KVQ_ERR_SHAPE;
+    // The reference requires power-of-two head_dim >= 16 and block_size >= 16
+    // (triton_fp16.py:197-198); anything else is a shape error here too.
+    if (!is_pow2(a->head_dim) || a->head_dim < 16) return KVQ_ERR_SHAPE;
+    if (!is_pow2(a->block_size) || a->block_size < 16) return KVQ_ERR_SHAPE;
+    if (a->head_dim < 32 || a->head_dim > 256) return KVQ_ERR_UNSUPPORTED;
+    if (a->q_heads / a->kv_heads > kMaxGroup) return KVQ_ERR_UNSUPPORTED;
+    if (a->block_size > 4096) return KVQ_ERR_UNSUPPORTED;
+    if (!(a->scale == a->scale)) return KVQ_ERR_SHAPE;  // NaN scale
+    if (a->kv_format < KVQ_KV_F16 || a->kv_format > KVQ_KV_INT4) return KVQ_ERR_FORMAT;
+    if (a->kv_format != KVQ_KV_F16) {
+        if (!a->k_scale || !a->k_zero || !a->v_scale || !a->v_zero) return KVQ_ERR_FORMAT;
+        if (a->k_group < a->block_size || a->k_group % a->block_size != 0)
+            return KVQ_ERR_UNSUPPORTED;
+        if (!aligned16(a->k_scale) || !aligned16(a->k_zero) || !aligned16(a->v_scale) ||
+            !aligned16(a->v_zero))
+            return KVQ_ERR_ALIGNMENT;
+    }
+    // Vector loads: 16-byte aligned bases and row strides that keep every row aligned.
+    const int64_t vec = a->kv_format == KVQ_KV_F16 ? 8 : 16;  // elements per 16 bytes
+    if (!aligned16(a->q) || !aligned16(a->k_cache) || !aligned16(a->v_cache))
+        return KVQ_ERR_ALIGNMENT;
+    if (need_out && !aligned16(a->out)) return KVQ_ERR_ALIGNMENT;
+    if (a->q_stride_b % 8 || a->q_stride_h % 8) return KVQ_ERR_ALIGNMENT;
+    if (need_out && (a->o_stride_b % 8 || a->o_stride_h % 8)) return KVQ_ERR_ALIGNMENT;
+    if (a->k_stride_blk % vec || a->k_stride_tok % vec || a->k_stride_head % vec)
+        return KVQ_ERR_ALIGNMENT;
+    if (a->v_stride_blk % vec || a->v_stride_tok % vec || a->v_stride_head % vec)
+        return KVQ_ERR_ALIGNMENT;
+    // Lane offsets inside a 16-token chunk are 32-bit byte offsets.
+    const int64_t lim = int64_t(1) << 30;
+    if (a->k_stride_tok < 0 || a->v_stride_tok < 0 || 16 * a->k_stride_tok + a->head_dim > lim ||
+        16 * a->v_stride_tok + a->head_dim > lim)
+        return KVQ_ERR_UNSUPPORTED;
+    return KVQ_OK;
+}
+
+kvq::DecodeParams make_params(const kvq_decode_args* a) {
+    kvq::DecodeParams p{};
+    p.q = a->q;
+    p.q_sb = a->q_stride_b;
+    p.q_sh = a->q_stride_h;
+    p.k = a->k_cache;
+    p.k_sblk = a->k_stride_blk;
+    p.k_stok = a->k_stride_tok;
+    p.k_sh = a->k_stride_head;
+    p.v = a->v_cache;
+    p.v_sblk = a->v_stride_blk;
+    p.v_stok = a->v_stride_tok;
+    p.v_sh = a->v_stride_head;
+    p.bt = a->block_table;
+    p.bt_sb = a->bt_stride_b;
+    p.seq_lens = a->seq_lens;
+    p.out = a->out;
+    p.o_sb = a->o_stride_b;
+    p.o_sh = a->o_stride_h;
+    p.k_scale = static_cast<const _Float16*>(a->k_scale);
+    p.k_zero = static_cast<const _Float16*>(a->k_zero);
+    p.v_scale = static_cast<const _Float16*>(a->v_scale);
+    p.v_zero = static_cast<const _Float16*>(a->v_zero);
+    p.batch = a->batch;
+    p.q_heads = a->q_heads;
+    p.kv_heads = a->kv_heads;
+    p.group = a->q_heads / a->kv_heads;
+    p.block_size = a->block_size;
+    p.max_blocks = a->max_blocks;
+    p.num_blocks = a->num_blocks;
+    p.cpp_shift = ilog2(a->block_size / 16);
+    p.k_group_chunks = a->kv_format == KVQ_KV_F16 ? 0 : a->k_group / 16;
+    p.k_group_pages = a->kv_format == KVQ_KV_F16 ? 0 : a->k_group / a->block_size;
+    p.scale_log2 = a->scale * 1.4426950408889634f;
+    return p;
+}
+
+int64_t lds_bytes(const kvq_decode_args* a, int waves) {
+    const int group = a->q_heads / a->kv_heads;
+    return int64_t(4) * (int64_t(waves) * group * a->head_dim + 32 * waves);
+}
+
+// Waves per workgroup: the caller's choice if given, else as many as give each wave at
+// least 8 chunks of the split (at most 16), within the LDS budget of the cross-wave
+// combine. Returns 0 when the caller's choice is invalid.
+int pick_waves(const kvq_decode_args* a, int pages_per_split) {
+    if (a->waves_per_group != 0) {
+        const int w = a->waves_per_group;
+        if (w != 1 && w != 2 && w != 4 && w != 8 && w != 16) return 0;
+        return lds_bytes(a, w) <= kLdsBudget ? w : 0;
+    }
+    const int64_t chunks = int64_t(pages_per_split) * (a->block_size / 16);
+    int w = 16;
+    while (w > 1 && chunks < 8 * w) w >>= 1;
+    while (w > 1 && lds_bytes(a, w) > kLdsBudget) w >>= 1;
+    return w;
+}
+
+// Pipeline depth: the caller's choice if given (1 or 2), else 1. Returns 0 when invalid.
+int pick_pipeline(const kvq_decode_args* a) {
+    if (a->pipeline == 0) return 1;
+    return (a->pipeline == 1 || a->pipeline == 2) ? a->pipeline : 0;
+}
+
+int hip_status(hipError_t e) { return e == hipSuccess ? KVQ_OK : KVQ_ERR_HIP; }
+
+}  // namespace
+
+extern "C" {
+
+const char* kvq_version(void) { return "kvq 0.1.0 gfx950"; }
+
+const char* kvq_status_string(int status) {
+    switch (status) {
+        case KVQ_OK: return "ok";
+        case KVQ_ERR_NULL_POINTER: return "null pointer";
+        case KVQ_ERR_SHAPE: return "inconsistent shape";
+        case KVQ_ERR_UNSUPPORTED: return "unsupported configuration";
+        case KVQ_ERR_ALIGNMENT: return "misaligned pointer or stride";
+        case KVQ_ERR_SPLITS: return "invalid split configuration";
+        case KVQ_ERR_FORMAT: return "invalid kv format or missing scales";
+        case KVQ_ERR_HIP: return "HIP launch error";
+        default: return "unknown status";
+    }
+}
+
+int kvq_choose_num_splits(int32_t batch, int32_t kv_heads, int32_t block_size,
+                          int32_t max_pages, int32_t cu_count, int32_t target_per_cu,
+                          int32_t min_tokens_per_split) {
+    if (batch < 1 || kv_heads < 1 || block_size < 1 || max_pages < 0 || cu_count < 1 ||
+        target_per_cu < 1 || min_tokens_per_split < 0)
+        return KVQ_ERR_SHAPE;
+    const int64_t want = cdiv(int64_t(target_per_cu) * cu_count, int64_t(batch) * kv_heads);
+    int64_t p2 = 1;
+    while (p2 < want) p2 <<= 1;
+    const int64_t per = min_tokens_per_split / block_size;
+    int64_t cap = max_pages / (per > 1 ? per : 1);
+    if (cap < 1) cap = 1;
+    const int64_t s = p2 < cap ? p2 : cap;
+    return int(s < 1 ? 1 : s);
+}
+
+int kvq_normalize_splits(int32_t num_splits, int32_t max_pages, int32_t* splits_out,
+                         int32_t* pages_per_split_out) {
+    if (!splits_out || !pages_per_split_out) return KVQ_ERR_NULL_POINTER;
+    if (max_pages < 1) return KVQ_ERR_SHAPE;
+    int s = num_splits < 1 ? 1 : (num_splits > max_pages ? max_pages : num_splits);
+    int pps = max_pages;
+    if (s > 1) {
+        pps = cdiv(max_pages, s);
+        s = cdiv(max_pages, pps);
+    }
+    *splits_out = s;
+    *pages_per_split_out = pps;
+    return KVQ_OK;
+}
+
+int kvq_decode_split(const kvq_decode_args* args, int32_t num_splits, int32_t pages_per_split,
+                     float* o_part, float* lse, kvq_stream_t stream) {
+    int st = check_decode_args(args, false);
+    if (st != KVQ_OK) return st;
+    if (!o_part || !lse) return KVQ_ERR_NULL_POINTER;
+    if (num_splits < 1 || pages_per_split < 1 || num_splits > 65535) return KVQ_ERR_SPLITS;
+    if (int64_t(num_splits) * pages_per_split < args->max_blocks) return KVQ_ERR_SPLITS;
+    const int waves = pick_waves(args, pages_per_split);
+    const int pipe = pick_pipeline(args);
+    if (waves == 0 || pipe == 0) return KVQ_ERR_UNSUPPORTED;
+    kvq::DecodeParams p = make_params(args);
+    p.o_part = o_part;
+    p.lse = lse;
+    p.num_splits = num_splits;
+    p.pages_per_split = pages_per_split;
+    return hip_status(kvq::launch_decode(p, args->kv_format, args->head_dim, false, waves, pipe,
+                                         reinterpret_cast<hipStream_t>(stream)));
+}
+
+int kvq_decode_merge(const float* o_part, const float* lse, void* out, int64_t o_stride_b,
+                     int64_t o_stride_h, int32_t batch, int32_t q_heads, int32_t head_dim,
+                     int32_t num_splits, kvq_stream_t stream) {
+    if (!o_part || !lse || !out) return KVQ_ERR_NULL_POINTER;
+    if (batch < 1 || q_heads < 1 || num_splits < 1) return KVQ_ERR_SHAPE;
+    if (batch > 65535) return KVQ_ERR_UNSUPPORTED;
+    if (!is_pow2(head_dim) || head_dim < 16) return KVQ_ERR_SHAPE;
+    if (head_dim < 32 || head_dim > 256) return KVQ_ERR_UNSUPPORTED;
+    return hip_status(kvq::launch_merge(o_part, lse, out, o_stride_b, o_stride_h, batch, q_heads,
+                                        head_dim, num_splits,
+                                        reinterpret_cast<hipStream_t>(stream)));
+}
+
+int kvq_decode_single(const kvq_decode_args* args, kvq_stream_t stream) {
+    int st = check_decode_args(args, true);
+    if (st != KVQ_OK) return st;
+    const int waves = pick_waves(args, args->max_blocks);
+    const int pipe = pick_pipeline(args);
+    if (waves == 0 || pipe == 0) return KVQ_ERR_UNSUPPORTED;
+    kvq::DecodeParams p = make_params(args);
+    p.num_splits = 1;
+    p.pages_per_split = args->max_blocks;
+    return hip_status(kvq::launch_decode(p, args->kv_format, args->head_dim, true, waves, pipe,
+                                         reinterpret_cast<hipStream_t>(stream)));
+}
+
+int kvq_paged_decode(const kvq_decode_args* args, int32_t num_splits, float* o_part, float* lse,
+                     kvq_stream_t stream) {
+    int st = check_decode_args(args, true);
+    if (st != KVQ_OK) return st;
+    int32_t s = 1, pps = 1;
+    st = kvq_normalize_splits(num_splits, args->max_blocks, &s, &pps);
+    if (st != KVQ_OK) return st;
+    if (s == 1) return kvq_decode_single(args, stream);
+    st = kvq_decode_split(args, s, pps, o_part, lse, stream);
+    if (st != KVQ_OK) return st;
+    return kvq_decode_merge(o_part, lse, args->out, args->o_stride_b, args->o_stride_h,
+                            args->batch, args->q_heads, args->head_dim, s, stream);
+}
+
+int kvq_quantize_cache(const kvq_decode_args* args, const void* k_src, const void* v_src,
+                       int64_t src_stride_blk, int64_t src_stride_tok, int64_t src_stride_head,
+                       kvq_stream_t stream) {
+    (void)args; (void)k_src; (void)v_src; (void)src_stride_blk; (void)src_stride_tok;
+    (void)src_stride_head; (void)stream;
+    return KVQ_ERR_UNSUPPORTED;
+}
+
+int kvq_quantize_append(const kvq_decode_args* args, const void* k_new, const void* v_new,
+                        void* k_resid, kvq_stream_t stream) {
+    (void)args; (void)k_new; (void)v_new; (void)k_resid; (void)stream;
+    return KVQ_ERR_UNSUPPORTED;
+}
+
+}  // extern "C"

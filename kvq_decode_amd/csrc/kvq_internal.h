@@ -1,0 +1,75 @@
+// Internal interface between the C ABI (capi.cpp) and the HIP kernels (decode.hip,
+// quant.hip). Not installed; the public boundary is include/kvq.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kvq.h"
+
+namespace kvq {
+
+// Kernel-side view of one decode call. Built on the host from kvq_decode_args after
+// validation; passed by value as the kernel argument.
+struct DecodeParams {
+    const void* q;
+    int64_t q_sb, q_sh;
+    const void* k;
+    int64_t k_sblk, k_stok, k_sh;
+    const void* v;
+    int64_t v_sblk, v_stok, v_sh;
+    const int32_t* bt;
+    int64_t bt_sb;
+    const int32_t* seq_lens;
+    void* out;  // fp16 output (single pass)
+    int64_t o_sb, o_sh;
+    float* o_part;  // split-KV workspace (stage 1)
+    float* lse;
+    const _Float16* k_scale;
+    const _Float16* k_zero;
+    const _Float16* v_scale;
+    const _Float16* v_zero;
+    int32_t batch, q_heads, kv_heads, group, block_size, max_blocks, num_blocks;
+    int32_t cpp_shift;       // log2(block_size / 16): 16-token chunks per page
+    int32_t k_group_chunks;  // 16-token chunks per K scale group (quantized formats)
+    int32_t k_group_pages;   // pages per K scale group
+    int32_t num_splits, pages_per_split;
+    float scale_log2;        // softmax scale * log2(e)
+};
+
+// Launches the decode kernel for the format/head_dim in `fmt`/`head_dim`. `final_out`
+// selects the single-pass variant (writes p.out) over stage 1 (writes p.o_part/p.lse).
+hipError_t launch_decode(const DecodeParams& p, int kv_format, int head_dim, bool final_out,
+                         int waves_per_group, int pipeline, hipStream_t stream);
+
+hipError_t launch_merge(const float* o_part, const float* lse, void* out, int64_t o_sb,
+                        int64_t o_sh, int batch, int q_heads, int head_dim, int num_splits,
+                        hipStream_t stream);
+
+// Bulk quantization of fp16 paged caches into codes + scales (quant.hip).
+struct QuantParams {
+    const _Float16* k_src;
+    const _Float16* v_src;
+    int64_t s_sblk, s_stok, s_sh;
+    uint8_t* k_codes;
+    uint8_t* v_codes;
+    int64_t k_sblk, k_stok, k_sh;
+    int64_t v_sblk, v_stok, v_sh;
+    _Float16* k_scale;
+    _Float16* k_zero;
+    _Float16* v_scale;
+    _Float16* v_zero;
+    const int32_t* bt;
+    int64_t bt_sb;
+    const int32_t* seq_lens;
+    const _Float16* k_new;   // append only: [batch, kv_heads, head_dim]
+    const _Float16* v_new;
+    _Float16* k_resid;       // append only: [batch, kv_heads, k_group, head_dim]
+    int32_t batch, kv_heads, head_dim, block_size, max_blocks, num_blocks, k_group;
+    int32_t max_groups;      // cdiv(max_blocks * block_size, k_group)
+};
+
+hipError_t launch_quantize_cache(const QuantParams& p, int kv_format, hipStream_t stream);
+hipError_t launch_quantize_append(const QuantParams& p, int kv_format, hipStream_t stream);
+
+}  // namespace kvq

@@ -1,0 +1,164 @@
+"""HIP decode path (libkvq.so) vs the numpy oracle on identical inputs. Needs a GPU.
+
+Mirrors the reference's kernel tests (tests/test_triton_fp16.py:23-62): the 120-case grid,
+determinism, and split-vs-single-pass agreement, plus stage-1 parity, NaN garbage in
+unused slots and the BASELINE configurations at full size.
+
+Tolerance (north star: max-abs 2e-3 / max-rel 1e-2 for fp16 KV): every element must
+satisfy |out - ref| <= 2e-3 + 1e-2 * |ref|, with ref the oracle's float32 output (before
+its cast to fp16), and max |out - ref| < 2e-3 as the reference asserts
+(test_triton_fp16.py:42).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.attention import (build_paged_cache, normalize_splits, paged_decode_attention_ref,
+                              split_decode_ref)
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(32, 8, 128), (4, 4, 64), (8, 1, 64)]  # Llama-3-8B, MHA, MQA
+ATOL, RTOL = 2e-3, 1e-2
+
+
+def make(Hq, Hkv, D, block_size, lens, seed=0):
+    rng = np.random.default_rng(seed)
+    B, S = len(lens), max(lens)
+    q = rng.standard_normal((B, Hq, D)).astype(np.float16)
+    k = rng.standard_normal((B, S, Hkv, D)).astype(np.float16)
+    v = rng.standard_normal((B, S, Hkv, D)).astype(np.float16)
+    sl = np.array(lens, np.int32)
+    kc, vc, bt = build_paged_cache(k, v, sl, block_size, rng)
+    return q, kc, vc, bt, sl
+
+
+def to_gpu(*arrs):
+    return [torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in arrs]
+
+
+def check_close(out, ref, tag=""):
+    out = out.float().cpu().numpy()
+    diff = np.abs(out - ref)
+    max_abs = float(diff.max())
+    max_rel = float((diff / np.maximum(np.abs(ref), 1e-3)).max())
+    print(f"\n[{tag}] max_abs={max_abs:.3e} max_rel(clamp 1e-3)={max_rel:.3e}", flush=True)
+    assert np.isfinite(out).all()
+    assert max_abs < ATOL
+    assert np.all(diff <= ATOL + RTOL * np.abs(ref))
+
+
+# 1 = single pass; 2, 3, 7 = split-KV (7 exceeds the page count of short sequences, so some
+# splits are empty); None = heuristic (test_triton_fp16.py:21-24)
+@pytest.mark.parametrize("num_splits", [1, 2, 3, 7, None])
+@pytest.mark.parametrize("Hq,Hkv,D", SHAPES)
+@pytest.mark.parametrize("block_size", [16, 32])
+@pytest.mark.parametrize("lens", [[1], [37], [100, 33, 1, 64], [4096, 1000, 17, 2049]])
+def test_matches_reference(Hq, Hkv, D, block_size, lens, num_splits):
+    from kvq_decode_amd import paged_decode_attention
+    q, kc, vc, bt, sl = make(Hq, Hkv, D, block_size, lens)
+    ref = paged_decode_attention_ref(q, kc, vc, bt, sl, out_dtype=np.float32)
+    out = paged_decode_attention(*to_gpu(q, kc, vc, bt, sl), num_splits=num_splits)
+    torch.cuda.synchronize()
+    check_close(out, ref, f"Hq={Hq} Hkv={Hkv} D={D} bs={block_size} splits={num_splits} lens={lens}")
+
+
+def test_split_kv_is_deterministic():
+    from kvq_decode_amd import paged_decode_attention
+    args = to_gpu(*make(32, 8, 128, 16, [4096, 1000, 17, 2049]))
+    a = paged_decode_attention(*args, num_splits=8)
+    b = paged_decode_attention(*args, num_splits=8)
+    assert torch.equal(a, b)
+
+
+def test_splits_agree_with_single_pass():
+    from kvq_decode_amd import paged_decode_attention
+    args = to_gpu(*make(32, 8, 128, 32, [4096, 1000, 17, 2049]))
+    base = paged_decode_attention(*args, num_splits=1)
+    for n in (2, 5, 16):
+        out = paged_decode_attention(*args, num_splits=n)
+        assert (out.float() - base.float()).abs().max().item() < 2e-3
+
+
+@pytest.mark.parametrize("num_splits", [2, 7, 33])
+def test_stage1_partials_match_oracle(num_splits):
+    """o_part / lse of stage 1 vs the oracle's split semantics (triton_fp16.py:114-144),
+    including the empty-split convention o = 0, lse = -inf."""
+    from kvq_decode_amd.ops import paged_decode_split
+    q, kc, vc, bt, sl = make(32, 8, 128, 16, [700, 5, 130])
+    S, pps = normalize_splits(num_splits, bt.shape[1])
+    scale = 1 / math.sqrt(128)
+    o_ref, l_ref = split_decode_ref(q, kc, vc, bt, sl, scale, S, pps)
+    o, l = paged_decode_split(*to_gpu(q, kc, vc, bt, sl), scale, S, pps)
+    torch.cuda.synchronize()
+    o, l = o.cpu().numpy(), l.cpu().numpy()
+    assert np.array_equal(np.isneginf(l), np.isneginf(l_ref))
+    fin = np.isfinite(l_ref)
+    np.testing.assert_allclose(l[fin], l_ref[fin], atol=2e-3)
+    np.testing.assert_allclose(o, o_ref, atol=2e-3, rtol=1e-2)
+    assert np.all(o[np.isneginf(l_ref)] == 0)
+
+
+@pytest.mark.parametrize("num_splits", [1, 4])
+def test_nan_garbage_in_unused_slots(num_splits):
+    """Unused slots of each sequence's last page hold NaN/inf: the kernel never reads them
+    (rows past seq_len are redirected to the last valid token and masked)."""
+    from kvq_decode_amd import paged_decode_attention
+    lens = [37, 1, 250]
+    q, kc, vc, bt, sl = make(32, 8, 128, 16, lens)
+    for b, n in enumerate(lens):
+        if n % 16:
+            blk = bt[b, (n - 1) // 16]
+            kc[blk, n % 16:] = np.nan
+            vc[blk, n % 16:] = np.inf
+    ref = paged_decode_attention_ref(q, np.nan_to_num(kc), np.nan_to_num(vc), bt, sl,
+                                     out_dtype=np.float32)
+    out = paged_decode_attention(*to_gpu(q, kc, vc, bt, sl), num_splits=num_splits)
+    check_close(out, ref, f"nan-garbage splits={num_splits}")
+
+
+@pytest.mark.parametrize("waves,pipeline", [(1, 1), (2, 2), (4, 1), (8, 2), (16, 1), (16, 2)])
+def test_workgroup_shapes_agree(waves, pipeline):
+    """Every (waves per workgroup, pipeline depth) kernel variant gives the same result."""
+    from kvq_decode_amd import paged_decode_attention
+    q, kc, vc, bt, sl = make(32, 8, 128, 16, [3000, 77, 1])
+    ref = paged_decode_attention_ref(q, kc, vc, bt, sl, out_dtype=np.float32)
+    args = to_gpu(q, kc, vc, bt, sl)
+    for splits in (1, 6):
+        out = paged_decode_attention(*args, num_splits=splits, waves_per_group=waves,
+                                     pipeline=pipeline)
+        check_close(out, ref, f"waves={waves} pipe={pipeline} splits={splits}")
+
+
+def _baseline_case(B, ctx, pool, seed=0):
+    """q, K, V ~ N(0,1) fp16, block_table a random permutation of the
+    pool, block_size 16, every sequence ctx tokens (generated on the GPU, copied back
+    for the oracle)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    Hq, Hkv, D, bs = 32, 8, 128, 16
+    q = torch.randn(B, Hq, D, generator=g, device="cuda").half()
+    kc = torch.randn(pool, bs, Hkv, D, generator=g, device="cuda").half()
+    vc = torch.randn(pool, bs, Hkv, D, generator=g, device="cuda").half()
+    nb = ctx // bs
+    bt = torch.randperm(pool, generator=g, device="cuda")[: B * nb].view(B, nb).int()
+    sl = torch.full((B,), ctx, dtype=torch.int32, device="cuda")
+    return q, kc, vc, bt, sl
+
+
+@pytest.mark.parametrize("B,ctx,pool,splits", [
+    (1, 4096, 256, 1),        # C1: no split
+    (8, 32768, 16384, None),  # C2: auto split (32 on 256 CUs)
+    (8, 32768, 16384, 8),
+    (1, 131072, 8192, None),  # C3: auto split
+    (1, 131072, 8192, 16),
+])
+def test_baseline_configs_match_oracle(B, ctx, pool, splits):
+    from kvq_decode_amd import paged_decode_attention
+    q, kc, vc, bt, sl = _baseline_case(B, ctx, pool)
+    out = paged_decode_attention(q, kc, vc, bt, sl, num_splits=splits)
+    torch.cuda.synchronize()
+    ref = paged_decode_attention_ref(q.cpu().numpy(), kc.cpu().numpy(), vc.cpu().numpy(),
+                                     bt.cpu().numpy(), sl.cpu().numpy(), out_dtype=np.float32)
+    check_close(out, ref, f"B={B} ctx={ctx} splits={splits}")
