@@ -47,6 +47,7 @@ int check_decode_args(const kvq_decode_args* a, bool need_out) {
     if (a->kv_format < KVQ_KV_F16 || a->kv_format > KVQ_KV_INT4) return KVQ_ERR_FORMAT;
     if (a->kv_format != KVQ_KV_F16) {
         if (!a->k_scale || !a->k_zero || !a->v_scale || !a->v_zero) return KVQ_ERR_FORMAT;
+        if (a->head_dim != 128) return KVQ_ERR_UNSUPPORTED;
         if (a->k_group < a->block_size || a->k_group % a->block_size != 0)
             return KVQ_ERR_UNSUPPORTED;
         if (!aligned16(a->k_scale) || !aligned16(a->k_zero) || !aligned16(a->v_scale) ||
@@ -137,6 +138,56 @@ int pick_pipeline(const kvq_decode_args* a) {
 }
 
 int hip_status(hipError_t e) { return e == hipSuccess ? KVQ_OK : KVQ_ERR_HIP; }
+
+// Checks for the quantize entry points: args->k_cache / v_cache (codes) and the scale /
+// zero tensors are the destinations; kv_format must be a quantized format.
+int check_quant_args(const kvq_decode_args* a) {
+    if (!a) return KVQ_ERR_NULL_POINTER;
+    if (!a->k_cache || !a->v_cache || !a->block_table || !a->seq_lens) return KVQ_ERR_NULL_POINTER;
+    if (a->kv_format < KVQ_KV_INT8 || a->kv_format > KVQ_KV_INT4) return KVQ_ERR_FORMAT;
+    if (!a->k_scale || !a->k_zero || !a->v_scale || !a->v_zero) return KVQ_ERR_FORMAT;
+    if (a->batch < 1 || a->kv_heads < 1 || a->max_blocks < 1 || a->num_blocks < 1)
+        return KVQ_ERR_SHAPE;
+    if (!is_pow2(a->block_size) || a->block_size < 16) return KVQ_ERR_SHAPE;
+    if (!is_pow2(a->head_dim) || a->head_dim < 16) return KVQ_ERR_SHAPE;
+    if (a->head_dim < 32 || a->head_dim > 256) return KVQ_ERR_UNSUPPORTED;
+    if (a->k_group < a->block_size || a->k_group % a->block_size != 0) return KVQ_ERR_UNSUPPORTED;
+    if (a->batch > 65535 || a->kv_heads > 65535) return KVQ_ERR_UNSUPPORTED;
+    const int64_t tokens = int64_t(a->max_blocks) * a->block_size;
+    if (tokens / 16 > 65535 || cdiv(tokens, a->k_group) > 65535) return KVQ_ERR_UNSUPPORTED;
+    if (a->k_stride_blk % 16 || a->k_stride_tok % 16 || a->k_stride_head % 16 ||
+        a->v_stride_blk % 16 || a->v_stride_tok % 16 || a->v_stride_head % 16)
+        return KVQ_ERR_ALIGNMENT;
+    return KVQ_OK;
+}
+
+kvq::QuantParams make_quant_params(const kvq_decode_args* a) {
+    kvq::QuantParams p{};
+    p.k_codes = static_cast<uint8_t*>(const_cast<void*>(a->k_cache));
+    p.v_codes = static_cast<uint8_t*>(const_cast<void*>(a->v_cache));
+    p.k_sblk = a->k_stride_blk;
+    p.k_stok = a->k_stride_tok;
+    p.k_sh = a->k_stride_head;
+    p.v_sblk = a->v_stride_blk;
+    p.v_stok = a->v_stride_tok;
+    p.v_sh = a->v_stride_head;
+    p.k_scale = static_cast<_Float16*>(const_cast<void*>(a->k_scale));
+    p.k_zero = static_cast<_Float16*>(const_cast<void*>(a->k_zero));
+    p.v_scale = static_cast<_Float16*>(const_cast<void*>(a->v_scale));
+    p.v_zero = static_cast<_Float16*>(const_cast<void*>(a->v_zero));
+    p.bt = a->block_table;
+    p.bt_sb = a->bt_stride_b;
+    p.seq_lens = a->seq_lens;
+    p.batch = a->batch;
+    p.kv_heads = a->kv_heads;
+    p.head_dim = a->head_dim;
+    p.block_size = a->block_size;
+    p.max_blocks = a->max_blocks;
+    p.num_blocks = a->num_blocks;
+    p.k_group = a->k_group;
+    p.max_groups = cdiv(int64_t(a->max_blocks) * a->block_size, a->k_group);
+    return p;
+}
 
 }  // namespace
 
@@ -251,15 +302,31 @@ int kvq_paged_decode(const kvq_decode_args* args, int32_t num_splits, float* o_p
 int kvq_quantize_cache(const kvq_decode_args* args, const void* k_src, const void* v_src,
                        int64_t src_stride_blk, int64_t src_stride_tok, int64_t src_stride_head,
                        kvq_stream_t stream) {
-    (void)args; (void)k_src; (void)v_src; (void)src_stride_blk; (void)src_stride_tok;
-    (void)src_stride_head; (void)stream;
-    return KVQ_ERR_UNSUPPORTED;
+    int st = check_quant_args(args);
+    if (st != KVQ_OK) return st;
+    if (!k_src || !v_src) return KVQ_ERR_NULL_POINTER;
+    if (src_stride_blk < 0 || src_stride_tok < 0 || src_stride_head < 0) return KVQ_ERR_SHAPE;
+    kvq::QuantParams p = make_quant_params(args);
+    p.k_src = static_cast<const _Float16*>(k_src);
+    p.v_src = static_cast<const _Float16*>(v_src);
+    p.s_sblk = src_stride_blk;
+    p.s_stok = src_stride_tok;
+    p.s_sh = src_stride_head;
+    return hip_status(kvq::launch_quantize_cache(p, args->kv_format,
+                                                 reinterpret_cast<hipStream_t>(stream)));
 }
 
 int kvq_quantize_append(const kvq_decode_args* args, const void* k_new, const void* v_new,
                         void* k_resid, kvq_stream_t stream) {
-    (void)args; (void)k_new; (void)v_new; (void)k_resid; (void)stream;
-    return KVQ_ERR_UNSUPPORTED;
+    int st = check_quant_args(args);
+    if (st != KVQ_OK) return st;
+    if (!k_new || !v_new || !k_resid) return KVQ_ERR_NULL_POINTER;
+    kvq::QuantParams p = make_quant_params(args);
+    p.k_new = static_cast<const _Float16*>(k_new);
+    p.v_new = static_cast<const _Float16*>(v_new);
+    p.k_resid = static_cast<_Float16*>(k_resid);
+    return hip_status(kvq::launch_quantize_append(p, args->kv_format,
+                                                  reinterpret_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

@@ -30,74 +30,9 @@
 #include <math.h>
 #include <stdint.h>
 
-#include "kvq_internal.h"
+#include "decode_common.h"
 
 namespace kvq {
-
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-
-template <int N>
-struct HalfVec {
-    typedef _Float16 type __attribute__((ext_vector_type(N)));
-};
-
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLn2 = 0.6931471805599453f;
-
-__device__ __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }
-
-// Reductions across the four 16-lane rows of a wave64 without LDS: gfx950's
-// v_permlane{16,32}_swap exchange rows between two registers; combining both halves of
-// the swap gives every lane the reduction over the row pair.
-__device__ __forceinline__ float rows_max(float v) {
-    const unsigned u = __float_as_uint(v);
-    auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-    const unsigned w = __float_as_uint(v);
-    auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-
-__device__ __forceinline__ float rows_sum(float v) {
-    const unsigned u = __float_as_uint(v);
-    auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-    const unsigned w = __float_as_uint(v);
-    auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
-    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// Lazy running max: the exponent reference m of a head column moves only when a score
-// exceeds it by more than kLazyMax (log2 units), so p = 2^(s - m) <= 2^kLazyMax (256,
-// exact in fp16 up to its usual rounding). Numerator and denominator share m, so the
-// result is unchanged; the common chunk needs no cross-lane max and no rescale.
-constexpr float kLazyMax = 8.0f;
-
-// Block-table entries for 64 consecutive pages, one per lane; a wave reads its page's
-// physical block with v_readlane (no scalar-load round trip per chunk).
-struct PageWindow {
-    int base;  // first page held
-    int reg;   // lane i holds block_table[b][base + i] (0 past the sequence)
-};
-
-__device__ __forceinline__ void window_load(const DecodeParams& p, int b, int base, int n_pages,
-                                            PageWindow& w) {
-    const int lane = __lane_id();
-    w.base = base;
-    const int page = base + lane;
-    w.reg = page < n_pages ? p.bt[(int64_t)b * p.bt_sb + page] : 0;
-}
-
-__device__ __forceinline__ int window_phys(const DecodeParams& p, int b, int page, int n_pages,
-                                           PageWindow& w) {
-    if (page - w.base >= 64) window_load(p, b, page, n_pages, w);
-    int phys = __builtin_amdgcn_readlane(w.reg, page - w.base);
-    return min(max(phys, 0), p.num_blocks - 1);
-}
 
 // One 16-token chunk of one kv head, fp16 cache, as held by one lane.
 template <int D>
@@ -136,14 +71,6 @@ __device__ __forceinline__ void load_chunk_f16(const DecodeParams& p, int b, int
         ch.v[r] = *(const vrow*)(vb + voff);
     }
 }
-
-// Online-softmax state of one wave: running reference max m and partial sum l of its
-// lane (head l%16, tokens 4g..4g+3 of every chunk), and O^T accumulator tiles.
-template <int D>
-struct SoftmaxState {
-    f4 acc[D / 16];
-    float m, l;
-};
 
 // One chunk: QK^T, softmax update, PV. MASK handles the sequence's partial last chunk.
 template <int D, bool MASK>
@@ -210,19 +137,9 @@ void decode_f16_kernel(const DecodeParams p) {
     const int i16 = lane & 15, g = lane >> 4;
     const int G = p.group;
     const bool head_ok = i16 < G;
-
-    int seq_len = p.seq_lens[b];
-    seq_len = min(max(seq_len, 0), p.max_blocks * p.block_size);
-    const int n_pages = cdiv(seq_len, p.block_size);
-    const int pg_lo = split * p.pages_per_split;
-    const int pg_hi = min(pg_lo + p.pages_per_split, n_pages);
-    const int c_lo = pg_lo << p.cpp_shift;
-    const int c_hi = min(pg_hi << p.cpp_shift, cdiv(seq_len, 16));
-    const int nch = max(c_hi - c_lo, 0);
-    const int per = cdiv(nch, W);
-    const int w_lo = c_lo + wave * per;
-    const int w_hi = min(w_lo + per, c_hi);
-    const int c_full = seq_len >> 4;  // chunks below this index are fully valid
+    const WaveRange wr = wave_range<W>(p, b, split, wave);
+    const int seq_len = wr.seq_len, n_pages = wr.n_pages, w_lo = wr.w_lo, w_hi = wr.w_hi;
+    const int c_full = wr.c_full;
 
     // Q^T operand: lane (head i16, g) holds Q[head][32*k + 8*g + 0..7]; padded heads = 0.
     h8 qop[NST];
@@ -273,54 +190,8 @@ void decode_f16_kernel(const DecodeParams p) {
         }
     }
 
-    // Column sum of l over the four token rows (the lanes of a column share m).
-    const float l = rows_sum(st.l);
-    const float m = st.m;
-
-    // Combine the W waves through LDS: [W][G][D] accumulators, [W][16] m and l.
-    extern __shared__ float smem[];
-    float* sm_acc = smem;
-    float* sm_m = smem + W * G * D;
-    float* sm_l = sm_m + W * 16;
-    if (head_ok) {
-        float* dst = sm_acc + (wave * G + i16) * D;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-#pragma unroll
-            for (int t = 0; t < DV; ++t) dst[DV * (4 * g + r) + t] = st.acc[t][r];
-        }
-        if (g == 0) {
-            sm_m[wave * 16 + i16] = m;
-            sm_l[wave * 16 + i16] = l;
-        }
-    }
-    __syncthreads();
-
-    const int hq0 = kvh * G;
-    for (int idx = threadIdx.x; idx < G * D; idx += W * 64) {
-        const int hh = idx / D, d = idx - hh * D;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < W; ++w) M = fmaxf(M, sm_m[w * 16 + hh]);
-        float L = 0.f, O = 0.f;
-        if (M > -INFINITY) {
-#pragma unroll
-            for (int w = 0; w < W; ++w) {
-                const float e = fast_exp2(sm_m[w * 16 + hh] - M);
-                L += e * sm_l[w * 16 + hh];
-                O += e * sm_acc[(w * G + hh) * D + d];
-            }
-        }
-        const float o = L > 0.f ? O / L : 0.f;
-        if (FINAL) {
-            _Float16* out = (_Float16*)p.out + (int64_t)b * p.o_sb + (int64_t)(hq0 + hh) * p.o_sh;
-            out[d] = (_Float16)o;
-        } else {
-            const int64_t row = ((int64_t)b * p.q_heads + hq0 + hh) * p.num_splits + split;
-            p.o_part[row * D + d] = o;
-            if (d == 0) p.lse[row] = L > 0.f ? (M + __builtin_amdgcn_logf(L)) * kLn2 : -INFINITY;
-        }
-    }
+    combine_store<D, W, FINAL>(p, st.acc, 1.f, 0.f, st.m, rows_sum(st.l), wave, i16, g, kvh,
+                               split, b);
 }
 
 // Stage 2: one workgroup of 4 waves per (q head, sequence). Wave w folds splits
@@ -422,7 +293,8 @@ static hipError_t launch_f16_d(const DecodeParams& p, bool final_out, int waves,
 
 hipError_t launch_decode(const DecodeParams& p, int kv_format, int head_dim, bool final_out,
                          int waves, int pipe, hipStream_t stream) {
-    if (kv_format != KVQ_KV_F16) return hipErrorInvalidValue;
+    if (kv_format != KVQ_KV_F16)
+        return launch_decode_q(p, kv_format, head_dim, final_out, waves, stream);
     switch (head_dim) {
         case 32: return launch_f16_d<32>(p, final_out, waves, pipe, stream);
         case 64: return launch_f16_d<64>(p, final_out, waves, pipe, stream);

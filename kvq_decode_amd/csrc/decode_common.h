@@ -1,0 +1,171 @@
+// Device helpers shared by the fp16 and the quantized decode kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "kvq_internal.h"
+
+namespace kvq {
+
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+template <int N>
+struct HalfVec {
+    typedef _Float16 type __attribute__((ext_vector_type(N)));
+};
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+// Reductions across the four 16-lane rows of a wave64 without LDS: gfx950's
+// v_permlane{16,32}_swap exchange rows between two registers; combining both halves of
+// the swap gives every lane the reduction over the row pair.
+__device__ __forceinline__ float rows_max(float v) {
+    const unsigned u = __float_as_uint(v);
+    auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const unsigned w = __float_as_uint(v);
+    auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float rows_sum(float v) {
+    const unsigned u = __float_as_uint(v);
+    auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const unsigned w = __float_as_uint(v);
+    auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Lazy running max: the exponent reference m of a head column moves only when a score
+// exceeds it by more than kLazyMax (log2 units), so p = 2^(s - m) <= 2^kLazyMax (256,
+// exact in fp16 up to its usual rounding). Numerator and denominator share m, so the
+// result is unchanged; the common chunk needs no cross-lane max and no rescale.
+constexpr float kLazyMax = 8.0f;
+
+// Block-table entries for 64 consecutive pages, one per lane; a wave reads its page's
+// physical block with v_readlane (no scalar-load round trip per chunk).
+struct PageWindow {
+    int base;  // first page held
+    int reg;   // lane i holds block_table[b][base + i] (0 past the sequence)
+};
+
+__device__ __forceinline__ void window_load(const DecodeParams& p, int b, int base, int n_pages,
+                                            PageWindow& w) {
+    const int lane = __lane_id();
+    w.base = base;
+    const int page = base + lane;
+    w.reg = page < n_pages ? p.bt[(int64_t)b * p.bt_sb + page] : 0;
+}
+
+__device__ __forceinline__ int window_phys(const DecodeParams& p, int b, int page, int n_pages,
+                                           PageWindow& w) {
+    if (page - w.base >= 64) window_load(p, b, page, n_pages, w);
+    int phys = __builtin_amdgcn_readlane(w.reg, page - w.base);
+    return min(max(phys, 0), p.num_blocks - 1);
+}
+
+// Online-softmax state of one wave: running reference max m and partial sum l of its
+// lane (head l%16, tokens 4g..4g+3 of every chunk), and O^T accumulator tiles.
+template <int D>
+struct SoftmaxState {
+    f4 acc[D / 16];
+    float m, l;
+};
+
+// Combines the W waves of a workgroup through LDS and writes the split's result.
+// Each wave passes its O^T tiles (lane = head l%16, rows 4g..4g+3 of every tile), which
+// hold acc_scale * acc + corr after the per-format correction, its column's reference max
+// m and its column sum l. LDS: [W][G][D] accumulators then [W][16] m and l.
+// FINAL writes o / l in fp16 to p.out (single pass); otherwise the normalized partial to
+// o_part and its natural-log LSE to lse (stage 1, reference triton_fp16.py:138-143),
+// with o = 0, lse = -inf for an empty split.
+template <int D, int W, bool FINAL>
+__device__ __forceinline__ void combine_store(const DecodeParams& p, const f4* acc,
+                                              float acc_scale, float corr, float m, float l,
+                                              int wave, int i16, int g, int kvh, int split,
+                                              int b) {
+    constexpr int DV = D / 16;
+    const int G = p.group;
+    extern __shared__ float smem[];
+    float* sm_acc = smem;
+    float* sm_m = smem + W * G * D;
+    float* sm_l = sm_m + W * 16;
+    if (i16 < G) {
+        float* dst = sm_acc + (wave * G + i16) * D;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+            for (int t = 0; t < DV; ++t) dst[DV * (4 * g + r) + t] = acc_scale * acc[t][r] + corr;
+        }
+        if (g == 0) {
+            sm_m[wave * 16 + i16] = m;
+            sm_l[wave * 16 + i16] = l;
+        }
+    }
+    __syncthreads();
+
+    const int hq0 = kvh * G;
+    for (int idx = threadIdx.x; idx < G * D; idx += W * 64) {
+        const int hh = idx / D, d = idx - hh * D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < W; ++w) M = fmaxf(M, sm_m[w * 16 + hh]);
+        float L = 0.f, O = 0.f;
+        if (M > -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+                const float e = fast_exp2(sm_m[w * 16 + hh] - M);
+                L += e * sm_l[w * 16 + hh];
+                O += e * sm_acc[(w * G + hh) * D + d];
+            }
+        }
+        const float o = L > 0.f ? O / L : 0.f;
+        if (FINAL) {
+            _Float16* out = (_Float16*)p.out + (int64_t)b * p.o_sb + (int64_t)(hq0 + hh) * p.o_sh;
+            out[d] = (_Float16)o;
+        } else {
+            const int64_t row = ((int64_t)b * p.q_heads + hq0 + hh) * p.num_splits + split;
+            p.o_part[row * D + d] = o;
+            if (d == 0) p.lse[row] = L > 0.f ? (M + __builtin_amdgcn_logf(L)) * kLn2 : -INFINITY;
+        }
+    }
+}
+
+// The chunk range [w_lo, w_hi) of one wave: split `split` of the sequence covers pages
+// [split * pps, min((split + 1) * pps, cdiv(seq_len, block_size))) (reference
+// triton_fp16.py:114-116), cut into 16-token chunks, cut into W contiguous runs.
+struct WaveRange {
+    int seq_len, n_pages, w_lo, w_hi, c_full;
+};
+
+template <int W>
+__device__ __forceinline__ WaveRange wave_range(const DecodeParams& p, int b, int split,
+                                                int wave) {
+    WaveRange r;
+    int seq_len = p.seq_lens[b];
+    seq_len = min(max(seq_len, 0), p.max_blocks * p.block_size);
+    r.seq_len = seq_len;
+    r.n_pages = cdiv(seq_len, p.block_size);
+    const int pg_lo = split * p.pages_per_split;
+    const int pg_hi = min(pg_lo + p.pages_per_split, r.n_pages);
+    const int c_lo = pg_lo << p.cpp_shift;
+    const int c_hi = min(pg_hi << p.cpp_shift, cdiv(seq_len, 16));
+    const int nch = max(c_hi - c_lo, 0);
+    const int per = cdiv(nch, W);
+    r.w_lo = c_lo + wave * per;
+    r.w_hi = min(r.w_lo + per, c_hi);
+    r.c_full = seq_len >> 4;  // chunks below this index are fully valid
+    return r;
+}
+
+}  // namespace kvq

@@ -42,6 +42,10 @@ struct DecodeParams {
 hipError_t launch_decode(const DecodeParams& p, int kv_format, int head_dim, bool final_out,
                          int waves_per_group, int pipeline, hipStream_t stream);
 
+// Quantized formats (decode_q.hip); head_dim 128 only.
+hipError_t launch_decode_q(const DecodeParams& p, int kv_format, int head_dim, bool final_out,
+                           int waves_per_group, hipStream_t stream);
+
 hipError_t launch_merge(const float* o_part, const float* lse, void* out, int64_t o_sb,
                         int64_t o_sh, int batch, int q_heads, int head_dim, int num_splits,
                         hipStream_t stream);

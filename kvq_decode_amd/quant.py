@@ -1,0 +1,164 @@
+"""KIVI-quantized paged KV cache: bulk quantization (prefill) and quantize-on-append
+(decode), through libkvq.so.
+
+The reference plans quantized KV (README.md:7, :16) but has no code for it; its byte
+model (src/bpt/roofline.py:6-9) fixes the scheme: asymmetric fp16 scale + zero, keys per
+channel over groups of `k_group` tokens, values per token. Storage (include/kvq.h):
+    k_codes, v_codes  uint8 [num_blocks, block_size, Hkv, D]   (int8 / fp8_e4m3 bits)
+                      uint8 [num_blocks, block_size, Hkv, D/2] (int4, low nibble = even channel)
+    k_scale, k_zero   fp16 [num_blocks, Hkv, D]  - group g of sequence b lives in block
+                      block_table[b, g * k_group // block_size]
+    v_scale, v_zero   fp16 [num_blocks, Hkv, block_size]
+"""
+import ctypes
+from typing import NamedTuple, Optional
+
+import torch
+
+from kvq_decode_amd import _lib
+from kvq_decode_amd._lib import KV_FORMATS, DecodeArgs
+from kvq_decode_amd.ops import DEFAULT_K_GROUP, KvqArgumentError, _require
+
+QUANT_FORMATS = ("int8", "fp8_e4m3", "int4")
+
+
+class QuantizedKVCache(NamedTuple):
+    k_codes: torch.Tensor
+    v_codes: torch.Tensor
+    k_scale: torch.Tensor
+    k_zero: torch.Tensor
+    v_scale: torch.Tensor
+    v_zero: torch.Tensor
+    kv_format: str
+    k_group: int
+
+    def decode_kwargs(self):
+        """Keyword arguments for paged_decode_attention."""
+        return dict(kv_format=self.kv_format, k_scale=self.k_scale, k_zero=self.k_zero,
+                    v_scale=self.v_scale, v_zero=self.v_zero, k_group=self.k_group)
+
+
+def allocate_quantized_cache(num_blocks: int, block_size: int, kv_heads: int, head_dim: int,
+                             kv_format: str, device, k_group: int = DEFAULT_K_GROUP
+                             ) -> QuantizedKVCache:
+    """Uninitialized code and scale tensors for a quantized paged cache."""
+    _require(kv_format in QUANT_FORMATS, f"kv_format must be one of {QUANT_FORMATS}")
+    dc = head_dim // 2 if kv_format == "int4" else head_dim
+    shape = (num_blocks, block_size, kv_heads, dc)
+    kc = torch.empty(shape, dtype=torch.uint8, device=device)
+    vc = torch.empty(shape, dtype=torch.uint8, device=device)
+    ks = torch.empty((num_blocks, kv_heads, head_dim), dtype=torch.float16, device=device)
+    vs = torch.empty((num_blocks, kv_heads, block_size), dtype=torch.float16, device=device)
+    return QuantizedKVCache(kc, vc, ks, torch.empty_like(ks), vs, torch.empty_like(vs),
+                            kv_format, k_group)
+
+
+def _qargs(cache: QuantizedKVCache, block_table, seq_lens, head_dim):
+    """kvq_decode_args describing the quantized cache as the destination."""
+    nb, bs, hkv, _ = cache.k_codes.shape
+    a = DecodeArgs()
+    a.k_cache = cache.k_codes.data_ptr()
+    a.k_stride_blk, a.k_stride_tok, a.k_stride_head = cache.k_codes.stride()[:3]
+    a.v_cache = cache.v_codes.data_ptr()
+    a.v_stride_blk, a.v_stride_tok, a.v_stride_head = cache.v_codes.stride()[:3]
+    a.block_table, a.bt_stride_b = block_table.data_ptr(), block_table.stride(0)
+    a.seq_lens = seq_lens.data_ptr()
+    a.batch, a.kv_heads, a.head_dim = block_table.shape[0], hkv, head_dim
+    a.q_heads = hkv
+    a.block_size, a.max_blocks, a.num_blocks = bs, block_table.shape[1], nb
+    a.kv_format = KV_FORMATS[cache.kv_format]
+    a.k_group = cache.k_group
+    a.k_scale, a.k_zero = cache.k_scale.data_ptr(), cache.k_zero.data_ptr()
+    a.v_scale, a.v_zero = cache.v_scale.data_ptr(), cache.v_zero.data_ptr()
+    return a
+
+
+def _check_cache(cache: QuantizedKVCache, block_table, seq_lens, head_dim):
+    _require(cache.kv_format in QUANT_FORMATS, f"kv_format must be one of {QUANT_FORMATS}")
+    _require(block_table.dtype == seq_lens.dtype == torch.int32,
+             "block_table and seq_lens must be int32")
+    _require(block_table.stride(1) == 1 and seq_lens.is_contiguous(),
+             "block_table rows and seq_lens must be contiguous")
+    nb, bs, hkv, dc = cache.k_codes.shape
+    _require(dc == (head_dim // 2 if cache.kv_format == "int4" else head_dim),
+             "code cache width does not match head_dim")
+    _require(cache.k_scale.shape == (nb, hkv, head_dim) and cache.k_scale.is_contiguous(),
+             "k_scale must be contiguous [num_blocks, Hkv, D]")
+    _require(cache.v_scale.shape == (nb, hkv, bs) and cache.v_scale.is_contiguous(),
+             "v_scale must be contiguous [num_blocks, Hkv, block_size]")
+    _require(cache.k_group % bs == 0, "k_group must be a multiple of block_size")
+    dev = cache.k_codes.device
+    _require(dev.type == "cuda", "kvq runs on the GPU only (no CPU fallback)")
+
+
+def quantize_paged_cache(k_cache: torch.Tensor, v_cache: torch.Tensor,
+                         block_table: torch.Tensor, seq_lens: torch.Tensor, kv_format: str,
+                         k_group: int = DEFAULT_K_GROUP,
+                         out: Optional[QuantizedKVCache] = None) -> QuantizedKVCache:
+    """Quantize the valid tokens of fp16 paged caches (bulk / prefill).
+
+    Codes are written for the seq_lens[b] tokens of every sequence; K scales per channel
+    for every group of k_group tokens (a sequence's last group may be partial), V scales
+    per token. Slots past each sequence are left untouched."""
+    _require(k_cache.dtype == v_cache.dtype == torch.float16, "source caches must be fp16")
+    _require(k_cache.shape == v_cache.shape and k_cache.stride() == v_cache.stride(),
+             "k_cache and v_cache must have the same shape and strides")
+    _require(k_cache.stride(3) == 1, "innermost dimension must be contiguous")
+    nb, bs, hkv, d = k_cache.shape
+    if out is None:
+        out = allocate_quantized_cache(nb, bs, hkv, d, kv_format, k_cache.device, k_group)
+    _require(out.kv_format == kv_format and out.k_group == k_group,
+             "out cache format / group differ")
+    _check_cache(out, block_table, seq_lens, d)
+    args = _qargs(out, block_table, seq_lens, d)
+    stream = torch.cuda.current_stream(k_cache.device).cuda_stream
+    _lib.check("kvq_quantize_cache",
+               _lib.lib().kvq_quantize_cache(ctypes.byref(args), k_cache.data_ptr(),
+                                             v_cache.data_ptr(), k_cache.stride(0),
+                                             k_cache.stride(1), k_cache.stride(2), stream))
+    return out
+
+
+def init_k_residual(k_cache: torch.Tensor, block_table: torch.Tensor, seq_lens: torch.Tensor,
+                    k_group: int = DEFAULT_K_GROUP) -> torch.Tensor:
+    """fp16 residual [B, Hkv, k_group, D] holding, for each sequence, the K rows of its
+    open (last, incomplete) group - what quantize_append needs after a bulk prefill.
+    Rows of a complete last group are zero (the next token opens a new group)."""
+    B = block_table.shape[0]
+    nb, bs, hkv, d = k_cache.shape
+    resid = torch.zeros((B, hkv, k_group, d), dtype=torch.float16, device=k_cache.device)
+    lens = seq_lens.tolist()
+    for b, n in enumerate(lens):
+        t0 = (n // k_group) * k_group
+        if t0 >= n:
+            continue
+        t = torch.arange(t0, n, device=k_cache.device)
+        phys = block_table[b, t // bs].long()
+        resid[b, :, : n - t0] = k_cache[phys, t % bs].permute(1, 0, 2)
+    return resid
+
+
+def quantize_append(cache: QuantizedKVCache, k_new: torch.Tensor, v_new: torch.Tensor,
+                    block_table: torch.Tensor, seq_lens: torch.Tensor,
+                    k_resid: torch.Tensor) -> None:
+    """Quantize one new token per sequence into the cache (decode-time write path).
+
+    seq_lens must already count the new token: the token is at position seq_lens[b] - 1.
+    k_new / v_new: fp16 [B, Hkv, D]. V is quantized per token into its slot. K joins the
+    fp16 residual k_resid [B, Hkv, k_group, D] of its group, and the group is re-quantized
+    from the residual, so the cache always equals quantize_paged_cache of all tokens."""
+    B, hkv, d = k_new.shape
+    _check_cache(cache, block_table, seq_lens, d)
+    for name, t, shape in (("k_new", k_new, (B, hkv, d)), ("v_new", v_new, (B, hkv, d)),
+                           ("k_resid", k_resid, (B, hkv, cache.k_group, d))):
+        _require(t.dtype == torch.float16 and tuple(t.shape) == shape and t.is_contiguous(),
+                 f"{name} must be contiguous fp16 of shape {shape}")
+    args = _qargs(cache, block_table, seq_lens, d)
+    stream = torch.cuda.current_stream(k_new.device).cuda_stream
+    _lib.check("kvq_quantize_append",
+               _lib.lib().kvq_quantize_append(ctypes.byref(args), k_new.data_ptr(),
+                                              v_new.data_ptr(), k_resid.data_ptr(), stream))
+
+
+__all__ = ["QuantizedKVCache", "allocate_quantized_cache", "quantize_paged_cache",
+           "init_k_residual", "quantize_append", "QUANT_FORMATS", "KvqArgumentError"]

@@ -1,0 +1,172 @@
+"""The C ABI (include/kvq.h) on the CPU: the library loads, exports exactly the functions
+the header declares, computes the split heuristic/normalization, and rejects bad
+arguments with the documented status before any HIP call. No GPU is touched: every
+rejected call below breaks exactly one precondition, so no launch is ever reached."""
+import ctypes
+import json
+import os
+import re
+import subprocess
+
+import pytest
+
+from kvq_decode_amd import _lib
+from kvq_decode_amd._lib import DecodeArgs
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "kvq.h")
+GOLDEN = os.path.join(REPO, "tests", "golden", "reference_known_answers.json")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(kvq_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    names = declared_functions()
+    assert names == sorted(_lib.EXPORTED_SYMBOLS)
+    L = _lib.lib()
+    for n in names:
+        assert hasattr(L, n), n
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True).stdout
+    exported = sorted(set(re.findall(r"\bT (kvq_\w+)$", out, re.M)))
+    assert exported == names
+
+
+def test_struct_layout_matches_header():
+    """ctypes mirror of kvq_decode_args: same field names in the same order."""
+    text = open(HEADER).read()
+    body = text[text.index("typedef struct kvq_decode_args {"):text.index("} kvq_decode_args;")]
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    fields = []
+    for line in body.splitlines()[1:]:
+        line = line.strip().rstrip(";")
+        if not line:
+            continue
+        line = re.sub(r"^(const\s+)?(void|int64_t|int32_t|float|int32_t)\s*\*?\s*", "", line)
+        fields += [f.strip().lstrip("*") for f in line.split(",")]
+    assert fields == [f[0] for f in DecodeArgs._fields_]
+
+
+def test_version_and_status_strings():
+    assert _lib.version().startswith("kvq ")
+    L = _lib.lib()
+    assert L.kvq_status_string(0) == b"ok"
+    assert L.kvq_status_string(-3) == b"unsupported configuration"
+
+
+def test_choose_num_splits_known_answers():
+    """The reference's own recorded auto split counts (results/*.json, A100 108 SMs and
+    T4 40 SMs, block_size 32) from its heuristic (triton_fp16.py:175-180)."""
+    L = _lib.lib()
+    rows = json.load(open(GOLDEN))["auto_splits"]
+    assert len(rows) == 16
+    for r in rows:
+        got = L.kvq_choose_num_splits(r["batch"], 8, r["block_size"], r["ctx"] // r["block_size"],
+                                      r["sms"], 8, 512)
+        assert got == r["auto_splits"], r
+
+
+def test_normalize_splits():
+    L = _lib.lib()
+    s, pps = ctypes.c_int32(), ctypes.c_int32()
+    for n, pages, want in [(7, 3, (3, 1)), (32, 2048, (32, 64)), (5, 8, (4, 2)), (0, 4, (1, 4))]:
+        assert L.kvq_normalize_splits(n, pages, ctypes.byref(s), ctypes.byref(pps)) == 0
+        assert (s.value, pps.value) == want
+    assert L.kvq_normalize_splits(4, 0, ctypes.byref(s), ctypes.byref(pps)) == _lib.KVQ_ERR_SHAPE
+
+
+def good_args():
+    """A fully valid argument block with fake (never dereferenced) 256-aligned pointers."""
+    a = DecodeArgs()
+    base = 1 << 40
+    a.q, a.q_stride_b, a.q_stride_h = base, 32 * 128, 128
+    a.k_cache, a.k_stride_blk, a.k_stride_tok, a.k_stride_head = base + (1 << 30), 16 * 8 * 128, 8 * 128, 128
+    a.v_cache, a.v_stride_blk, a.v_stride_tok, a.v_stride_head = base + (2 << 30), 16 * 8 * 128, 8 * 128, 128
+    a.block_table, a.bt_stride_b = base + (3 << 30), 64
+    a.seq_lens = base + (4 << 30)
+    a.out, a.o_stride_b, a.o_stride_h = base + (5 << 30), 32 * 128, 128
+    a.batch, a.q_heads, a.kv_heads, a.head_dim = 2, 32, 8, 128
+    a.block_size, a.max_blocks, a.num_blocks = 16, 64, 128
+    a.scale = 0.088
+    a.kv_format = 0
+    a.k_group = 128
+    return a
+
+
+BAD_CASES = [
+    ("q", 0, _lib.KVQ_ERR_NULL_POINTER),
+    ("block_table", 0, _lib.KVQ_ERR_NULL_POINTER),
+    ("out", 0, _lib.KVQ_ERR_NULL_POINTER),
+    ("batch", 0, _lib.KVQ_ERR_SHAPE),
+    ("q_heads", 30, _lib.KVQ_ERR_SHAPE),           # not a multiple of kv_heads
+    ("head_dim", 96, _lib.KVQ_ERR_SHAPE),          # not a power of two (reference asserts too)
+    ("head_dim", 512, _lib.KVQ_ERR_UNSUPPORTED),   # valid for the reference, not built here
+    ("block_size", 8, _lib.KVQ_ERR_SHAPE),
+    ("q_heads", 8 * 32, _lib.KVQ_ERR_UNSUPPORTED),  # group 32 > 16
+    ("kv_format", 9, _lib.KVQ_ERR_FORMAT),
+    ("kv_format", 1, _lib.KVQ_ERR_FORMAT),          # quantized without scale tensors
+    ("q", (1 << 40) + 8, _lib.KVQ_ERR_ALIGNMENT),
+    ("k_stride_tok", 8 * 128 + 4, _lib.KVQ_ERR_ALIGNMENT),
+    ("k_stride_tok", 1 << 27, _lib.KVQ_ERR_UNSUPPORTED),   # 32-bit lane offsets
+    ("waves_per_group", 3, _lib.KVQ_ERR_UNSUPPORTED),
+    ("pipeline", 5, _lib.KVQ_ERR_UNSUPPORTED),
+]
+
+
+@pytest.mark.parametrize("field,value,status", BAD_CASES)
+def test_single_pass_rejects(field, value, status):
+    a = good_args()
+    setattr(a, field, value)
+    assert _lib.lib().kvq_decode_single(ctypes.byref(a), None) == status
+
+
+def test_split_rejects_bad_split_geometry():
+    L = _lib.lib()
+    a = good_args()
+    op, lse = 1 << 41, 1 << 42
+    assert L.kvq_decode_split(ctypes.byref(a), 0, 4, op, lse, None) == _lib.KVQ_ERR_SPLITS
+    assert L.kvq_decode_split(ctypes.byref(a), 4, 8, op, lse, None) == _lib.KVQ_ERR_SPLITS  # 32 < 64 pages
+    assert L.kvq_decode_split(ctypes.byref(a), 4, 16, 0, lse, None) == _lib.KVQ_ERR_NULL_POINTER
+    assert L.kvq_decode_split(None, 4, 16, op, lse, None) == _lib.KVQ_ERR_NULL_POINTER
+
+
+def test_merge_and_quantize_reject():
+    L = _lib.lib()
+    assert L.kvq_decode_merge(0, 1 << 41, 1 << 42, 128, 128, 1, 32, 128, 4, None) == \
+        _lib.KVQ_ERR_NULL_POINTER
+    assert L.kvq_decode_merge(1 << 40, 1 << 41, 1 << 42, 128, 128, 1, 32, 100, 4, None) == \
+        _lib.KVQ_ERR_SHAPE
+    a = good_args()  # kv_format fp16 is not a quantization target
+    assert L.kvq_quantize_cache(ctypes.byref(a), 1 << 40, 1 << 40, 0, 0, 0, None) == \
+        _lib.KVQ_ERR_FORMAT
+    a.kv_format = 3
+    a.k_scale = a.k_zero = a.v_scale = a.v_zero = 1 << 43
+    a.k_group = 100  # not a multiple of block_size
+    assert L.kvq_quantize_cache(ctypes.byref(a), 1 << 40, 1 << 40, 0, 0, 0, None) == \
+        _lib.KVQ_ERR_UNSUPPORTED
+    a.k_group = 128
+    assert L.kvq_quantize_append(ctypes.byref(a), 0, 1 << 40, 1 << 41, None) == \
+        _lib.KVQ_ERR_NULL_POINTER
+
+
+def test_python_op_argument_errors_and_no_cpu_fallback():
+    """The host op raises the reference's AssertionError family for its preconditions
+    (triton_fp16.py:195-201) and refuses CPU tensors instead of falling back."""
+    import torch
+
+    from kvq_decode_amd import KvqArgumentError, paged_decode_attention
+    q = torch.zeros(2, 32, 128, dtype=torch.float16)
+    kc = torch.zeros(8, 16, 8, 128, dtype=torch.float16)
+    bt = torch.zeros(2, 4, dtype=torch.int32)
+    sl = torch.ones(2, dtype=torch.int32)
+    with pytest.raises(AssertionError):
+        paged_decode_attention(q.float(), kc, kc, bt, sl)
+    with pytest.raises(KvqArgumentError):
+        paged_decode_attention(q, kc, kc, bt.long(), sl)
+    with pytest.raises(KvqArgumentError):
+        paged_decode_attention(q[:, :30], kc, kc, bt, sl)
+    with pytest.raises(KvqArgumentError, match="GPU only"):
+        paged_decode_attention(q, kc, kc, bt, sl)

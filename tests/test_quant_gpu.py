@@ -1,0 +1,228 @@
+"""KIVI-quantized KV on the GPU vs the numpy spec (oracle/kivi.py). Needs a GPU.
+
+  * bulk quantizer: codes and scales bit-exact with the spec (valid slots only);
+  * decode over INT8 / FP8-e4m3 / INT4 caches: within |out - ref| <= 2e-3 + 1e-2 |ref| of
+    float32 attention over the dequantized cache (the north star's bar for quantized KV);
+  * quantize-on-append: appending tokens one at a time leaves exactly the cache the bulk
+    quantizer produces for all tokens.
+K ~ N(0,1) with 4 random outlier channels per kv head scaled x10.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import kivi
+from oracle.attention import build_paged_cache, paged_decode_attention_ref
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 1e-2
+FORMATS = ["int8", "fp8_e4m3", "int4"]
+
+
+def make(lens, bs, Hq=32, Hkv=8, D=128, seed=0, outliers=True):
+    rng = np.random.default_rng(seed)
+    B, S = len(lens), max(lens)
+    q = rng.standard_normal((B, Hq, D)).astype(np.float16)
+    k = rng.standard_normal((B, S, Hkv, D)).astype(np.float32)
+    if outliers:
+        for h in range(Hkv):
+            k[:, :, h, rng.choice(D, 4, replace=False)] *= 10
+    k = k.astype(np.float16)
+    v = rng.standard_normal((B, S, Hkv, D)).astype(np.float16)
+    sl = np.array(lens, np.int32)
+    kc, vc, bt = build_paged_cache(k, v, sl, bs, rng)
+    return q, kc, vc, bt, sl
+
+
+def gpu(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def valid_slots(bt, sl, bs):
+    """(phys, slot) of every valid token."""
+    out = []
+    for b, n in enumerate(sl):
+        for t in range(int(n)):
+            out.append((int(bt[b, t // bs]), t % bs))
+    return np.array(out)
+
+
+def lead_blocks(bt, sl, bs, group=128):
+    return sorted({int(bt[b, (g * group) // bs]) for b, n in enumerate(sl)
+                   for g in range(-(-int(n) // group))})
+
+
+def check_close(out, ref, tag):
+    out = out.float().cpu().numpy()
+    diff = np.abs(out - ref)
+    print(f"\n[{tag}] max_abs={diff.max():.3e} "
+          f"max_rel(clamp 1e-3)={(diff / np.maximum(np.abs(ref), 1e-3)).max():.3e}", flush=True)
+    assert np.isfinite(out).all()
+    assert diff.max() < ATOL
+    assert np.all(diff <= ATOL + RTOL * np.abs(ref))
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("bs", [16, 32])
+def test_bulk_quantizer_bit_exact(fmt, bs):
+    from kvq_decode_amd.quant import quantize_paged_cache
+    q, kc, vc, bt, sl = make([1, 37, 128, 129, 300, 1000], bs)
+    want = kivi.quantize_paged_cache(kc, vc, bt, sl, fmt)
+    got = quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt)
+    torch.cuda.synchronize()
+    slots = valid_slots(bt, sl, bs)
+    for name in ("k_codes", "v_codes"):
+        g = getattr(got, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
+        w = want[name][slots[:, 0], slots[:, 1]]
+        assert np.array_equal(g, w), f"{name}: {np.sum(g != w)} of {g.size} bytes differ"
+    lead = lead_blocks(bt, sl, bs)
+    for name in ("k_scale", "k_zero"):
+        g = getattr(got, name).cpu().numpy()[lead].view(np.uint16)
+        assert np.array_equal(g, want[name][lead].view(np.uint16)), name
+    for name in ("v_scale", "v_zero"):
+        g = getattr(got, name).cpu().numpy()[slots[:, 0], :, slots[:, 1]].view(np.uint16)
+        w = want[name][slots[:, 0], :, slots[:, 1]].view(np.uint16)
+        assert np.array_equal(g, w), name
+
+
+@pytest.mark.parametrize("num_splits", [1, 3, None])
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("bs", [16, 32])
+def test_decode_matches_fp32_attention_over_dequantized_cache(fmt, bs, num_splits):
+    from kvq_decode_amd import paged_decode_attention
+    from kvq_decode_amd.quant import quantize_paged_cache
+    lens = [1, 37, 300, 2049, 129]
+    q, kc, vc, bt, sl = make(lens, bs, seed=1)
+    qc = quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt)
+    host = {n: getattr(qc, n).cpu().numpy() for n in
+            ("k_codes", "v_codes", "k_scale", "k_zero", "v_scale", "v_zero")}
+    kd, vd = kivi.dequantize_paged_cache(host, bt, sl, fmt)
+    ref = paged_decode_attention_ref(q.astype(np.float32), kd, vd, bt, sl, out_dtype=np.float32)
+    out = paged_decode_attention(gpu(q), qc.k_codes, qc.v_codes, gpu(bt), gpu(sl),
+                                 num_splits=num_splits, **qc.decode_kwargs())
+    check_close(out, ref, f"{fmt} bs={bs} splits={num_splits}")
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_decode_group8_and_mqa_heads(fmt):
+    """Other GQA groups over a quantized cache: 8 q heads per kv head, and MQA."""
+    from kvq_decode_amd import paged_decode_attention
+    from kvq_decode_amd.quant import quantize_paged_cache
+    for Hq, Hkv in ((16, 2), (8, 1)):
+        q, kc, vc, bt, sl = make([700, 3], 16, Hq=Hq, Hkv=Hkv, seed=2)
+        qc = quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt)
+        host = {n: getattr(qc, n).cpu().numpy() for n in
+                ("k_codes", "v_codes", "k_scale", "k_zero", "v_scale", "v_zero")}
+        kd, vd = kivi.dequantize_paged_cache(host, bt, sl, fmt)
+        ref = paged_decode_attention_ref(q.astype(np.float32), kd, vd, bt, sl,
+                                         out_dtype=np.float32)
+        out = paged_decode_attention(gpu(q), qc.k_codes, qc.v_codes, gpu(bt), gpu(sl),
+                                     num_splits=2, **qc.decode_kwargs())
+        check_close(out, ref, f"{fmt} Hq={Hq} Hkv={Hkv}")
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_append_equals_bulk(fmt):
+    """Bulk-quantize a prefix, then append tokens one by one across group boundaries; the
+    cache must equal the bulk quantization of all tokens, bit for bit, and decode on it
+    must match."""
+    from kvq_decode_amd.quant import init_k_residual, quantize_append, quantize_paged_cache
+    bs = 16
+    n0 = [100, 1, 127, 250]
+    n1 = [140, 40, 131, 260]
+    q, kc, vc, bt, sl1 = make(n1, bs, Hkv=2, seed=3)
+    Hkv = kc.shape[2]
+    kc_g, vc_g, bt_g = gpu(kc), gpu(vc), gpu(bt)
+    sl0 = torch.tensor(n0, dtype=torch.int32, device="cuda")
+    qc = quantize_paged_cache(kc_g, vc_g, bt_g, sl0, fmt)
+    resid = init_k_residual(kc_g, bt_g, sl0)
+    cur = list(n0)
+    while any(c < e for c, e in zip(cur, n1)):
+        nxt = [min(c + 1, e) for c, e in zip(cur, n1)]
+        grow = [b for b in range(4) if nxt[b] > cur[b]]
+        # sequences that already reached their length re-append their last token (idempotent)
+        k_new = torch.empty((4, Hkv, 128), dtype=torch.float16, device="cuda")
+        v_new = torch.empty_like(k_new)
+        for b in range(4):
+            t = nxt[b] - 1
+            k_new[b] = kc_g[bt_g[b, t // bs], t % bs]
+            v_new[b] = vc_g[bt_g[b, t // bs], t % bs]
+        sl = torch.tensor(nxt, dtype=torch.int32, device="cuda")
+        quantize_append(qc, k_new, v_new, bt_g, sl, resid)
+        cur = nxt
+        assert grow
+    torch.cuda.synchronize()
+    want = quantize_paged_cache(kc_g, vc_g, bt_g, gpu(sl1), fmt)
+    torch.cuda.synchronize()
+    slots = valid_slots(bt, sl1, bs)
+    for name in ("k_codes", "v_codes"):
+        g = getattr(qc, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
+        w = getattr(want, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
+        assert np.array_equal(g, w), name
+    lead = lead_blocks(bt, sl1, bs)
+    for name in ("k_scale", "k_zero"):
+        assert np.array_equal(getattr(qc, name).cpu().numpy()[lead],
+                              getattr(want, name).cpu().numpy()[lead]), name
+    for name in ("v_scale", "v_zero"):
+        g = getattr(qc, name).cpu().numpy()[slots[:, 0], :, slots[:, 1]]
+        w = getattr(want, name).cpu().numpy()[slots[:, 0], :, slots[:, 1]]
+        assert np.array_equal(g, w), name
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp8_e4m3"])
+def test_c4_full_size(fmt):
+    """B=16, seq_len 32768, bs 16, 32768-block pool, outlier K. The
+    quantizer is checked bit-exact and the decode against the oracle on two sequences
+    (the oracle takes seconds per sequence at this size)."""
+    _full_size_case(fmt, [32768] * 16, check_seqs=(0, 15))
+
+
+def test_c5_int4_full_size():
+    """INT4, B=64, seq_lens ~ U[1024, 32768] (seed 0), shared pool."""
+    lens = np.random.default_rng(0).integers(1024, 32769, 64).tolist()
+    _full_size_case("int4", lens, check_seqs=(0, 31, 63))
+
+
+def _full_size_case(fmt, lens, check_seqs):
+    from kvq_decode_amd import paged_decode_attention
+    from kvq_decode_amd.quant import quantize_paged_cache
+    g = torch.Generator(device="cuda").manual_seed(0)
+    B, Hq, Hkv, D, bs = len(lens), 32, 8, 128, 16
+    pages = [-(-n // bs) for n in lens]
+    pool = sum(pages)
+    mb = max(pages)
+    q = torch.randn(B, Hq, D, generator=g, device="cuda").half()
+    k = torch.randn(pool, bs, Hkv, D, generator=g, device="cuda")
+    for h in range(Hkv):
+        ch = torch.randperm(D, generator=g, device="cuda")[:4]
+        k[:, :, h, ch] *= 10
+    k = k.half()
+    v = torch.randn(pool, bs, Hkv, D, generator=g, device="cuda").half()
+    perm = torch.randperm(pool, generator=g, device="cuda").int()
+    bt = torch.zeros(B, mb, dtype=torch.int32, device="cuda")
+    o = 0
+    for b, n in enumerate(pages):
+        bt[b, :n] = perm[o:o + n]
+        o += n
+    sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    qc = quantize_paged_cache(k, v, bt, sl, fmt)
+    out = paged_decode_attention(q, qc.k_codes, qc.v_codes, bt, sl, **qc.decode_kwargs())
+    torch.cuda.synchronize()
+    btn, sln = bt.cpu().numpy(), sl.cpu().numpy()
+    for b in check_seqs:
+        blocks = btn[b, :pages[b]].astype(np.int64)
+        sub_bt = np.arange(pages[b], dtype=np.int32)[None]
+        sub_sl = sln[b:b + 1]
+        kc, vc = k[blocks].cpu().numpy(), v[blocks].cpu().numpy()
+        want = kivi.quantize_paged_cache(kc, vc, sub_bt, sub_sl, fmt)
+        host = {n: getattr(qc, n)[blocks].cpu().numpy() for n in
+                ("k_codes", "v_codes", "k_scale", "k_zero", "v_scale", "v_zero")}
+        n = int(sub_sl[0])
+        flat = lambda a: a.reshape(-1, *a.shape[2:])[:n]  # noqa: E731
+        assert np.array_equal(flat(host["k_codes"]), flat(want["k_codes"]))
+        assert np.array_equal(flat(host["v_codes"]), flat(want["v_codes"]))
+        kd, vd = kivi.dequantize_paged_cache(host, sub_bt, sub_sl, fmt)
+        ref = paged_decode_attention_ref(q[b:b + 1].cpu().numpy().astype(np.float32), kd, vd,
+                                         sub_bt, sub_sl, out_dtype=np.float32)
+        check_close(out[b:b + 1], ref, f"{fmt} full-size seq {b} len {n}")
