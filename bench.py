@@ -28,12 +28,18 @@ METRIC = ("achieved KV-read TB/s & % of 8 TB/s HBM peak; µs per decode step (1 
 PEAK_GBPS = 8000.0
 HQ, HKV, D, BS = 32, 8, 128, 16
 
-# name -> (batch, ctx, pool blocks, description); BASELINE.json configs[0..2]
+# name -> (batch, ctx, pool blocks, kv_format, description). ctx None = ragged lengths
+# U[1024, 32768]; pool None = sum of the sequences' pages.
 CONFIGS = {
-    "C1": (1, 4096, 256, "C1: fp16 KV, batch 1, seq_len 4096, no split"),
-    "C2": (8, 32768, 16384, "C2: fp16 KV, batch 8, seq_len 32768, split-KV + merge"),
-    "C3": (1, 131072, 8192, "C3: fp16 KV, batch 1, seq_len 131072, split-KV + merge"),
-    "B1_64K": (1, 65536, 4096, "fp16 KV, batch 1, seq_len 65536 (north-star 50% point)"),
+    "C1": (1, 4096, 256, "fp16", "C1: fp16 KV, batch 1, seq_len 4096, no split"),
+    "C2": (8, 32768, 16384, "fp16", "C2: fp16 KV, batch 8, seq_len 32768, split-KV + merge"),
+    "C3": (1, 131072, 8192, "fp16", "C3: fp16 KV, batch 1, seq_len 131072, split-KV + merge"),
+    "B1_64K": (1, 65536, 4096, "fp16", "fp16 KV, batch 1, seq_len 65536 (north-star 50% point)"),
+    "C4_INT8": (16, 32768, 32768, "int8", "C4: INT8 KIVI KV, batch 16, seq_len 32768"),
+    "C4_FP8": (16, 32768, 32768, "fp8_e4m3", "C4: FP8-e4m3 KIVI KV, batch 16, seq_len 32768"),
+    "B16_FP16": (16, 32768, 32768, "fp16", "fp16 KV, batch 16, seq_len 32768 (INT4 comparison)"),
+    "B16_INT4": (16, 32768, 32768, "int4", "INT4 KIVI KV, batch 16, seq_len 32768 (>=3x target)"),
+    "C5": (64, None, None, "int4", "C5: INT4 KIVI KV, batch 64, seq_lens U[1024, 32768]"),
 }
 
 
@@ -41,23 +47,59 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def make_inputs(B, ctx, pool, seed=0):
+def seq_lengths(B, ctx, seed=0):
+    import numpy as np
+    if ctx is not None:
+        return [ctx] * B
+    return np.random.default_rng(seed).integers(1024, 32769, B).tolist()
+
+
+def make_inputs(B, ctx, pool, seed=0, kv_format="fp16"):
+    """q, K, V ~ N(0,1) fp16 (K with 4 random outlier channels per kv head scaled x10 for
+    the quantized configs, BASELINE.json configs[3-4]), a block table that is a random
+    permutation of the pool, and the sequence lengths. Quantized caches are built with
+    the library's own bulk quantizer. Returns (q, k, v, bt, sl, fmt_kwargs)."""
     import torch
     g = torch.Generator(device="cuda").manual_seed(seed)
+    lens = seq_lengths(B, ctx, seed)
+    pages = [-(-n // BS) for n in lens]
+    pool = pool if pool is not None else sum(pages)
     q = torch.randn(B, HQ, D, generator=g, device="cuda").half()
-    k = torch.randn(pool, BS, HKV, D, generator=g, device="cuda").half()
+    k = torch.randn(pool, BS, HKV, D, generator=g, device="cuda")
+    if kv_format != "fp16":
+        for h in range(HKV):
+            k[:, :, h, torch.randperm(D, generator=g, device="cuda")[:4]] *= 10
+    k = k.half()
     v = torch.randn(pool, BS, HKV, D, generator=g, device="cuda").half()
-    nb = ctx // BS
-    bt = torch.randperm(pool, generator=g, device="cuda")[: B * nb].view(B, nb).int().contiguous()
-    sl = torch.full((B,), ctx, dtype=torch.int32, device="cuda")
-    return q, k, v, bt, sl
+    perm = torch.randperm(pool, generator=g, device="cuda").int()
+    bt = torch.zeros(B, max(pages), dtype=torch.int32, device="cuda")
+    o = 0
+    for b, n in enumerate(pages):
+        bt[b, :n] = perm[o:o + n]
+        o += n
+    sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    fmt = {}
+    if kv_format != "fp16":
+        from kvq_decode_amd.quant import quantize_paged_cache
+        qc = quantize_paged_cache(k, v, bt, sl, kv_format)
+        torch.cuda.synchronize()
+        del k, v
+        k, v = qc.k_codes, qc.v_codes
+        fmt = qc.decode_kwargs()
+    return q, k, v, bt, sl, fmt
+
+
+def kv_bytes(lens, kv_format):
+    """Algorithmic KV bytes of one step (reference roofline.py:50-63 per token-head)."""
+    from kvq_decode_amd.roofline import bytes_per_token_head
+    return int(round(sum(lens) * HKV * bytes_per_token_head(D, kv_format)))
 
 
 class Step:
     """One decode step through the C ABI with prebuilt arguments and workspace, so the
     timed loop issues exactly the library's launches (split + merge, or single pass)."""
 
-    def __init__(self, q, k, v, bt, sl, splits, waves=0, pipeline=0):
+    def __init__(self, q, k, v, bt, sl, splits, waves=0, pipeline=0, fmt=None):
         import ctypes
 
         import torch
@@ -70,7 +112,7 @@ class Step:
         self.out = torch.empty_like(q)
         self.splits, self.pps = ops.normalize_splits(splits, bt.shape[1])
         self.args = ops.build_args(q, k, v, bt, sl, self.out, 1.0 / math.sqrt(D),
-                                   waves_per_group=waves, pipeline=pipeline)
+                                   waves_per_group=waves, pipeline=pipeline, **(fmt or {}))
         self.o_part = torch.empty(B, HQ, self.splits, D, dtype=torch.float32, device="cuda")
         self.lse = torch.empty(B, HQ, self.splits, dtype=torch.float32, device="cuda")
         self.stream = torch.cuda.current_stream().cuda_stream
@@ -132,12 +174,12 @@ def time_stage1(step, iters):
 
 def time_flushed(step, iters):
     """Median step time with the 256 MB Infinity Cache flushed before each step (a 1 GiB
-    scratch write), per-iteration events around the step only."""
+    scratch buffer is read, leaving clean lines), per-iteration events around the step."""
     import torch
-    scratch = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+    scratch = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
     ts = []
     for _ in range(iters):
-        scratch.zero_()
+        scratch.sum()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         step()
@@ -150,14 +192,14 @@ def time_flushed(step, iters):
 
 
 def cpu_baseline(q, k, v, bt, sl):
-    """The numpy oracle (oracle/attention.py, fp32) on the full workload on the host: one
-    BLAS thread, 1 warmup + 3 timed reps. Checker code, timed only as the CPU baseline."""
-    import numpy as np
+    """The numpy oracle (oracle/attention.py, fp32) on the full fp16 workload on the host:
+    one BLAS thread, 1 warmup + 3 timed reps. Checker code, timed only as the CPU
+    baseline."""
     from threadpoolctl import threadpool_limits
 
     from oracle.attention import paged_decode_attention_ref
     qn, kn, vn, btn, sln = (t.cpu().numpy() for t in (q, k, v, bt, sl))
-    nbytes = float(sum(int(x) for x in sln)) * HKV * 2 * D * 2
+    nbytes = kv_bytes([int(x) for x in sln], "fp16")
     with threadpool_limits(limits=1):
         paged_decode_attention_ref(qn, kn, vn, btn, sln)
         reps = 3
@@ -173,7 +215,8 @@ def cpu_baseline(q, k, v, bt, sl):
 
 def read_traffic(workload, splits):
     """HBM bytes per stage-1 launch measured by rocprofv3 --pmc, if a summary for this
-    workload and split count is committed under profiles/ (see DESIGN.md), else None."""
+    workload and split count is committed under profiles/, else None. The file holds
+    `key = value` lines; `splits` must match and `hbm_bytes_per_launch` is returned."""
     path = os.path.join(REPO, "profiles", f"decode_split_{workload}_traffic.txt")
     if not os.path.exists(path):
         return None
@@ -191,23 +234,70 @@ def read_traffic(workload, splits):
         return None
 
 
+def default_plan(config, B, max_pages):
+    """(splits, waves) the op would use with num_splits=None (C1: no split, configs[0])."""
+    from kvq_decode_amd import _sm_count
+    from kvq_decode_amd.ops import plan_decode
+    if config == "C1":
+        return 1, 0
+    return plan_decode(B, HKV, BS, max_pages, _sm_count(0), CONFIGS[config][3])
+
+
+def run_config(config, steps, warmup, splits=None, waves=0, pipeline=0, flushed=True):
+    """Measure one configuration; returns the result fields (no CPU baseline)."""
+    B, ctx, pool, fmt_name, desc = CONFIGS[config]
+    q, k, v, bt, sl, fmt = make_inputs(B, ctx, pool, kv_format=fmt_name)
+    lens = [int(x) for x in sl.tolist()]
+    if splits is None:
+        splits, planned = default_plan(config, B, bt.shape[1])
+        waves = waves or planned
+    step = Step(q, k, v, bt, sl, splits, waves, pipeline, fmt)
+    nbytes = kv_bytes(lens, fmt_name)
+    log(f"{config}: {desc}; splits={step.splits} pages/split={step.pps} KV bytes/step={nbytes}")
+    wall_ms, ev_ms = time_steps(step, steps, warmup)
+    stage1_ms = time_stage1(step, max(20, min(steps, 100)))
+    flushed_ms = time_flushed(step, 30) if flushed else None
+    log(f"  wall {wall_ms * 1e3:.1f} us/step (events {ev_ms * 1e3:.1f}), stage 1 "
+        f"{stage1_ms * 1e3:.1f} us" + (f", flushed median {flushed_ms * 1e3:.1f} us" if flushed else ""))
+    tbs = nbytes / (wall_ms * 1e-3) / 1e12
+    achieved = nbytes / (stage1_ms * 1e-3) / 1e9
+    kernel = "decode_f16_kernel" if fmt_name == "fp16" else "decode_q_kernel"
+    res = {
+        "value": round(tbs, 4), "ms_per_step": round(wall_ms, 5),
+        "us_per_step": round(wall_ms * 1e3, 2),
+        "pct_of_hbm_peak": round(100 * tbs * 1e3 / PEAK_GBPS, 2),
+        "us_per_step_flushed_median": round(flushed_ms * 1e3, 2) if flushed else None,
+        "config": {"workload": desc, "batch": B, "seq_len": ctx if ctx else "U[1024,32768]",
+                   "sum_seq_lens": sum(lens), "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
+                   "block_size": BS, "pool_blocks": k.shape[0], "num_splits": step.splits,
+                   "pages_per_split": step.pps, "waves_per_group": waves,
+                   "kv_bytes_per_step": nbytes, "kv_format": fmt_name},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
+                     "traffic": read_traffic(config, step.splits),
+                     "kernel": f"{kernel} (stage 1)", "kernel_us": round(stage1_ms * 1e3, 2)},
+    }
+    return res, (q, k, v, bt, sl)
+
+
 def sweep(args):
     import torch
-    B, ctx, pool, _ = CONFIGS[args.config]
-    q, k, v, bt, sl = make_inputs(B, ctx, pool)
-    nbytes = B * ctx * HKV * 2 * D * 2
-    log(f"{args.config}: B={B} ctx={ctx} kv={nbytes / 1e9:.3f} GB")
+    B, ctx, pool, fmt_name, _ = CONFIGS[args.config]
+    q, k, v, bt, sl, fmt = make_inputs(B, ctx, pool, kv_format=fmt_name)
+    nbytes = kv_bytes([int(x) for x in sl.tolist()], fmt_name)
+    log(f"{args.config}: B={B} ctx={ctx} {fmt_name} kv={nbytes / 1e9:.3f} GB")
     log(f"{'splits':>6}{'waves':>6}{'pipe':>5}{'step_us':>10}{'stage1_us':>11}{'TB/s':>8}{'%peak':>7}")
+    pipes = (1, 2) if fmt_name == "fp16" else (1,)
     for splits in [int(s) for s in args.sweep_splits.split(",")]:
         for waves in [int(w) for w in args.sweep_waves.split(",")]:
-            for pipe in (1, 2):
+            for pipe in pipes:
                 try:
-                    st = Step(q, k, v, bt, sl, splits, waves, pipe)
+                    st = Step(q, k, v, bt, sl, splits, waves, pipe, fmt)
+                    _, ev_ms = time_steps(st, 20, 5)
+                    s1 = time_stage1(st, 20)
                 except Exception as e:  # invalid combination for this config
                     log(f"{splits:>6}{waves:>6}{pipe:>5}  skipped: {e}")
                     continue
-                _, ev_ms = time_steps(st, 20, 5)
-                s1 = time_stage1(st, 20)
                 tbs = nbytes / (ev_ms * 1e-3) / 1e12
                 log(f"{st.splits:>6}{waves:>6}{pipe:>5}{ev_ms * 1e3:>10.1f}{s1 * 1e3:>11.1f}"
                     f"{tbs:>8.3f}{100 * tbs * 1e3 / PEAK_GBPS:>7.1f}")
@@ -221,79 +311,46 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="C2", choices=sorted(CONFIGS))
-    ap.add_argument("--splits", type=int, default=None, help="default: the heuristic")
+    ap.add_argument("--splits", type=int, default=None, help="default: the op's heuristic")
     ap.add_argument("--waves", type=int, default=0)
     ap.add_argument("--pipeline", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--sweep", action="store_true")
-    ap.add_argument("--sweep-splits", default="8,16,32,64")
-    ap.add_argument("--sweep-waves", default="1,2,4,8,16")
+    ap.add_argument("--sweep", action="store_true", help="split/waves sweep, table on stderr")
+    ap.add_argument("--sweep-splits", default="1,2,4,8,16,32,64,128")
+    ap.add_argument("--sweep-waves", default="1,2,4,8")
+    ap.add_argument("--suite", action="store_true",
+                    help="every configuration; one JSON line per configuration")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); the "
               "multi-GPU sharding of the path is described in DESIGN.md", file=sys.stderr)
         sys.exit(2)
 
-    import torch
-
-    from kvq_decode_amd import _sm_count, choose_num_splits
     if args.sweep:
         sweep(args)
         return
-
-    B, ctx, pool, desc = CONFIGS[args.config]
-    log(f"bench {args.config}: {desc}")
-    q, k, v, bt, sl = make_inputs(B, ctx, pool)
-    cus = _sm_count(0)
-    splits = args.splits if args.splits is not None else choose_num_splits(B, HKV, BS, ctx // BS, cus)
-    if args.config == "C1" and args.splits is None:
-        splits = 1
-    step = Step(q, k, v, bt, sl, splits, args.waves, args.pipeline)
-    nbytes = B * ctx * HKV * 2 * D * 2
-    log(f"splits={step.splits} pages/split={step.pps} CUs={cus} KV bytes/step={nbytes}")
-
-    wall_ms, ev_ms = time_steps(step, args.steps, args.warmup)
-    log(f"timed {args.steps} steps: wall {wall_ms * 1e3:.1f} us/step, events {ev_ms * 1e3:.1f} us/step")
-    stage1_ms = time_stage1(step, max(20, min(args.steps, 100)))
-    log(f"stage-1 kernel average: {stage1_ms * 1e3:.1f} us")
-    flushed_ms = time_flushed(step, 30)
-    log(f"flushed-cache median step: {flushed_ms * 1e3:.1f} us")
-
-    tbs = nbytes / (wall_ms * 1e-3) / 1e12
-    achieved_gbps = nbytes / (stage1_ms * 1e-3) / 1e9
-    traffic = read_traffic(args.config, step.splits)
-    result = {
-        "metric": METRIC,
-        "value": round(tbs, 4),
-        "unit": "TB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(wall_ms, 5),
-        "us_per_step": round(wall_ms * 1e3, 2),
-        "pct_of_hbm_peak": round(100 * tbs * 1e3 / PEAK_GBPS, 2),
-        "us_per_step_flushed_median": round(flushed_ms * 1e3, 2),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "fp16",
-        "data": "synthetic: q, K, V ~ N(0,1) fp16, random-permutation block table, seed 0",
-        "config": {"workload": desc, "batch": B, "seq_len": ctx, "q_heads": HQ, "kv_heads": HKV,
-                   "head_dim": D, "block_size": BS, "pool_blocks": pool,
-                   "num_splits": step.splits, "pages_per_split": step.pps,
-                   "kv_bytes_per_step": nbytes, "kv_format": "fp16"},
-        "roofline": {"bound": "hbm", "achieved": round(achieved_gbps, 1), "peak": PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved_gbps / PEAK_GBPS, 4),
-                     "traffic": traffic, "kernel": "decode_f16_kernel (stage 1)",
-                     "kernel_us": round(stage1_ms * 1e3, 2)},
-    }
-    if not args.no_cpu_baseline:
-        log("cpu baseline (numpy oracle) ...")
-        cb = cpu_baseline(q, k, v, bt, sl)
-        log(f"cpu baseline: {cb['s_per_step'] * 1e3:.0f} ms/step")
-        cb.pop("s_per_step")
-        result["cpu_baseline"] = cb
-    print(json.dumps(result), flush=True)
+    import torch
+    names = list(CONFIGS) if args.suite else [args.config]
+    for name in names:
+        res, inputs = run_config(name, args.steps, args.warmup, args.splits, args.waves,
+                                 args.pipeline)
+        result = {"metric": METRIC, "value": res.pop("value"), "unit": "TB/s", "n_gpus": 1,
+                  "steps": args.steps, "warmup": args.warmup, **res,
+                  "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                  "dtype": "fp16",
+                  "data": "synthetic: q, K, V ~ N(0,1) fp16 (quantized configs: K with 4 "
+                          "outlier channels x10 per kv head), random-permutation block "
+                          "table, seed 0"}
+        fmt_name = CONFIGS[name][3]
+        if not args.no_cpu_baseline and not args.suite and fmt_name == "fp16":
+            log("cpu baseline (numpy oracle) ...")
+            cb = cpu_baseline(*inputs)
+            log(f"cpu baseline: {cb['s_per_step'] * 1e3:.0f} ms/step")
+            cb.pop("s_per_step")
+            result["cpu_baseline"] = cb
+        del inputs
+        torch.cuda.empty_cache()
+        print(json.dumps(result), flush=True)
 
 
 if __name__ == "__main__":

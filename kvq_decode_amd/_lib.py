@@ -28,6 +28,7 @@ EXPORTED_SYMBOLS = (
     "kvq_version",
     "kvq_status_string",
     "kvq_choose_num_splits",
+    "kvq_plan_decode",
     "kvq_normalize_splits",
     "kvq_decode_split",
     "kvq_decode_merge",
@@ -89,6 +90,8 @@ def lib():
         L.kvq_status_string.argtypes = [ctypes.c_int]
         L.kvq_choose_num_splits.restype = ctypes.c_int
         L.kvq_choose_num_splits.argtypes = [_i32] * 7
+        L.kvq_plan_decode.restype = ctypes.c_int
+        L.kvq_plan_decode.argtypes = [_i32] * 6 + [ctypes.POINTER(_i32)] * 2
         L.kvq_normalize_splits.restype = ctypes.c_int
         L.kvq_normalize_splits.argtypes = [_i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)]
         args_p = ctypes.POINTER(DecodeArgs)

@@ -21,6 +21,12 @@ int ilog2(int64_t x) {
 }
 
 int cdiv(int64_t a, int64_t b) { return int((a + b - 1) / b); }
+// largest power of two <= x, and 1 for x < 1
+int64_t pow2_floor(int64_t x) {
+    int64_t p = 1;
+    while (p * 2 <= x) p *= 2;
+    return p;
+}
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
@@ -48,7 +54,9 @@ int check_decode_args(const kvq_decode_args* a, bool need_out) {
     if (a->kv_format != KVQ_KV_F16) {
         if (!a->k_scale || !a->k_zero || !a->v_scale || !a->v_zero) return KVQ_ERR_FORMAT;
         if (a->head_dim != 128) return KVQ_ERR_UNSUPPORTED;
-        if (a->k_group < a->block_size || a->k_group % a->block_size != 0)
+        // a K group spans at most the decode kernel's 64-page block-table window
+        if (a->k_group < a->block_size || a->k_group % a->block_size != 0 ||
+            !is_pow2(a->k_group) || a->k_group / a->block_size > 64)
             return KVQ_ERR_UNSUPPORTED;
         if (!aligned16(a->k_scale) || !aligned16(a->k_zero) || !aligned16(a->v_scale) ||
             !aligned16(a->v_zero))
@@ -105,6 +113,7 @@ kvq::DecodeParams make_params(const kvq_decode_args* a) {
     p.num_blocks = a->num_blocks;
     p.cpp_shift = ilog2(a->block_size / 16);
     p.k_group_chunks = a->kv_format == KVQ_KV_F16 ? 0 : a->k_group / 16;
+    p.k_group_shift = a->kv_format == KVQ_KV_F16 ? 0 : ilog2(a->k_group / 16);
     p.k_group_pages = a->kv_format == KVQ_KV_F16 ? 0 : a->k_group / a->block_size;
     p.scale_log2 = a->scale * 1.4426950408889634f;
     return p;
@@ -112,11 +121,12 @@ kvq::DecodeParams make_params(const kvq_decode_args* a) {
 
 int64_t lds_bytes(const kvq_decode_args* a, int waves) {
     const int group = a->q_heads / a->kv_heads;
-    return int64_t(4) * (int64_t(waves) * group * a->head_dim + 32 * waves);
+    const int64_t stage = a->kv_format == KVQ_KV_F16 ? 0 : 128 * int64_t(waves);
+    return int64_t(4) * (int64_t(waves) * group * a->head_dim + 32 * waves + stage);
 }
 
 // Waves per workgroup: the caller's choice if given, else as many as give each wave at
-// least 8 chunks of the split (at most 16), within the LDS budget of the cross-wave
+// least 8 chunks of the split (at most 8), within the LDS budget of the cross-wave
 // combine. Returns 0 when the caller's choice is invalid.
 int pick_waves(const kvq_decode_args* a, int pages_per_split) {
     if (a->waves_per_group != 0) {
@@ -124,16 +134,20 @@ int pick_waves(const kvq_decode_args* a, int pages_per_split) {
         if (w != 1 && w != 2 && w != 4 && w != 8 && w != 16) return 0;
         return lds_bytes(a, w) <= kLdsBudget ? w : 0;
     }
+    // At most 8 waves: 16-wave workgroups need 4 waves per SIMD, which caps the kernels
+    // at 128 VGPRs and makes them spill.
     const int64_t chunks = int64_t(pages_per_split) * (a->block_size / 16);
-    int w = 16;
+    int w = 8;
     while (w > 1 && chunks < 8 * w) w >>= 1;
     while (w > 1 && lds_bytes(a, w) > kLdsBudget) w >>= 1;
     return w;
 }
 
-// Pipeline depth: the caller's choice if given (1 or 2), else 1. Returns 0 when invalid.
+// Pipeline depth of the fp16 kernel: the caller's choice if given (1 or 2), else 2 up to
+// head_dim 128 (a second chunk in registers still fits without spilling) and 1 above.
+// Returns 0 when invalid.
 int pick_pipeline(const kvq_decode_args* a) {
-    if (a->pipeline == 0) return 1;
+    if (a->pipeline == 0) return a->head_dim <= 128 ? 2 : 1;
     return (a->pipeline == 1 || a->pipeline == 2) ? a->pipeline : 0;
 }
 
@@ -223,6 +237,28 @@ int kvq_choose_num_splits(int32_t batch, int32_t kv_heads, int32_t block_size,
     if (cap < 1) cap = 1;
     const int64_t s = p2 < cap ? p2 : cap;
     return int(s < 1 ? 1 : s);
+}
+
+int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t max_pages,
+                    int32_t kv_format, int32_t cu_count, int32_t* splits_out,
+                    int32_t* waves_out) {
+    if (!splits_out || !waves_out) return KVQ_ERR_NULL_POINTER;
+    if (batch < 1 || kv_heads < 1 || max_pages < 1 || cu_count < 1) return KVQ_ERR_SHAPE;
+    if (!is_pow2(block_size) || block_size < 16) return KVQ_ERR_SHAPE;
+    if (kv_format < KVQ_KV_F16 || kv_format > KVQ_KV_INT4) return KVQ_ERR_FORMAT;
+    const bool quant = kv_format != KVQ_KV_F16;
+    const int64_t chunks = int64_t(max_pages) * (block_size / 16);
+    const int64_t waves_per_cu = quant ? 8 : 4;
+    const int64_t chunks_per_wave = quant ? 64 : 256;
+    int64_t per_pair = pow2_floor(waves_per_cu * cu_count / (int64_t(batch) * kv_heads));
+    const int64_t balance = pow2_floor(cdiv(chunks, chunks_per_wave));
+    if (per_pair < balance) per_pair = balance;
+    const int64_t cap = pow2_floor(chunks / 4);
+    if (per_pair > cap) per_pair = cap;
+    const int64_t waves = per_pair < 4 ? per_pair : 4;
+    *waves_out = int32_t(waves);
+    *splits_out = int32_t(per_pair / waves);
+    return KVQ_OK;
 }
 
 int kvq_normalize_splits(int32_t num_splits, int32_t max_pages, int32_t* splits_out,

@@ -194,69 +194,51 @@ void decode_f16_kernel(const DecodeParams p) {
                                split, b);
 }
 
-// Stage 2: one workgroup of 4 waves per (q head, sequence). Wave w folds splits
-// w, w+4, ... with its own running max; lanes cover D/64 consecutive columns each; the
-// four waves are combined through LDS.
+// Stage 2 (reference _merge_kernel, triton_fp16.py:147-163): one workgroup of 256 threads
+// per (q head, sequence) = 8 groups of 32 threads; a thread owns D/32 consecutive columns
+// and its group folds splits g, g+8, ... First the global max of lse (every thread scans
+// all splits: S floats, cache-resident), so the weighted sum needs no rescaling and its
+// loads are independent; then the 8 groups are summed through LDS.
 template <int D>
 __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ o_part,
                                                     const float* __restrict__ lse,
                                                     _Float16* __restrict__ out, int64_t o_sb,
                                                     int64_t o_sh, int q_heads, int S) {
-    constexpr int PER = D >= 64 ? D / 64 : 1;
+    constexpr int PER = D / 32;  // columns per thread (1..8)
     const int hq = blockIdx.x, b = blockIdx.y;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int t = threadIdx.x, lane32 = t & 31, grp = t >> 5;
     const int64_t row0 = ((int64_t)b * q_heads + hq) * S;
-    const int d0 = lane * PER;
-    const bool col_ok = d0 < D;
-
+    const float* L = lse + row0;
     float M = -INFINITY;
-    for (int s = wave; s < S; s += 4) M = fmaxf(M, lse[row0 + s]);
+    for (int s = 0; s < S; ++s) M = fmaxf(M, L[s]);
     float wsum = 0.f;
     float acc[PER];
 #pragma unroll
     for (int e = 0; e < PER; ++e) acc[e] = 0.f;
     if (M > -INFINITY) {
 #pragma unroll 4
-        for (int s = wave; s < S; s += 4) {
-            const float w = fast_exp2((lse[row0 + s] - M) * kLog2e);
+        for (int s = grp; s < S; s += 8) {
+            const float w = fast_exp2((L[s] - M) * kLog2e);
+            const float* src = o_part + (row0 + s) * D + lane32 * PER;
             wsum += w;
-            if (col_ok) {
-                const float* src = o_part + (row0 + s) * D + d0;
 #pragma unroll
-                for (int e = 0; e < PER; ++e) acc[e] += w * src[e];
-            }
+            for (int e = 0; e < PER; ++e) acc[e] += w * src[e];
         }
     }
-    __shared__ float sm_m[4], sm_w[4];
-    __shared__ float sm_acc[4][D];
-    if (lane == 0) {
-        sm_m[wave] = M;
-        sm_w[wave] = wsum;
-    }
-    if (col_ok) {
+    __shared__ float sm_acc[8][D];
+    __shared__ float sm_w[8];
 #pragma unroll
-        for (int e = 0; e < PER; ++e) sm_acc[wave][d0 + e] = acc[e];
-    }
+    for (int e = 0; e < PER; ++e) sm_acc[grp][lane32 * PER + e] = acc[e];
+    if (lane32 == 0) sm_w[grp] = wsum;
     __syncthreads();
-    if (wave == 0 && col_ok) {
-        float Mx = fmaxf(fmaxf(sm_m[0], sm_m[1]), fmaxf(sm_m[2], sm_m[3]));
-        float W = 0.f;
-        float o[PER];
+    for (int d = t; d < D; d += 256) {
+        float o = 0.f, W = 0.f;
 #pragma unroll
-        for (int e = 0; e < PER; ++e) o[e] = 0.f;
-        if (Mx > -INFINITY) {
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const float f = fast_exp2((sm_m[w] - Mx) * kLog2e);
-                W += f * sm_w[w];
-#pragma unroll
-                for (int e = 0; e < PER; ++e) o[e] += f * sm_acc[w][d0 + e];
-            }
+        for (int g = 0; g < 8; ++g) {
+            o += sm_acc[g][d];
+            W += sm_w[g];
         }
-        _Float16* dst = out + (int64_t)b * o_sb + (int64_t)hq * o_sh + d0;
-#pragma unroll
-        for (int e = 0; e < PER; ++e) dst[e] = (_Float16)(W > 0.f ? o[e] / W : 0.f);
+        out[(int64_t)b * o_sb + (int64_t)hq * o_sh + d] = (_Float16)(W > 0.f ? o / W : 0.f);
     }
 }
 

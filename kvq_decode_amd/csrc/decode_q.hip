@@ -9,7 +9,7 @@
 //   code c -> fp16 h exactly, with c = F * (h - B):
 //     INT8  h = 1024 + c  (v_perm with 0x64 bytes; F = 1, B = 1024)
 //     INT4  h = 1 + c/64  (nibble into mantissa bits 4-7 of 1.0; F = 64, B = 1)
-//     FP8   h = f(c)/256  (e4m3 sign/exponent/mantissa re-based into fp16; F = 256, B = 0)
+//     FP8   h = f(c)      (v_cvt_scalef32_pk_f16_fp8, exact; F = 1, B = 0)
 //   K (x = c * s_d + z_d, per channel d):
 //     q.k = sum_d q'_d c_d + sum_d q_d z_d,  q' = q * s = hi + lo (two fp16 parts,
 //           recomputed per K group)
@@ -45,20 +45,31 @@ constexpr uint32_t kNib = 0x00F000F0u;
 __device__ __forceinline__ uint32_t i8_lo(uint32_t x) { return perm(kMagicI8, x, 0x04010400u); }
 __device__ __forceinline__ uint32_t i8_hi(uint32_t x) { return perm(kMagicI8, x, 0x04030402u); }
 
-// e4m3fn bytes placed at bits 8-15 / 24-31 (sign at 15 / 31) -> fp16 f(c) / 256:
-// sign stays, exponent+mantissa (7 bits) move to fp16 bits 7-13.
-__device__ __forceinline__ uint32_t f8_fix(uint32_t y) {
-    return (y & 0x80008000u) | ((y >> 1) & 0x3F803F80u);
+// The nibble mask and the 1.0 pattern, held in registers the compiler cannot see through,
+// so (x & mask) | magic becomes one v_and_or_b32 (VOP3 takes no literal constants here)
+// instead of a v_and_b32 + v_or_b32 pair with literals.
+struct I4Consts {
+    uint32_t nib, magic;
+};
+
+__device__ __forceinline__ I4Consts i4_consts() {
+    I4Consts c{kNib, kMagicI4};
+    asm volatile("" : "+v"(c.nib), "+v"(c.magic));
+    return c;
+}
+
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
+    return (x & m) | o;
 }
 
 // Nibbles of one dword (byte j = codes 2j (low), 2j+1 (high)) -> 8 halves 1 + c/64 in the
 // order codes {0,4, 1,5, 2,6, 3,7}.
-__device__ __forceinline__ u4v i4_dword(uint32_t x) {
+__device__ __forceinline__ u4v i4_dword(uint32_t x, I4Consts k) {
     u4v r;
-    r[0] = ((x << 4) & kNib) | kMagicI4;
-    r[1] = (x & kNib) | kMagicI4;
-    r[2] = ((x >> 4) & kNib) | kMagicI4;
-    r[3] = ((x >> 8) & kNib) | kMagicI4;
+    r[0] = and_or(x << 4, k.nib, k.magic);
+    r[1] = and_or(x, k.nib, k.magic);
+    r[2] = and_or(x >> 4, k.nib, k.magic);
+    r[3] = and_or(x >> 8, k.nib, k.magic);
     return r;
 }
 
@@ -74,7 +85,7 @@ struct QFmt<KVQ_KV_INT8> {
     static constexpr int KLOADS = 2, VBYTES = 8;
     __device__ static int chan_base(int st, int g) { return 64 * (st >> 1) + 16 * g + 8 * (st & 1); }
     static constexpr bool permuted() { return false; }
-    __device__ static h8 kop(const u4v* kr, int st) {
+    __device__ static h8 kop(const u4v* kr, int st, I4Consts) {
         const u4v x = kr[st >> 1];
         const uint32_t d0 = x[2 * (st & 1)], d1 = x[2 * (st & 1) + 1];
         u4v o;
@@ -94,27 +105,37 @@ struct QFmt<KVQ_KV_INT8> {
     }
 };
 
+// FP8: gfx950 converts OCP e4m3fn to fp16 exactly in hardware (two codes per
+// v_cvt_scalef32_pk_f16_fp8, scale 1.0), so h = f(c) with F = 1, B = 0.
+__device__ __forceinline__ uint32_t f8_lo(uint32_t x) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 1.0f, false));
+}
+__device__ __forceinline__ uint32_t f8_hi(uint32_t x) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 1.0f, true));
+}
+
 template <>
 struct QFmt<KVQ_KV_FP8_E4M3> {
-    static constexpr float F = 256.f, B = 0.f;
+    static constexpr float F = 1.f, B = 0.f;
     static constexpr int KLOADS = 2, VBYTES = 8;
     __device__ static int chan_base(int st, int g) { return 64 * (st >> 1) + 16 * g + 8 * (st & 1); }
     static constexpr bool permuted() { return false; }
-    __device__ static h8 kop(const u4v* kr, int st) {
+    __device__ static h8 kop(const u4v* kr, int st, I4Consts) {
         const u4v x = kr[st >> 1];
         const uint32_t d0 = x[2 * (st & 1)], d1 = x[2 * (st & 1) + 1];
         u4v o;
-        o[0] = f8_fix(perm(0u, d0, 0x010C000Cu));
-        o[1] = f8_fix(perm(0u, d0, 0x030C020Cu));
-        o[2] = f8_fix(perm(0u, d1, 0x010C000Cu));
-        o[3] = f8_fix(perm(0u, d1, 0x030C020Cu));
+        o[0] = f8_lo(d0);
+        o[1] = f8_hi(d0);
+        o[2] = f8_lo(d1);
+        o[3] = f8_hi(d1);
         return __builtin_bit_cast(h8, o);
     }
     __device__ static void vpair(uint32_t a, uint32_t b, uint32_t* out4) {
-        out4[0] = f8_fix(perm(b, a, 0x040C000Cu));
-        out4[1] = f8_fix(perm(b, a, 0x050C010Cu));
-        out4[2] = f8_fix(perm(b, a, 0x060C020Cu));
-        out4[3] = f8_fix(perm(b, a, 0x070C030Cu));
+        const uint32_t y0 = perm(b, a, 0x05010400u), y1 = perm(b, a, 0x07030602u);
+        out4[0] = f8_lo(y0);
+        out4[1] = f8_hi(y0);
+        out4[2] = f8_lo(y1);
+        out4[3] = f8_hi(y1);
     }
 };
 
@@ -127,36 +148,39 @@ struct QFmt<KVQ_KV_INT4> {
     static constexpr int KLOADS = 1, VBYTES = 4;
     __device__ static int chan_base(int st, int g) { return 32 * g + 8 * st; }
     static constexpr bool permuted() { return true; }
-    __device__ static h8 kop(const u4v* kr, int st) {
-        return __builtin_bit_cast(h8, i4_dword(kr[0][st]));
+    __device__ static h8 kop(const u4v* kr, int st, I4Consts k) {
+        return __builtin_bit_cast(h8, i4_dword(kr[0][st], k));
     }
     // Tiles 0..3 (channels 0..3 of the lane's 8) or 4..7 of token pair (ra, rb) from the
     // dwords a, b holding each token's 8 codes.
-    __device__ static void vpair_half(uint32_t a, uint32_t b, uint32_t sel, uint32_t* out4) {
+    __device__ static void vpair_half(uint32_t a, uint32_t b, uint32_t sel, uint32_t* out4,
+                                      I4Consts k) {
         const uint32_t y = perm(b, a, sel);  // low 16 bits: ra's 4 codes, high: rb's
-        out4[0] = ((y << 4) & kNib) | kMagicI4;
-        out4[1] = (y & kNib) | kMagicI4;
-        out4[2] = ((y >> 4) & kNib) | kMagicI4;
-        out4[3] = ((y >> 8) & kNib) | kMagicI4;
+        out4[0] = and_or(y << 4, k.nib, k.magic);
+        out4[1] = and_or(y, k.nib, k.magic);
+        out4[2] = and_or(y >> 4, k.nib, k.magic);
+        out4[3] = and_or(y >> 8, k.nib, k.magic);
     }
 };
 
-// Raw codes of one 16-token chunk as held by one lane, plus the 4 tokens' V scale/zero.
+// Raw codes of one 16-token chunk as held by one lane, the 4 tokens' V scale/zero, and
+// (lane l) channels 2l, 2l+1 of the scale/zero of the chunk's K group. The group data is
+// loaded with every chunk, not only with a group's first one: loads issued on every path
+// keep the compiler's wait counts exact, so no chunk waits for loads it does not use.
 template <int FMT>
 struct ChunkQ {
     u4v k[QFmt<FMT>::KLOADS];
     uint32_t v[4][QFmt<FMT>::VBYTES / 4];
     h4 vs, vz;
+    uint32_t ks2, kz2;
 };
 
 template <int FMT>
-__device__ __forceinline__ void load_chunk_q(const DecodeParams& p, int b, int kvh, int c,
-                                             int valid, int i16, int g, int n_pages,
-                                             PageWindow& win, ChunkQ<FMT>& ch) {
+__device__ __forceinline__ void load_chunk_q(const DecodeParams& p, int kvh, int c, int valid,
+                                             int i16, int g, int phys, int lead,
+                                             ChunkQ<FMT>& ch) {
     typedef QFmt<FMT> Q;
-    const int page = c >> p.cpp_shift;
-    const int slot = (c - (page << p.cpp_shift)) << 4;
-    const int phys = window_phys(p, b, page, n_pages, win);
+    const int slot = (c & ((1 << p.cpp_shift) - 1)) << 4;
     const char* kb = (const char*)p.k + (int64_t)phys * p.k_sblk + (int64_t)slot * p.k_stok +
                      (int64_t)kvh * p.k_sh;
     const char* vb = (const char*)p.v + (int64_t)phys * p.v_sblk + (int64_t)slot * p.v_stok +
@@ -181,82 +205,87 @@ __device__ __forceinline__ void load_chunk_q(const DecodeParams& p, int b, int k
     const int64_t vsz = ((int64_t)phys * p.kv_heads + kvh) * p.block_size + slot + 4 * g;
     ch.vs = *(const h4*)(p.v_scale + vsz);
     ch.vz = *(const h4*)(p.v_zero + vsz);
+    // K group scale/zero, stored with the group's first page `lead`
+    const int64_t krow = ((int64_t)lead * p.kv_heads + kvh) * 128 + 2 * __lane_id();
+    ch.ks2 = *(const uint32_t*)(p.k_scale + krow);
+    ch.kz2 = *(const uint32_t*)(p.k_zero + krow);
 }
 
-// Per-wave state of the quantized kernel beyond the softmax state: the q' operand of the
-// current K group and its MFMA accumulator input.
-struct KGroupState {
-    int group;     // K scale group the operands belong to (-1 = none yet)
-    float cinit;   // sum_d q z / F - B * sum_d q' of this lane's head column
-};
-
-// q' = q * s in fp16 would lose 2^-12 relative per channel - enough to move logits by
-// ~1e-3 on outlier channels - so q' is kept as an unevaluated sum hi + lo of two fp16
-// operands (hi = fp16(q s), lo = fp16(q s - hi); q s is exact in fp32), and the QK^T
-// MFMA chain runs once per part. C uses the same hi + lo sums.
+// q' = q * s would lose 2^-12 relative per channel in fp16 - enough to move logits by
+// ~1e-3 on outlier channels - so it is kept as hi + lo: hi = fp16(q s) (v_pk_mul_f16),
+// lo = fma(q, s, -hi) rounded once (v_pk_fma_f16: q s - hi is exact), and the QK^T
+// MFMA chain runs once per part. C = sum q z / F - B * sum (hi + lo) (v_dot2_f32_f16).
+// The group's scales (lane l holds channels 2l, 2l+1) pass through the wave's 512-byte
+// LDS slot `stage` to reach every lane in k-operand order.
 template <int FMT>
-__device__ __forceinline__ void load_kgroup(const DecodeParams& p, int b, int kvh, int grp,
-                                            int g, const h8* qop, h8* qhi, h8* qlo,
-                                            KGroupState& ks) {
+__device__ __forceinline__ float make_qprime(uint32_t s2, uint32_t z2, uint32_t* stage, int g,
+                                             const h8* qop, h8* qhi, h8* qlo) {
     typedef QFmt<FMT> Q;
-    const int lead_page = grp * p.k_group_pages;
-    int phys = p.bt[(int64_t)b * p.bt_sb + lead_page];
-    phys = min(max(phys, 0), p.num_blocks - 1);
-    const int64_t row = ((int64_t)phys * p.kv_heads + kvh) * 128;
+    const int lane = __lane_id();
+    stage[lane] = s2;
+    stage[64 + lane] = z2;
+    const _Float16* ss = (const _Float16*)stage;
+    const _Float16* zz = (const _Float16*)(stage + 64);
     float qz = 0.f, qs = 0.f;
+    const h2 one = {(_Float16)1.f, (_Float16)1.f};
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
-        h8 s = *(const h8*)(p.k_scale + row + Q::chan_base(st, g));
-        h8 z = *(const h8*)(p.k_zero + row + Q::chan_base(st, g));
+        h8 sv = *(const h8*)(ss + Q::chan_base(st, g));
+        h8 zv = *(const h8*)(zz + Q::chan_base(st, g));
         if constexpr (Q::permuted()) {
-            s = __builtin_shufflevector(s, s, 0, 4, 1, 5, 2, 6, 3, 7);
-            z = __builtin_shufflevector(z, z, 0, 4, 1, 5, 2, 6, 3, 7);
+            sv = __builtin_shufflevector(sv, sv, 0, 4, 1, 5, 2, 6, 3, 7);
+            zv = __builtin_shufflevector(zv, zv, 0, 4, 1, 5, 2, 6, 3, 7);
         }
+        const h8 hi = qop[st] * sv;
+        const h8 lo = __builtin_elementwise_fma(qop[st], sv, -hi);
+        qhi[st] = hi;
+        qlo[st] = lo;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float qe = (float)qop[st][e];
-            const float prod = qe * (float)s[e];  // exact: 11-bit x 11-bit mantissas
-            const _Float16 hi = (_Float16)prod;
-            const _Float16 lo = (_Float16)(prod - (float)hi);
-            qhi[st][e] = hi;
-            qlo[st][e] = lo;
-            qz += qe * (float)z[e];
-            qs += (float)hi + (float)lo;
+        for (int e = 0; e < 8; e += 2) {
+            const h2 qa = {qop[st][e], qop[st][e + 1]};
+            const h2 za = {zv[e], zv[e + 1]};
+            const h2 ha = {hi[e], hi[e + 1]};
+            const h2 la = {lo[e], lo[e + 1]};
+            qz = __builtin_amdgcn_fdot2(qa, za, qz, false);
+            qs = __builtin_amdgcn_fdot2(ha, one, qs, false);
+            qs = __builtin_amdgcn_fdot2(la, one, qs, false);
         }
     }
     qz = rows_sum(qz);
     qs = rows_sum(qs);
-    ks.cinit = qz * (1.f / Q::F) - Q::B * qs;
-    ks.group = grp;
+    return qz * (1.f / Q::F) - Q::B * qs;
 }
 
 template <int FMT, bool MASK>
 __device__ __forceinline__ void chunk_q(const ChunkQ<FMT>& ch, const h8* qhi, const h8* qlo,
                                         float cinit, float sl2f, int valid, int g,
-                                        SoftmaxState<128>& st, float& corr) {
+                                        SoftmaxState<128>& st, float& corr, I4Consts k4) {
     typedef QFmt<FMT> Q;
-    f4 s = (f4)cinit;
+    // hi and lo parts in two independent MFMA chains (half the dependent-chain latency)
+    f4 sh = (f4)cinit, sl = (f4)0.f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const h8 kh = Q::kop(ch.k, k);
-        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qhi[k], s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qlo[k], s, 0, 0, 0);
+        const h8 kh = Q::kop(ch.k, k, k4);
+        sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qhi[k], sh, 0, 0, 0);
+        sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qlo[k], sl, 0, 0, 0);
     }
     float s2[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) s2[r] = s[r] * sl2f;
+    for (int r = 0; r < 4; ++r) s2[r] = (sh[r] + sl[r]) * sl2f;
     if (MASK) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) s2[r] = 4 * g + r < valid ? s2[r] : -INFINITY;
     }
     const float lm = fmaxf(fmaxf(s2[0], s2[1]), fmaxf(s2[2], s2[3]));
-    float alpha = 1.f;
-    if (__builtin_amdgcn_ballot_w64(lm > st.m + kLazyMax) != 0) {
+    if (__builtin_amdgcn_ballot_w64(lm > st.m + kLazyMax) != 0) {  // rare: the max moved
         const float mn = fmaxf(st.m, rows_max(lm));
-        alpha = fast_exp2(st.m - mn);
+        const float alpha = fast_exp2(st.m - mn);
         st.m = mn;
+        st.l *= alpha;
+        corr *= alpha;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) st.acc[t] *= alpha;
     }
-    st.l *= alpha;
     float pr[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(s2[r] - st.m);
@@ -270,16 +299,17 @@ __device__ __forceinline__ void chunk_q(const ChunkQ<FMT>& ch, const h8* qhi, co
         const _Float16 pp = ok ? (_Float16)(pr[r] * (float)ch.vs[r]) : (_Float16)0.f;
         pop[r] = pp;
         const float zt = ok ? (float)ch.vz[r] : 0.f;
-        cadd += pr[r] * zt - (Q::F * Q::B) * (float)pp;
+        if constexpr (Q::B != 0.f) cadd += pr[r] * zt - (Q::F * Q::B) * (float)pp;
+        else cadd += pr[r] * zt;
     }
-    corr = corr * alpha + cadd;
+    corr += cadd;
     // V^T operands: tiles t of token pairs (0,1) and (2,3).
     uint32_t a01[8], a23[8];
     if constexpr (FMT == KVQ_KV_INT4) {
-        QFmt<KVQ_KV_INT4>::vpair_half(ch.v[0][0], ch.v[1][0], 0x05040100u, a01);
-        QFmt<KVQ_KV_INT4>::vpair_half(ch.v[0][0], ch.v[1][0], 0x07060302u, a01 + 4);
-        QFmt<KVQ_KV_INT4>::vpair_half(ch.v[2][0], ch.v[3][0], 0x05040100u, a23);
-        QFmt<KVQ_KV_INT4>::vpair_half(ch.v[2][0], ch.v[3][0], 0x07060302u, a23 + 4);
+        QFmt<KVQ_KV_INT4>::vpair_half(ch.v[0][0], ch.v[1][0], 0x05040100u, a01, k4);
+        QFmt<KVQ_KV_INT4>::vpair_half(ch.v[0][0], ch.v[1][0], 0x07060302u, a01 + 4, k4);
+        QFmt<KVQ_KV_INT4>::vpair_half(ch.v[2][0], ch.v[3][0], 0x05040100u, a23, k4);
+        QFmt<KVQ_KV_INT4>::vpair_half(ch.v[2][0], ch.v[3][0], 0x07060302u, a23 + 4, k4);
     } else {
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
@@ -291,12 +321,14 @@ __device__ __forceinline__ void chunk_q(const ChunkQ<FMT>& ch, const h8* qhi, co
     for (int t = 0; t < 8; ++t) {
         u2 w = {a01[t], a23[t]};
         const h4 a = __builtin_bit_cast(h4, w);
-        st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pop, st.acc[t] * alpha, 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
+        st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pop, st.acc[t], 0, 0, 0);
     }
 }
 
-template <int FMT, int W, bool FINAL>
+// P-deep register ring: chunk c + P is loaded while chunk c computes, the block-table
+// entries of chunks c + 2P .. c + 3P - 1 meanwhile (requires k_group >= 16 * P tokens, so
+// a ring step never starts two K groups; smaller groups use P = 1).
+template <int FMT, int W, bool FINAL, int P>
 __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) {
     typedef QFmt<FMT> Q;
     constexpr int D = 128, DV = 8;
@@ -307,7 +339,9 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
     const int G = p.group;
     const bool head_ok = i16 < G;
     const WaveRange wr = wave_range<W>(p, b, split, wave);
-    const int seq_len = wr.seq_len, n_pages = wr.n_pages, w_lo = wr.w_lo, w_hi = wr.w_hi;
+    const int seq_len = wr.seq_len, w_lo = wr.w_lo, w_hi = wr.w_hi;
+    const int kgs = p.k_group_shift;  // log2 of 16-token chunks per K group
+    const I4Consts k4 = i4_consts();
 
     // q in this format's k-operand order (zero for padded heads).
     h8 qop[4];
@@ -327,23 +361,61 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
     for (int t = 0; t < DV; ++t) st.acc[t] = (f4)0.f;
     st.m = -INFINITY;
     st.l = 0.f;
-    float corr = 0.f;
+    float corr = 0.f, cinit = 0.f;
     const float sl2f = p.scale_log2 * Q::F;
-    KGroupState ks;
-    ks.group = -1;
-    ks.cinit = 0.f;
     h8 qhi[4], qlo[4];
 
-    PageWindow win;
-    window_load(p, b, w_lo >> p.cpp_shift, n_pages, win);
-    for (int c = w_lo; c < w_hi; ++c) {
-        const int grp = c / p.k_group_chunks;
-        if (grp != ks.group) load_kgroup<FMT>(p, b, kvh, grp, g, qop, qhi, qlo, ks);
-        const int valid = min(seq_len - (c << 4), 16);
+    auto valid_of = [&](int c) { return min(seq_len - (c << 4), 16); };
+
+    extern __shared__ float smem[];
+    uint32_t* stage = (uint32_t*)(smem + W * G * D + 2 * W * 16) + wave * 128;
+    // The ring covers the wave's fully valid chunks [w_lo, r_hi); the sequence's partial
+    // last chunk (at most one per sequence) is handled once after it. Every load in the
+    // ring is issued on every path (chunks past r_hi - 1 re-read chunk r_hi - 1 and are
+    // never used), so each wait counts exactly the loads still in flight behind it.
+    const int r_hi = min(w_hi, wr.c_full);
+    const int gmask = (1 << kgs) - 1;
+    if (w_lo < r_hi) {
+        const int last = r_hi - 1;
+        ChunkQ<FMT> ring[P];
+        int pg_cur = chunk_pages<P>(p, b, w_lo, last, kgs);
+        int pg_nxt = chunk_pages<P>(p, b, w_lo + P, last, kgs);
+        // Issued slot by slot: a slot's loads moved behind a later slot's would make the
+        // ring's waits (vmcnt counts the loads issued after the awaited one) drain it.
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            load_chunk_q<FMT>(p, kvh, min(w_lo + i, last), 16, i16, g,
+                              __builtin_amdgcn_readlane(pg_cur, i),
+                              __builtin_amdgcn_readlane(pg_cur, P + i), ring[i]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        for (int c0 = w_lo; c0 < r_hi; c0 += P) {
+            pg_cur = pg_nxt;  // pages of chunks c0 + P .. c0 + 2P - 1
+            pg_nxt = chunk_pages<P>(p, b, c0 + 2 * P, last, kgs);
+#pragma unroll
+            for (int i = 0; i < P; ++i) {
+                const int c = c0 + i;
+                if (c < r_hi) {
+                    if (c == w_lo || (c & gmask) == 0)
+                        cinit = make_qprime<FMT>(ring[i].ks2, ring[i].kz2, stage, g, qop, qhi, qlo);
+                    chunk_q<FMT, false>(ring[i], qhi, qlo, cinit, sl2f, 16, g, st, corr, k4);
+                }
+                load_chunk_q<FMT>(p, kvh, min(c + P, last), 16, i16, g,
+                                  __builtin_amdgcn_readlane(pg_cur, i),
+                                  __builtin_amdgcn_readlane(pg_cur, P + i), ring[i]);
+            }
+        }
+    }
+    if (w_lo <= r_hi && r_hi < w_hi) {  // this wave owns the partial last chunk c_full
+        const int c = r_hi;
+        const int valid = valid_of(c);
+        const int pg = chunk_pages<1>(p, b, c, c, kgs);
         ChunkQ<FMT> ch;
-        load_chunk_q<FMT>(p, b, kvh, c, valid, i16, g, n_pages, win, ch);
-        if (valid == 16) chunk_q<FMT, false>(ch, qhi, qlo, ks.cinit, sl2f, 16, g, st, corr);
-        else chunk_q<FMT, true>(ch, qhi, qlo, ks.cinit, sl2f, valid, g, st, corr);
+        load_chunk_q<FMT>(p, kvh, c, valid, i16, g, __builtin_amdgcn_readlane(pg, 0),
+                          __builtin_amdgcn_readlane(pg, 1), ch);
+        if (c == w_lo || (c & gmask) == 0)
+            cinit = make_qprime<FMT>(ch.ks2, ch.kz2, stage, g, qop, qhi, qlo);
+        chunk_q<FMT, true>(ch, qhi, qlo, cinit, sl2f, valid, g, st, corr, k4);
     }
 
     combine_store<D, W, FINAL>(p, st.acc, Q::F, rows_sum(corr), st.m, rows_sum(st.l), wave, i16,
@@ -353,8 +425,12 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
 template <int FMT, int W, bool FINAL>
 static hipError_t launch_q(const DecodeParams& p, hipStream_t stream) {
     const dim3 grid(p.kv_heads, FINAL ? 1 : p.num_splits, p.batch);
-    const size_t shmem = sizeof(float) * (W * p.group * 128 + 2 * W * 16);
-    hipLaunchKernelGGL((decode_q_kernel<FMT, W, FINAL>), grid, dim3(W * 64), shmem, stream, p);
+    // cross-wave combine ([W][G][128] + [W][16] m, l) then one 512-byte K-scale slot per wave
+    const size_t shmem = sizeof(float) * (W * p.group * 128 + 2 * W * 16 + W * 128);
+    if (p.k_group_shift >= 2)
+        hipLaunchKernelGGL((decode_q_kernel<FMT, W, FINAL, 4>), grid, dim3(W * 64), shmem, stream, p);
+    else
+        hipLaunchKernelGGL((decode_q_kernel<FMT, W, FINAL, 1>), grid, dim3(W * 64), shmem, stream, p);
     return hipGetLastError();
 }
 
@@ -365,7 +441,6 @@ static hipError_t launch_q_w(const DecodeParams& p, int waves, hipStream_t strea
         case 2: return launch_q<FMT, 2, FINAL>(p, stream);
         case 4: return launch_q<FMT, 4, FINAL>(p, stream);
         case 8: return launch_q<FMT, 8, FINAL>(p, stream);
-        case 16: return launch_q<FMT, 16, FINAL>(p, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -32,6 +32,7 @@ struct DecodeParams {
     int32_t batch, q_heads, kv_heads, group, block_size, max_blocks, num_blocks;
     int32_t cpp_shift;       // log2(block_size / 16): 16-token chunks per page
     int32_t k_group_chunks;  // 16-token chunks per K scale group (quantized formats)
+    int32_t k_group_shift;   // log2(k_group_chunks)
     int32_t k_group_pages;   // pages per K scale group
     int32_t num_splits, pages_per_split;
     float scale_log2;        // softmax scale * log2(e)

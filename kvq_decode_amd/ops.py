@@ -58,6 +58,28 @@ def choose_num_splits(batch: int, kv_heads: int, block_size: int, max_pages: int
     return _lib.check("kvq_choose_num_splits", s)
 
 
+def plan_decode(batch: int, kv_heads: int, block_size: int, max_pages: int,
+                cu_count: int, kv_format: str = "fp16") -> Tuple[int, int]:
+    """(num_splits, waves_per_group) for the MI355X kernels when num_splits is None: the
+    split-KV decomposition the reference's heuristic aims at (triton_fp16.py:175-180:
+    enough programs to fill the GPU, no tiny splits), counted in waves because one
+    workgroup here holds several waves that combine through LDS. Computed by the library
+    (kvq_plan_decode): about 4 waves per CU for fp16 and 8 for quantized caches, at most
+    256 (fp16) / 64 (quantized) 16-token chunks per wave, 4 waves per workgroup."""
+    _require(kv_format in KV_FORMATS, f"kv_format must be one of {tuple(KV_FORMATS)}")
+    s, w = ctypes.c_int32(), ctypes.c_int32()
+    _lib.check("kvq_plan_decode",
+               _lib.lib().kvq_plan_decode(batch, kv_heads, block_size, max_pages,
+                                          KV_FORMATS[kv_format], cu_count, ctypes.byref(s),
+                                          ctypes.byref(w)))
+    return s.value, w.value
+
+
+def auto_splits(batch: int, kv_heads: int, block_size: int, max_pages: int,
+                cu_count: int, kv_format: str = "fp16") -> int:
+    return plan_decode(batch, kv_heads, block_size, max_pages, cu_count, kv_format)[0]
+
+
 def normalize_splits(num_splits: int, max_pages: int) -> Tuple[int, int]:
     """(splits, pages_per_split) after the reference's clamp/re-derivation
     (triton_fp16.py:211-217)."""
@@ -141,7 +163,9 @@ def paged_decode_attention(
     int32 (every entry >= 1). num_splits: None = heuristic, 1 = single pass, n = split
     each sequence n ways. Returns [B, Hq, D] fp16 (written into `out` when given).
     `workspace` = (o_part, lse) float32 buffers of at least the shapes
-    `workspace_shapes(B, Hq, D, S)` for the normalized split count S."""
+    `workspace_shapes(B, Hq, D, S)` for the normalized split count S. With
+    num_splits=None the split count and workgroup size come from `plan_decode`
+    (`choose_num_splits` keeps the reference's formula for callers that want it)."""
     _require(kv_format in KV_FORMATS, f"unknown kv_format {kv_format!r}")
     B, Hq, D = q.shape
     _, block_size, Hkv, Dc = k_cache.shape
@@ -192,8 +216,13 @@ def paged_decode_attention(
                  "out must be float16 [B, Hq, D] with a contiguous last dim")
 
     max_pages = block_table.shape[1]
-    splits = (num_splits if num_splits is not None else
-              choose_num_splits(B, Hkv, block_size, max_pages, _sm_count(dev.index or 0)))
+    if num_splits is None:
+        splits, planned_waves = plan_decode(B, Hkv, block_size, max_pages,
+                                            _sm_count(dev.index or 0), kv_format)
+        if waves_per_group == 0:
+            waves_per_group = planned_waves
+    else:
+        splits = num_splits
     splits, pps = normalize_splits(splits, max_pages)
     args = build_args(q, k_cache, v_cache, block_table, seq_lens, out, scale, kv_format,
                       k_scale, k_zero, v_scale, v_zero, k_group, waves_per_group, pipeline)

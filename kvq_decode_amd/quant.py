@@ -6,6 +6,9 @@ model (src/bpt/roofline.py:6-9) fixes the scheme: asymmetric fp16 scale + zero, 
 channel over groups of `k_group` tokens, values per token. Storage (include/kvq.h):
     k_codes, v_codes  uint8 [num_blocks, block_size, Hkv, D]   (int8 / fp8_e4m3 bits)
                       uint8 [num_blocks, block_size, Hkv, D/2] (int4, low nibble = even channel)
+                      stored head-major (strides of [num_blocks, Hkv, block_size, Dc]), so
+                      the codes of one (block, kv head) are one contiguous run; any strides
+                      with 16-byte aligned rows are accepted
     k_scale, k_zero   fp16 [num_blocks, Hkv, D]  - group g of sequence b lives in block
                       block_table[b, g * k_group // block_size]
     v_scale, v_zero   fp16 [num_blocks, Hkv, block_size]
@@ -41,12 +44,17 @@ class QuantizedKVCache(NamedTuple):
 def allocate_quantized_cache(num_blocks: int, block_size: int, kv_heads: int, head_dim: int,
                              kv_format: str, device, k_group: int = DEFAULT_K_GROUP
                              ) -> QuantizedKVCache:
-    """Uninitialized code and scale tensors for a quantized paged cache."""
+    """Uninitialized code and scale tensors for a quantized paged cache.
+
+    The code tensors are [num_blocks, block_size, Hkv, Dc] views of head-major storage: a
+    decode workgroup reads one kv head, and an int4 token row of one head is 64 bytes, half
+    an HBM cache line - token-major storage would fetch every line twice, once for each
+    of the two heads sharing it, from workgroups on different XCDs."""
     _require(kv_format in QUANT_FORMATS, f"kv_format must be one of {QUANT_FORMATS}")
     dc = head_dim // 2 if kv_format == "int4" else head_dim
-    shape = (num_blocks, block_size, kv_heads, dc)
-    kc = torch.empty(shape, dtype=torch.uint8, device=device)
-    vc = torch.empty(shape, dtype=torch.uint8, device=device)
+    shape = (num_blocks, kv_heads, block_size, dc)
+    kc = torch.empty(shape, dtype=torch.uint8, device=device).permute(0, 2, 1, 3)
+    vc = torch.empty(shape, dtype=torch.uint8, device=device).permute(0, 2, 1, 3)
     ks = torch.empty((num_blocks, kv_heads, head_dim), dtype=torch.float16, device=device)
     vs = torch.empty((num_blocks, kv_heads, block_size), dtype=torch.float16, device=device)
     return QuantizedKVCache(kc, vc, ks, torch.empty_like(ks), vs, torch.empty_like(vs),

@@ -69,6 +69,34 @@ def test_choose_num_splits_known_answers():
         assert got == r["auto_splits"], r
 
 
+def test_plan_decode():
+    """The MI355X planner's choices for the benchmark shapes (256 CUs, 8 kv heads, block
+    16), its caps, and its argument errors."""
+    from kvq_decode_amd.ops import plan_decode
+    cases = [  # batch, max_pages, format -> (splits, waves)
+        (8, 2048, "fp16", (4, 4)),      # 4 waves/CU: 16 per (sequence, kv head)
+        (16, 2048, "fp16", (2, 4)),
+        (1, 8192, "fp16", (32, 4)),     # 128 per pair
+        (16, 2048, "int4", (8, 4)),     # <= 64 chunks per wave for quantized
+        (64, 2048, "int8", (8, 4)),
+        (64, 64, "fp16", (1, 2)),       # 2 per pair from 4 waves/CU
+        (2, 3, "fp16", (1, 1)),         # at least 4 chunks per wave
+    ]
+    for batch, pages, fmt, want in cases:
+        assert plan_decode(batch, 8, 16, pages, 256, fmt) == want, (batch, pages, fmt)
+    assert plan_decode(1, 8, 32, 4096, 256, "fp16") == (32, 4)  # 2 chunks per page
+    L = _lib.lib()
+    s, w = ctypes.c_int32(), ctypes.c_int32()
+    assert L.kvq_plan_decode(0, 8, 16, 64, 0, 256, ctypes.byref(s), ctypes.byref(w)) == \
+        _lib.KVQ_ERR_SHAPE
+    assert L.kvq_plan_decode(1, 8, 16, 64, 7, 256, ctypes.byref(s), ctypes.byref(w)) == \
+        _lib.KVQ_ERR_FORMAT
+    assert L.kvq_plan_decode(1, 8, 24, 64, 0, 256, ctypes.byref(s), ctypes.byref(w)) == \
+        _lib.KVQ_ERR_SHAPE
+    assert L.kvq_plan_decode(1, 8, 16, 64, 0, 256, None, ctypes.byref(w)) == \
+        _lib.KVQ_ERR_NULL_POINTER
+
+
 def test_normalize_splits():
     L = _lib.lib()
     s, pps = ctypes.c_int32(), ctypes.c_int32()

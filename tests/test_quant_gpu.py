@@ -123,6 +123,35 @@ def test_decode_group8_and_mqa_heads(fmt):
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
+def test_code_layout_does_not_change_results(fmt):
+    """The quantizer allocates head-major code storage; decode reads codes through their
+    strides, so the same codes stored token-major (the fp16 cache's layout) and written
+    by the quantizer into a token-major cache give bit-identical outputs."""
+    from kvq_decode_amd import paged_decode_attention
+    from kvq_decode_amd.quant import QuantizedKVCache, quantize_paged_cache
+    q, kc, vc, bt, sl = make([1, 37, 300, 2049], 16, seed=4)
+    qc = quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt)
+    assert not qc.k_codes.is_contiguous()
+    tm = qc._replace(k_codes=qc.k_codes.contiguous(), v_codes=qc.v_codes.contiguous())
+    assert tm.k_codes.stride(1) > tm.k_codes.stride(2)
+    for splits in (1, None):
+        a = paged_decode_attention(gpu(q), qc.k_codes, qc.v_codes, gpu(bt), gpu(sl),
+                                   num_splits=splits, **qc.decode_kwargs())
+        b = paged_decode_attention(gpu(q), tm.k_codes, tm.v_codes, gpu(bt), gpu(sl),
+                                   num_splits=splits, **tm.decode_kwargs())
+        assert torch.equal(a, b)
+    # the quantizer writes through the destination's strides too
+    dst = QuantizedKVCache(torch.zeros_like(tm.k_codes), torch.zeros_like(tm.v_codes),
+                           *[torch.zeros_like(t) for t in qc[2:6]], fmt, qc.k_group)
+    quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt, out=dst)
+    slots = valid_slots(bt, sl, 16)
+    for name in ("k_codes", "v_codes"):
+        g = getattr(dst, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
+        w = getattr(qc, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
+        assert np.array_equal(g, w), name
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
 def test_append_equals_bulk(fmt):
     """Bulk-quantize a prefix, then append tokens one by one across group boundaries; the
     cache must equal the bulk quantization of all tokens, bit for bit, and decode on it
