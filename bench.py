@@ -234,6 +234,108 @@ def read_traffic(workload, splits):
         return None
 
 
+COPY_ELEMS = 1 << 28  # calibration copy: 2^28 int32 read, 2^28 float32 written (1 GiB each)
+
+
+def calibrate_copy(reps=3):
+    """The plain copy of known size that scales rocprofv3's FETCH_SIZE / WRITE_SIZE to
+    bytes: an int32 -> float32 conversion copy of COPY_ELEMS elements, reps times. Run it
+    alone under `rocprofv3 --pmc` (the process launches one fill and `reps` copies)."""
+    import torch
+    src = torch.full((COPY_ELEMS,), 7, dtype=torch.int32, device="cuda")
+    dst = torch.empty(COPY_ELEMS, dtype=torch.float32, device="cuda")
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"calibration copy: {reps} x {4 * COPY_ELEMS} bytes read and written")
+
+
+def profile_run(config, steps):
+    """`steps` untimed decode steps of `config` with its default plan, for counter runs."""
+    import torch
+    B, ctx, pool, fmt_name, _ = CONFIGS[config]
+    q, k, v, bt, sl, fmt = make_inputs(B, ctx, pool, kv_format=fmt_name)
+    splits, waves = default_plan(config, B, bt.shape[1])
+    step = Step(q, k, v, bt, sl, splits, waves, 0, fmt)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    log(f"profile run: {config} splits={step.splits} waves={waves} x {steps} steps")
+
+
+def _pmc_means(csv_dir, name_has):
+    """Mean Counter_Value per dispatch over dispatches whose kernel name contains
+    `name_has`, from a rocprofv3 --pmc -f csv output directory."""
+    import csv
+    import glob
+    vals = {}
+    for path in glob.glob(os.path.join(csv_dir, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(path)):
+            if name_has in r["Kernel_Name"]:
+                vals.setdefault(r["Dispatch_Id"], 0.0)
+                vals[r["Dispatch_Id"]] += float(r["Counter_Value"])
+    if not vals:
+        raise SystemExit(f"no dispatch of a kernel containing {name_has!r} under {csv_dir}")
+    return sum(vals.values()) / len(vals), len(vals)
+
+
+def traffic_summary(config, pmc_dir):
+    """Writes profiles/decode_split_<config>_traffic.txt from four rocprofv3 --pmc runs
+    under pmc_dir: copy_fetch/, copy_write/ (calibrate_copy) and fetch/, write/
+    (profile_run). Counter values are scaled by the copy's known bytes per counter unit."""
+    B, ctx, pool, fmt_name, desc = CONFIGS[config]
+    kernel = "decode_f16_kernel" if fmt_name == "fp16" else "decode_q_kernel"
+    cf, _ = _pmc_means(os.path.join(pmc_dir, "copy_fetch"), "copy")
+    cw, _ = _pmc_means(os.path.join(pmc_dir, "copy_write"), "copy")
+    kf, n = _pmc_means(os.path.join(pmc_dir, "fetch"), kernel)
+    kw, _ = _pmc_means(os.path.join(pmc_dir, "write"), kernel)
+    copy_bytes = 4 * COPY_ELEMS
+    rf, wf = copy_bytes / cf, copy_bytes / cw
+    lens = seq_lengths(B, ctx)
+    algo = kv_bytes(lens, fmt_name)
+    from kvq_decode_amd import ops
+    max_pages = max(-(-x // BS) for x in lens)
+    splits, waves = (1, 0) if config == "C1" else ops.plan_decode(B, HKV, BS, max_pages, 256,
+                                                                   fmt_name)
+    splits = ops.normalize_splits(splits, max_pages)[0]
+    rd, wr = kf * rf, kw * wf
+    lines = [
+        f"# HBM traffic of one stage-1 launch ({kernel}), {desc}",
+        "# rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (one counter per run), scaled by the same",
+        "# counters on a plain copy of known size (int32 -> float32, 1 GiB read, 1 GiB written).",
+        "# commands (each counter in its own run; D = an output directory):",
+        "#   rocprofv3 --pmc FETCH_SIZE -d D/copy_fetch -o f -f csv -- python3 bench.py "
+        "--calibrate-copy",
+        "#   rocprofv3 --pmc WRITE_SIZE -d D/copy_write -o w -f csv -- python3 bench.py "
+        "--calibrate-copy",
+        f"#   rocprofv3 --pmc FETCH_SIZE -d D/fetch -o f -f csv -- python3 bench.py --config "
+        f"{config} --profile-run 10",
+        f"#   rocprofv3 --pmc WRITE_SIZE -d D/write -o w -f csv -- python3 bench.py --config "
+        f"{config} --profile-run 10",
+        f"#   python3 bench.py --config {config} --traffic-summary D",
+        f"config = {config}",
+        f"splits = {splits}",
+        f"waves_per_group = {waves}",
+        f"dispatches = {n}",
+        f"fetch_size_per_dispatch = {kf:.1f}",
+        f"write_size_per_dispatch = {kw:.1f}",
+        f"copy_fetch_size = {cf:.1f}",
+        f"copy_write_size = {cw:.1f}",
+        f"fetch_bytes_per_unit = {rf:.2f}",
+        f"write_bytes_per_unit = {wf:.2f}",
+        f"hbm_read_bytes_per_launch = {rd:.0f}",
+        f"hbm_write_bytes_per_launch = {wr:.0f}",
+        f"hbm_bytes_per_launch = {rd + wr:.0f}",
+        f"algorithmic_bytes_per_launch = {algo}",
+        f"traffic_over_algorithmic = {(rd + wr) / algo:.4f}",
+    ]
+    path = os.path.join(REPO, "profiles", f"decode_split_{config}_traffic.txt")
+    with open(path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    log("\n".join(lines))
+    log(f"wrote {path}")
+
+
 def default_plan(config, B, max_pages):
     """(splits, waves) the op would use with num_splits=None (C1: no split, configs[0])."""
     from kvq_decode_amd import _sm_count
@@ -320,12 +422,28 @@ def main():
     ap.add_argument("--sweep-waves", default="1,2,4,8")
     ap.add_argument("--suite", action="store_true",
                     help="every configuration; one JSON line per configuration")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only the copy of known size (run under rocprofv3 --pmc)")
+    ap.add_argument("--profile-run", type=int, default=0, metavar="STEPS",
+                    help="only STEPS untimed steps of --config (run under rocprofv3 --pmc)")
+    ap.add_argument("--traffic-summary", metavar="PMC_DIR",
+                    help="write profiles/decode_split_<config>_traffic.txt from PMC_DIR/"
+                         "{copy_fetch,copy_write,fetch,write}")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); the "
               "multi-GPU sharding of the path is described in DESIGN.md", file=sys.stderr)
         sys.exit(2)
 
+    if args.traffic_summary:
+        traffic_summary(args.config, args.traffic_summary)
+        return
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
+    if args.profile_run:
+        profile_run(args.config, args.profile_run)
+        return
     if args.sweep:
         sweep(args)
         return

@@ -121,7 +121,8 @@ kvq::DecodeParams make_params(const kvq_decode_args* a) {
 
 int64_t lds_bytes(const kvq_decode_args* a, int waves) {
     const int group = a->q_heads / a->kv_heads;
-    const int64_t stage = a->kv_format == KVQ_KV_F16 ? 0 : 128 * int64_t(waves);
+    // quantized: a 512-byte K-scale slot per wave and 4 KB of q in k-operand order
+    const int64_t stage = a->kv_format == KVQ_KV_F16 ? 0 : 128 * int64_t(waves) + 1024;
     return int64_t(4) * (int64_t(waves) * group * a->head_dim + 32 * waves + stage);
 }
 

@@ -100,6 +100,21 @@ __device__ __forceinline__ int chunk_pages(const DecodeParams& p, int b, int c, 
     return min(max(phys, 0), p.num_blocks - 1);
 }
 
+// Buffer resource for raw (untyped) loads at a wave-uniform base: stride 0, no range
+// limit that matters (2^31 bytes), dword data format. Loads through it take a 32-bit lane
+// offset in a VGPR and a wave-uniform offset in an SGPR, so a page's address needs no
+// per-lane 64-bit arithmetic.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const void* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff,
+                                             0x00020000);
+}
+
+// byte offset of physical block `phys` for a block stride below 2^32 bytes (checked on the
+// host): one 32 x 32 -> 64-bit scalar multiply
+__device__ __forceinline__ uint64_t block_offset(int phys, int64_t stride) {
+    return (uint64_t)(uint32_t)phys * (uint32_t)stride;
+}
+
 // Online-softmax state of one wave: running reference max m and partial sum l of its
 // lane (head l%16, tokens 4g..4g+3 of every chunk), and O^T accumulator tiles.
 template <int D>

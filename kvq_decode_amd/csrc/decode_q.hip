@@ -175,40 +175,65 @@ struct ChunkQ {
     uint32_t ks2, kz2;
 };
 
+// Per-lane byte offsets of a chunk's loads inside its page (the page base and the slot
+// are wave-uniform): K row min(l%16, last) bytes [16g, +16) (+64 per further load), V rows
+// min(4g + r, last) bytes [VBYTES * (l%16), +VBYTES), V scales of tokens 4g..4g+3, and
+// channels 2l, 2l+1 of the K group scales. `last` = valid tokens - 1 of the chunk.
+struct QLaneOff {
+    uint32_t k, v[4], vs, ks;
+};
+
 template <int FMT>
-__device__ __forceinline__ void load_chunk_q(const DecodeParams& p, int kvh, int c, int valid,
-                                             int i16, int g, int phys, int lead,
+__device__ __forceinline__ QLaneOff lane_offsets(const DecodeParams& p, int i16, int g,
+                                                 int last) {
+    typedef QFmt<FMT> Q;
+    QLaneOff o;
+    o.k = (uint32_t)(min(i16, last) * (int)p.k_stok + 16 * g);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        o.v[r] = (uint32_t)(min(4 * g + r, last) * (int)p.v_stok + Q::VBYTES * i16);
+    o.vs = 8 * g;
+    o.ks = 4 * __lane_id();
+    return o;
+}
+
+template <int FMT>
+__device__ __forceinline__ void load_chunk_q(const DecodeParams& p, int kvh, int c,
+                                             const QLaneOff& lo, int phys, int lead,
                                              ChunkQ<FMT>& ch) {
     typedef QFmt<FMT> Q;
     const int slot = (c & ((1 << p.cpp_shift) - 1)) << 4;
-    const char* kb = (const char*)p.k + (int64_t)phys * p.k_sblk + (int64_t)slot * p.k_stok +
-                     (int64_t)kvh * p.k_sh;
-    const char* vb = (const char*)p.v + (int64_t)phys * p.v_sblk + (int64_t)slot * p.v_stok +
-                     (int64_t)kvh * p.v_sh;
-    const int last = valid - 1;
-    const uint32_t koff = (uint32_t)(min(i16, last) * (int)p.k_stok + 16 * g);
+    const char* kpage = (const char*)p.k + block_offset(phys, p.k_sblk) + (int64_t)kvh * p.k_sh;
+    const char* vpage = (const char*)p.v + block_offset(phys, p.v_sblk) + (int64_t)kvh * p.v_sh;
+    const auto rk = page_rsrc(kpage), rv = page_rsrc(vpage);
+    const int ks = slot * (int)p.k_stok, vsl = slot * (int)p.v_stok;
 #pragma unroll
-    for (int j = 0; j < Q::KLOADS; ++j) ch.k[j] = *(const u4v*)(kb + koff + 64 * j);
+    for (int j = 0; j < Q::KLOADS; ++j)
+        ch.k[j] = __builtin_amdgcn_raw_buffer_load_b128(rk, lo.k + 64 * j, ks, 0);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        const uint32_t voff = (uint32_t)(min(4 * g + r, last) * (int)p.v_stok + Q::VBYTES * i16);
         if constexpr (Q::VBYTES == 8) {
-            const u2 x = *(const u2*)(vb + voff);
+            const u2 x = __builtin_amdgcn_raw_buffer_load_b64(rv, lo.v[r], vsl, 0);
             ch.v[r][0] = x[0];
             ch.v[r][Q::VBYTES / 4 - 1] = x[1];
         } else {
-            ch.v[r][0] = *(const uint32_t*)(vb + voff);
+            ch.v[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, lo.v[r], vsl, 0);
         }
     }
     // V scale/zero of tokens slot + 4g .. +3 (4 consecutive halves; slots past the
     // sequence hold garbage and are masked in chunk_q).
-    const int64_t vsz = ((int64_t)phys * p.kv_heads + kvh) * p.block_size + slot + 4 * g;
-    ch.vs = *(const h4*)(p.v_scale + vsz);
-    ch.vz = *(const h4*)(p.v_zero + vsz);
+    const uint64_t vrow = ((uint64_t)(uint32_t)phys * (uint32_t)p.kv_heads + kvh) *
+                          (uint32_t)(2 * p.block_size);
+    const auto rvs = page_rsrc((const char*)p.v_scale + vrow);
+    const auto rvz = page_rsrc((const char*)p.v_zero + vrow);
+    ch.vs = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rvs, lo.vs, 2 * slot, 0));
+    ch.vz = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rvz, lo.vs, 2 * slot, 0));
     // K group scale/zero, stored with the group's first page `lead`
-    const int64_t krow = ((int64_t)lead * p.kv_heads + kvh) * 128 + 2 * __lane_id();
-    ch.ks2 = *(const uint32_t*)(p.k_scale + krow);
-    ch.kz2 = *(const uint32_t*)(p.k_zero + krow);
+    const uint64_t krow = ((uint64_t)(uint32_t)lead * (uint32_t)p.kv_heads + kvh) * 256u;
+    const auto rks = page_rsrc((const char*)p.k_scale + krow);
+    const auto rkz = page_rsrc((const char*)p.k_zero + krow);
+    ch.ks2 = __builtin_amdgcn_raw_buffer_load_b32(rks, lo.ks, 0, 0);
+    ch.kz2 = __builtin_amdgcn_raw_buffer_load_b32(rkz, lo.ks, 0, 0);
 }
 
 // q' = q * s would lose 2^-12 relative per channel in fp16 - enough to move logits by
@@ -219,7 +244,7 @@ __device__ __forceinline__ void load_chunk_q(const DecodeParams& p, int kvh, int
 // LDS slot `stage` to reach every lane in k-operand order.
 template <int FMT>
 __device__ __forceinline__ float make_qprime(uint32_t s2, uint32_t z2, uint32_t* stage, int g,
-                                             const h8* qop, h8* qhi, h8* qlo) {
+                                             const h8* qsh, h8* qhi, h8* qlo) {
     typedef QFmt<FMT> Q;
     const int lane = __lane_id();
     stage[lane] = s2;
@@ -236,13 +261,14 @@ __device__ __forceinline__ float make_qprime(uint32_t s2, uint32_t z2, uint32_t*
             sv = __builtin_shufflevector(sv, sv, 0, 4, 1, 5, 2, 6, 3, 7);
             zv = __builtin_shufflevector(zv, zv, 0, 4, 1, 5, 2, 6, 3, 7);
         }
-        const h8 hi = qop[st] * sv;
-        const h8 lo = __builtin_elementwise_fma(qop[st], sv, -hi);
+        const h8 qv = qsh[64 * st];
+        const h8 hi = qv * sv;
+        const h8 lo = __builtin_elementwise_fma(qv, sv, -hi);
         qhi[st] = hi;
         qlo[st] = lo;
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
-            const h2 qa = {qop[st][e], qop[st][e + 1]};
+            const h2 qa = {qv[e], qv[e + 1]};
             const h2 za = {zv[e], zv[e + 1]};
             const h2 ha = {hi[e], hi[e + 1]};
             const h2 la = {lo[e], lo[e + 1]};
@@ -290,17 +316,21 @@ __device__ __forceinline__ void chunk_q(const ChunkQ<FMT>& ch, const h8* qhi, co
 #pragma unroll
     for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(s2[r] - st.m);
     st.l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-    // p'' = fp16(p * s_t) feeds the MFMA; corr accumulates p z - F B p'' in fp32.
+    // p'' = fp16(p * s_t) feeds the MFMA (fma with +0 is the product: p, s >= 0, and it
+    // maps to v_fma_mix_f32 on the fp16 scale); corr accumulates p z (v_fma_mix_f32)
+    // and - F B p'' (exact products, v_dot2_f32_f16 on the p'' pairs) in fp32.
     h4 pop;
     float cadd = 0.f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const bool ok = !MASK || 4 * g + r < valid;
-        const _Float16 pp = ok ? (_Float16)(pr[r] * (float)ch.vs[r]) : (_Float16)0.f;
-        pop[r] = pp;
-        const float zt = ok ? (float)ch.vz[r] : 0.f;
-        if constexpr (Q::B != 0.f) cadd += pr[r] * zt - (Q::F * Q::B) * (float)pp;
-        else cadd += pr[r] * zt;
+        pop[r] = ok ? (_Float16)__builtin_fmaf(pr[r], (float)ch.vs[r], 0.f) : (_Float16)0.f;
+        cadd = __builtin_fmaf(pr[r], ok ? (float)ch.vz[r] : 0.f, cadd);
+    }
+    if constexpr (Q::B != 0.f) {
+        const h2 fb = {(_Float16)(-Q::F * Q::B), (_Float16)(-Q::F * Q::B)};
+        cadd = __builtin_amdgcn_fdot2(__builtin_shufflevector(pop, pop, 0, 1), fb, cadd, false);
+        cadd = __builtin_amdgcn_fdot2(__builtin_shufflevector(pop, pop, 2, 3), fb, cadd, false);
     }
     corr += cadd;
     // V^T operands: tiles t of token pairs (0,1) and (2,3).
@@ -343,18 +373,22 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
     const int kgs = p.k_group_shift;  // log2 of 16-token chunks per K group
     const I4Consts k4 = i4_consts();
 
-    // q in this format's k-operand order (zero for padded heads).
-    h8 qop[4];
-    {
+    // q in this format's k-operand order (zero for padded heads), kept in LDS for the
+    // once-per-K-group q' products: [4 k-steps][64 lanes] h8, written by wave 0.
+    extern __shared__ float smem[];
+    h8* qsh = (h8*)(smem + W * G * D + 2 * W * 16 + W * 128);
+    if (wave == 0) {
         const _Float16* qrow = (const _Float16*)p.q + (int64_t)b * p.q_sb +
                                (int64_t)(kvh * G + (head_ok ? i16 : 0)) * p.q_sh;
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
             h8 x = *(const h8*)(qrow + Q::chan_base(st, g));
             if constexpr (Q::permuted()) x = __builtin_shufflevector(x, x, 0, 4, 1, 5, 2, 6, 3, 7);
-            qop[st] = head_ok ? x : (h8)(_Float16)0;
+            qsh[64 * st + lane] = head_ok ? x : (h8)(_Float16)0;
         }
     }
+    __syncthreads();
+    qsh += lane;
 
     SoftmaxState<D> st;
 #pragma unroll
@@ -367,7 +401,6 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
 
     auto valid_of = [&](int c) { return min(seq_len - (c << 4), 16); };
 
-    extern __shared__ float smem[];
     uint32_t* stage = (uint32_t*)(smem + W * G * D + 2 * W * 16) + wave * 128;
     // The ring covers the wave's fully valid chunks [w_lo, r_hi); the sequence's partial
     // last chunk (at most one per sequence) is handled once after it. Every load in the
@@ -376,6 +409,7 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
     const int r_hi = min(w_hi, wr.c_full);
     const int gmask = (1 << kgs) - 1;
     if (w_lo < r_hi) {
+        const QLaneOff lo = lane_offsets<FMT>(p, i16, g, 15);
         const int last = r_hi - 1;
         ChunkQ<FMT> ring[P];
         int pg_cur = chunk_pages<P>(p, b, w_lo, last, kgs);
@@ -384,7 +418,7 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
         // ring's waits (vmcnt counts the loads issued after the awaited one) drain it.
 #pragma unroll
         for (int i = 0; i < P; ++i) {
-            load_chunk_q<FMT>(p, kvh, min(w_lo + i, last), 16, i16, g,
+            load_chunk_q<FMT>(p, kvh, min(w_lo + i, last), lo,
                               __builtin_amdgcn_readlane(pg_cur, i),
                               __builtin_amdgcn_readlane(pg_cur, P + i), ring[i]);
             __builtin_amdgcn_sched_barrier(0);
@@ -397,10 +431,10 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
                 const int c = c0 + i;
                 if (c < r_hi) {
                     if (c == w_lo || (c & gmask) == 0)
-                        cinit = make_qprime<FMT>(ring[i].ks2, ring[i].kz2, stage, g, qop, qhi, qlo);
+                        cinit = make_qprime<FMT>(ring[i].ks2, ring[i].kz2, stage, g, qsh, qhi, qlo);
                     chunk_q<FMT, false>(ring[i], qhi, qlo, cinit, sl2f, 16, g, st, corr, k4);
                 }
-                load_chunk_q<FMT>(p, kvh, min(c + P, last), 16, i16, g,
+                load_chunk_q<FMT>(p, kvh, min(c + P, last), lo,
                                   __builtin_amdgcn_readlane(pg_cur, i),
                                   __builtin_amdgcn_readlane(pg_cur, P + i), ring[i]);
             }
@@ -411,10 +445,10 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
         const int valid = valid_of(c);
         const int pg = chunk_pages<1>(p, b, c, c, kgs);
         ChunkQ<FMT> ch;
-        load_chunk_q<FMT>(p, kvh, c, valid, i16, g, __builtin_amdgcn_readlane(pg, 0),
-                          __builtin_amdgcn_readlane(pg, 1), ch);
+        load_chunk_q<FMT>(p, kvh, c, lane_offsets<FMT>(p, i16, g, valid - 1),
+                          __builtin_amdgcn_readlane(pg, 0), __builtin_amdgcn_readlane(pg, 1), ch);
         if (c == w_lo || (c & gmask) == 0)
-            cinit = make_qprime<FMT>(ch.ks2, ch.kz2, stage, g, qop, qhi, qlo);
+            cinit = make_qprime<FMT>(ch.ks2, ch.kz2, stage, g, qsh, qhi, qlo);
         chunk_q<FMT, true>(ch, qhi, qlo, cinit, sl2f, valid, g, st, corr, k4);
     }
 
@@ -425,8 +459,9 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
 template <int FMT, int W, bool FINAL>
 static hipError_t launch_q(const DecodeParams& p, hipStream_t stream) {
     const dim3 grid(p.kv_heads, FINAL ? 1 : p.num_splits, p.batch);
-    // cross-wave combine ([W][G][128] + [W][16] m, l) then one 512-byte K-scale slot per wave
-    const size_t shmem = sizeof(float) * (W * p.group * 128 + 2 * W * 16 + W * 128);
+    // cross-wave combine ([W][G][128] + [W][16] m, l), one 512-byte K-scale slot per wave,
+    // then q in k-operand order (4 KB)
+    const size_t shmem = sizeof(float) * (W * p.group * 128 + 2 * W * 16 + W * 128) + 4096;
     if (p.k_group_shift >= 2)
         hipLaunchKernelGGL((decode_q_kernel<FMT, W, FINAL, 4>), grid, dim3(W * 64), shmem, stream, p);
     else
