@@ -389,7 +389,10 @@ def sweep(args):
     nbytes = kv_bytes([int(x) for x in sl.tolist()], fmt_name)
     log(f"{args.config}: B={B} ctx={ctx} {fmt_name} kv={nbytes / 1e9:.3f} GB")
     log(f"{'splits':>6}{'waves':>6}{'pipe':>5}{'step_us':>10}{'stage1_us':>11}{'TB/s':>8}{'%peak':>7}")
-    pipes = (1, 2) if fmt_name == "fp16" else (1,)
+    if args.sweep_pipes:
+        pipes = tuple(int(x) for x in args.sweep_pipes.split(","))
+    else:
+        pipes = (1, 2) if fmt_name == "fp16" else (4,)
     for splits in [int(s) for s in args.sweep_splits.split(",")]:
         for waves in [int(w) for w in args.sweep_waves.split(",")]:
             for pipe in pipes:
@@ -420,6 +423,8 @@ def main():
     ap.add_argument("--sweep", action="store_true", help="split/waves sweep, table on stderr")
     ap.add_argument("--sweep-splits", default="1,2,4,8,16,32,64,128")
     ap.add_argument("--sweep-waves", default="1,2,4,8")
+    ap.add_argument("--sweep-pipes", default=None,
+                    help="chunks in flight per wave (default: 1,2 for fp16, 4 quantized)")
     ap.add_argument("--suite", action="store_true",
                     help="every configuration; one JSON line per configuration")
     ap.add_argument("--calibrate-copy", action="store_true",

@@ -93,9 +93,9 @@ typedef struct kvq_decode_args {
     const void* v_zero;
     int32_t waves_per_group;  /* tuning: waves per (kv head, split) workgroup, one of
                                  1, 2, 4, 8, 16; 0 = the library's choice */
-    int32_t pipeline;         /* tuning: 1 = one chunk of loads per wave at a time (higher
-                                 occupancy), 2 = next chunk's loads in flight during compute;
-                                 0 = the library's choice */
+    int32_t pipeline;         /* tuning: 16-token chunks of loads in flight per wave:
+                                 fp16 1 or 2, quantized 1, 2 or 4 (more chunks in flight,
+                                 fewer waves per SIMD); 0 = the library's choice */
 } kvq_decode_args;
 
 /* Library version string, e.g. "kvq 0.1.0 gfx950". */

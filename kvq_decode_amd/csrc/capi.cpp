@@ -133,6 +133,7 @@ int pick_waves(const kvq_decode_args* a, int pages_per_split) {
     if (a->waves_per_group != 0) {
         const int w = a->waves_per_group;
         if (w != 1 && w != 2 && w != 4 && w != 8 && w != 16) return 0;
+        if (w == 16 && a->kv_format != KVQ_KV_F16) return 0;  // quantized: up to 8
         return lds_bytes(a, w) <= kLdsBudget ? w : 0;
     }
     // At most 8 waves: 16-wave workgroups need 4 waves per SIMD, which caps the kernels
@@ -144,10 +145,16 @@ int pick_waves(const kvq_decode_args* a, int pages_per_split) {
     return w;
 }
 
-// Pipeline depth of the fp16 kernel: the caller's choice if given (1 or 2), else 2 up to
+// Loads in flight per wave, in 16-token chunks. fp16: the caller's 1 or 2, else 2 up to
 // head_dim 128 (a second chunk in registers still fits without spilling) and 1 above.
+// Quantized: the caller's 1, 2 or 4, else 2 for INT4 (1 KB per chunk and wave; the
+// kernel then fits 4 waves per SIMD) and 4 for INT8 / FP8 (2 KB, 2 waves per SIMD).
 // Returns 0 when invalid.
 int pick_pipeline(const kvq_decode_args* a) {
+    if (a->kv_format != KVQ_KV_F16) {
+        if (a->pipeline == 0) return a->kv_format == KVQ_KV_INT4 ? 2 : 4;
+        return (a->pipeline == 1 || a->pipeline == 2 || a->pipeline == 4) ? a->pipeline : 0;
+    }
     if (a->pipeline == 0) return a->head_dim <= 128 ? 2 : 1;
     return (a->pipeline == 1 || a->pipeline == 2) ? a->pipeline : 0;
 }

@@ -276,7 +276,7 @@ static hipError_t launch_f16_d(const DecodeParams& p, bool final_out, int waves,
 hipError_t launch_decode(const DecodeParams& p, int kv_format, int head_dim, bool final_out,
                          int waves, int pipe, hipStream_t stream) {
     if (kv_format != KVQ_KV_F16)
-        return launch_decode_q(p, kv_format, head_dim, final_out, waves, stream);
+        return launch_decode_q(p, kv_format, head_dim, final_out, waves, pipe, stream);
     switch (head_dim) {
         case 32: return launch_f16_d<32>(p, final_out, waves, pipe, stream);
         case 64: return launch_f16_d<64>(p, final_out, waves, pipe, stream);

@@ -236,17 +236,30 @@ __device__ __forceinline__ void load_chunk_q(const DecodeParams& p, int kvh, int
     ch.kz2 = __builtin_amdgcn_raw_buffer_load_b32(rkz, lo.ks, 0, 0);
 }
 
+// Half-row rotation: lane l reads lane (l & ~15) | ((l + 8) & 15), i.e. column n of a
+// 16-lane row meets column n ^ 8 (DPP row_ror:8).
+__device__ __forceinline__ float ror8(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf,
+                                                      false));
+}
+
 // q' = q * s would lose 2^-12 relative per channel in fp16 - enough to move logits by
 // ~1e-3 on outlier channels - so it is kept as hi + lo: hi = fp16(q s) (v_pk_mul_f16),
-// lo = fma(q, s, -hi) rounded once (v_pk_fma_f16: q s - hi is exact), and the QK^T
-// MFMA chain runs once per part. C = sum q z / F - B * sum (hi + lo) (v_dot2_f32_f16).
+// lo = fma(q, s, -hi) rounded once (v_pk_fma_f16: q s - hi is exact).
+// C = sum q z / F - B * sum (hi + lo) (v_dot2_f32_f16).
+// SPLIT (at most 8 heads per kv head): the MFMA's 16 columns hold hi in column h and lo
+// in column h + 8, so one QK^T chain gives both parts (summed across the half rows
+// after the MFMAs); lanes of columns >= 8 take C = 0. Otherwise hi and lo run in two
+// chains over columns [0, G).
 // The group's scales (lane l holds channels 2l, 2l+1) pass through the wave's 512-byte
-// LDS slot `stage` to reach every lane in k-operand order.
-template <int FMT>
+// LDS slot `stage` to reach every lane in k-operand order; `qsh` points at the lane's
+// q in k-operand order (head l % 8 when SPLIT) in LDS, 64 h8 apart per k-step.
+template <int FMT, bool SPLIT>
 __device__ __forceinline__ float make_qprime(uint32_t s2, uint32_t z2, uint32_t* stage, int g,
                                              const h8* qsh, h8* qhi, h8* qlo) {
     typedef QFmt<FMT> Q;
     const int lane = __lane_id();
+    const bool upper = SPLIT && (lane & 8);
     stage[lane] = s2;
     stage[64 + lane] = z2;
     const _Float16* ss = (const _Float16*)stage;
@@ -264,8 +277,12 @@ __device__ __forceinline__ float make_qprime(uint32_t s2, uint32_t z2, uint32_t*
         const h8 qv = qsh[64 * st];
         const h8 hi = qv * sv;
         const h8 lo = __builtin_elementwise_fma(qv, sv, -hi);
-        qhi[st] = hi;
-        qlo[st] = lo;
+        if constexpr (SPLIT) {
+            qhi[st] = upper ? lo : hi;
+        } else {
+            qhi[st] = hi;
+            qlo[st] = lo;
+        }
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
             const h2 qa = {qv[e], qv[e + 1]};
@@ -279,25 +296,36 @@ __device__ __forceinline__ float make_qprime(uint32_t s2, uint32_t z2, uint32_t*
     }
     qz = rows_sum(qz);
     qs = rows_sum(qs);
-    return qz * (1.f / Q::F) - Q::B * qs;
+    return upper ? 0.f : qz * (1.f / Q::F) - Q::B * qs;
 }
 
-template <int FMT, bool MASK>
+template <int FMT, bool MASK, bool SPLIT>
 __device__ __forceinline__ void chunk_q(const ChunkQ<FMT>& ch, const h8* qhi, const h8* qlo,
                                         float cinit, float sl2f, int valid, int g,
                                         SoftmaxState<128>& st, float& corr, I4Consts k4) {
     typedef QFmt<FMT> Q;
-    // hi and lo parts in two independent MFMA chains (half the dependent-chain latency)
-    f4 sh = (f4)cinit, sl = (f4)0.f;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const h8 kh = Q::kop(ch.k, k, k4);
-        sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qhi[k], sh, 0, 0, 0);
-        sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qlo[k], sl, 0, 0, 0);
-    }
     float s2[4];
+    if constexpr (SPLIT) {
+        // one chain; column h + 8 holds the lo part of head h: s = C[h] + C[h + 8] in
+        // both lanes of the pair
+        f4 sc = (f4)cinit;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) s2[r] = (sh[r] + sl[r]) * sl2f;
+        for (int k = 0; k < 4; ++k)
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(Q::kop(ch.k, k, k4), qhi[k], sc, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s2[r] = (sc[r] + ror8(sc[r])) * sl2f;
+    } else {
+        // hi and lo parts in two independent MFMA chains (half the dependent-chain latency)
+        f4 sh = (f4)cinit, sl = (f4)0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const h8 kh = Q::kop(ch.k, k, k4);
+            sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qhi[k], sh, 0, 0, 0);
+            sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qlo[k], sl, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s2[r] = (sh[r] + sl[r]) * sl2f;
+    }
     if (MASK) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) s2[r] = 4 * g + r < valid ? s2[r] : -INFINITY;
@@ -316,21 +344,28 @@ __device__ __forceinline__ void chunk_q(const ChunkQ<FMT>& ch, const h8* qhi, co
 #pragma unroll
     for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(s2[r] - st.m);
     st.l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-    // p'' = fp16(p * s_t) feeds the MFMA (fma with +0 is the product: p, s >= 0, and it
-    // maps to v_fma_mix_f32 on the fp16 scale); corr accumulates p z (v_fma_mix_f32)
-    // and - F B p'' (exact products, v_dot2_f32_f16 on the p'' pairs) in fp32.
-    h4 pop;
+    // p s_t feeds the MFMA as two fp16 parts, hi = fp16(p s_t) (fma with +0 is the
+    // product: p, s >= 0; v_fma_mix_f32 on the fp16 scale) and lo = fp16(p s_t - hi): one
+    // fp16 rounding of p s_t would be an error of up to 2^-11 (V - z) when one token
+    // dominates. corr accumulates p z (v_fma_mix_f32) and -F B (hi + lo) (exact
+    // products, v_dot2_f32_f16) in fp32.
+    h4 phi, plo;
     float cadd = 0.f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const bool ok = !MASK || 4 * g + r < valid;
-        pop[r] = ok ? (_Float16)__builtin_fmaf(pr[r], (float)ch.vs[r], 0.f) : (_Float16)0.f;
+        const float sv = (float)ch.vs[r];
+        const _Float16 hi = (_Float16)__builtin_fmaf(pr[r], sv, 0.f);
+        phi[r] = ok ? hi : (_Float16)0.f;
+        plo[r] = ok ? (_Float16)__builtin_fmaf(pr[r], sv, -(float)hi) : (_Float16)0.f;
         cadd = __builtin_fmaf(pr[r], ok ? (float)ch.vz[r] : 0.f, cadd);
     }
     if constexpr (Q::B != 0.f) {
         const h2 fb = {(_Float16)(-Q::F * Q::B), (_Float16)(-Q::F * Q::B)};
-        cadd = __builtin_amdgcn_fdot2(__builtin_shufflevector(pop, pop, 0, 1), fb, cadd, false);
-        cadd = __builtin_amdgcn_fdot2(__builtin_shufflevector(pop, pop, 2, 3), fb, cadd, false);
+        cadd = __builtin_amdgcn_fdot2(__builtin_shufflevector(phi, phi, 0, 1), fb, cadd, false);
+        cadd = __builtin_amdgcn_fdot2(__builtin_shufflevector(phi, phi, 2, 3), fb, cadd, false);
+        cadd = __builtin_amdgcn_fdot2(__builtin_shufflevector(plo, plo, 0, 1), fb, cadd, false);
+        cadd = __builtin_amdgcn_fdot2(__builtin_shufflevector(plo, plo, 2, 3), fb, cadd, false);
     }
     corr += cadd;
     // V^T operands: tiles t of token pairs (0,1) and (2,3).
@@ -347,18 +382,35 @@ __device__ __forceinline__ void chunk_q(const ChunkQ<FMT>& ch, const h8* qhi, co
             Q::vpair(ch.v[2][k], ch.v[3][k], a23 + 4 * k);
         }
     }
+    if constexpr (SPLIT) {
+        // column h takes p hi, column h + 8 p lo (the lanes of a pair hold the same p)
+        const h4 pop = (__lane_id() & 8) ? plo : phi;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        u2 w = {a01[t], a23[t]};
-        const h4 a = __builtin_bit_cast(h4, w);
-        st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pop, st.acc[t], 0, 0, 0);
+        for (int t = 0; t < 8; ++t) {
+            u2 w = {a01[t], a23[t]};
+            const h4 a = __builtin_bit_cast(h4, w);
+            st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pop, st.acc[t], 0, 0, 0);
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            u2 w = {a01[t], a23[t]};
+            const h4 a = __builtin_bit_cast(h4, w);
+            st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, phi, st.acc[t], 0, 0, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            u2 w = {a01[t], a23[t]};
+            const h4 a = __builtin_bit_cast(h4, w);
+            st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, plo, st.acc[t], 0, 0, 0);
+        }
     }
 }
 
 // P-deep register ring: chunk c + P is loaded while chunk c computes, the block-table
-// entries of chunks c + 2P .. c + 3P - 1 meanwhile (requires k_group >= 16 * P tokens, so
-// a ring step never starts two K groups; smaller groups use P = 1).
-template <int FMT, int W, bool FINAL, int P>
+// entries of chunks c + 2P .. c + 3P - 1 meanwhile. Every chunk carries its own K group's
+// scales, so any group size works with any P.
+template <int FMT, int W, bool FINAL, int P, bool SPLIT>
 __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) {
     typedef QFmt<FMT> Q;
     constexpr int D = 128, DV = 8;
@@ -388,7 +440,7 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
         }
     }
     __syncthreads();
-    qsh += lane;
+    qsh += SPLIT ? (lane & ~8) : lane;  // SPLIT: columns h and h + 8 read head h
 
     SoftmaxState<D> st;
 #pragma unroll
@@ -397,7 +449,7 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
     st.l = 0.f;
     float corr = 0.f, cinit = 0.f;
     const float sl2f = p.scale_log2 * Q::F;
-    h8 qhi[4], qlo[4];
+    h8 qhi[4], qlo[SPLIT ? 1 : 4];
 
     auto valid_of = [&](int c) { return min(seq_len - (c << 4), 16); };
 
@@ -431,8 +483,8 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
                 const int c = c0 + i;
                 if (c < r_hi) {
                     if (c == w_lo || (c & gmask) == 0)
-                        cinit = make_qprime<FMT>(ring[i].ks2, ring[i].kz2, stage, g, qsh, qhi, qlo);
-                    chunk_q<FMT, false>(ring[i], qhi, qlo, cinit, sl2f, 16, g, st, corr, k4);
+                        cinit = make_qprime<FMT, SPLIT>(ring[i].ks2, ring[i].kz2, stage, g, qsh, qhi, qlo);
+                    chunk_q<FMT, false, SPLIT>(ring[i], qhi, qlo, cinit, sl2f, 16, g, st, corr, k4);
                 }
                 load_chunk_q<FMT>(p, kvh, min(c + P, last), lo,
                                   __builtin_amdgcn_readlane(pg_cur, i),
@@ -448,52 +500,78 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
         load_chunk_q<FMT>(p, kvh, c, lane_offsets<FMT>(p, i16, g, valid - 1),
                           __builtin_amdgcn_readlane(pg, 0), __builtin_amdgcn_readlane(pg, 1), ch);
         if (c == w_lo || (c & gmask) == 0)
-            cinit = make_qprime<FMT>(ch.ks2, ch.kz2, stage, g, qsh, qhi, qlo);
-        chunk_q<FMT, true>(ch, qhi, qlo, cinit, sl2f, valid, g, st, corr, k4);
+            cinit = make_qprime<FMT, SPLIT>(ch.ks2, ch.kz2, stage, g, qsh, qhi, qlo);
+        chunk_q<FMT, true, SPLIT>(ch, qhi, qlo, cinit, sl2f, valid, g, st, corr, k4);
     }
 
+    if constexpr (SPLIT) {  // add the lo columns into the hi columns
+#pragma unroll
+        for (int t = 0; t < DV; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) st.acc[t][r] += ror8(st.acc[t][r]);
+    }
     combine_store<D, W, FINAL>(p, st.acc, Q::F, rows_sum(corr), st.m, rows_sum(st.l), wave, i16,
                                g, kvh, split, b);
 }
 
-template <int FMT, int W, bool FINAL>
+template <int FMT, int W, bool FINAL, int P, bool SPLIT>
 static hipError_t launch_q(const DecodeParams& p, hipStream_t stream) {
     const dim3 grid(p.kv_heads, FINAL ? 1 : p.num_splits, p.batch);
     // cross-wave combine ([W][G][128] + [W][16] m, l), one 512-byte K-scale slot per wave,
     // then q in k-operand order (4 KB)
     const size_t shmem = sizeof(float) * (W * p.group * 128 + 2 * W * 16 + W * 128) + 4096;
-    if (p.k_group_shift >= 2)
-        hipLaunchKernelGGL((decode_q_kernel<FMT, W, FINAL, 4>), grid, dim3(W * 64), shmem, stream, p);
-    else
-        hipLaunchKernelGGL((decode_q_kernel<FMT, W, FINAL, 1>), grid, dim3(W * 64), shmem, stream, p);
+    hipLaunchKernelGGL((decode_q_kernel<FMT, W, FINAL, P, SPLIT>), grid, dim3(W * 64), shmem,
+                       stream, p);
     return hipGetLastError();
 }
 
-template <int FMT, bool FINAL>
+// Up to 8 heads per kv head: hi / lo parts in the two column halves of one MFMA chain,
+// any ring depth. 9 to 16 heads: two chains, ring depth 4.
+template <int FMT, bool FINAL, int P>
 static hipError_t launch_q_w(const DecodeParams& p, int waves, hipStream_t stream) {
+    if (p.group > 8) {
+        switch (waves) {
+            case 1: return launch_q<FMT, 1, FINAL, 4, false>(p, stream);
+            case 2: return launch_q<FMT, 2, FINAL, 4, false>(p, stream);
+            case 4: return launch_q<FMT, 4, FINAL, 4, false>(p, stream);
+            case 8: return launch_q<FMT, 8, FINAL, 4, false>(p, stream);
+            default: return hipErrorInvalidValue;
+        }
+    }
     switch (waves) {
-        case 1: return launch_q<FMT, 1, FINAL>(p, stream);
-        case 2: return launch_q<FMT, 2, FINAL>(p, stream);
-        case 4: return launch_q<FMT, 4, FINAL>(p, stream);
-        case 8: return launch_q<FMT, 8, FINAL>(p, stream);
+        case 1: return launch_q<FMT, 1, FINAL, P, true>(p, stream);
+        case 2: return launch_q<FMT, 2, FINAL, P, true>(p, stream);
+        case 4: return launch_q<FMT, 4, FINAL, P, true>(p, stream);
+        case 8: return launch_q<FMT, 8, FINAL, P, true>(p, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <int FMT, bool FINAL>
+static hipError_t launch_q_p(const DecodeParams& p, int waves, int ring, hipStream_t stream) {
+    switch (ring) {
+        case 1: return launch_q_w<FMT, FINAL, 1>(p, waves, stream);
+        case 2: return launch_q_w<FMT, FINAL, 2>(p, waves, stream);
+        case 4: return launch_q_w<FMT, FINAL, 4>(p, waves, stream);
         default: return hipErrorInvalidValue;
     }
 }
 
 template <int FMT>
-static hipError_t launch_q_f(const DecodeParams& p, bool final_out, int waves,
+static hipError_t launch_q_f(const DecodeParams& p, bool final_out, int waves, int ring,
                              hipStream_t stream) {
-    return final_out ? launch_q_w<FMT, true>(p, waves, stream)
-                     : launch_q_w<FMT, false>(p, waves, stream);
+    return final_out ? launch_q_p<FMT, true>(p, waves, ring, stream)
+                     : launch_q_p<FMT, false>(p, waves, ring, stream);
 }
 
 hipError_t launch_decode_q(const DecodeParams& p, int kv_format, int head_dim, bool final_out,
-                           int waves, hipStream_t stream) {
+                           int waves, int ring, hipStream_t stream) {
     if (head_dim != 128) return hipErrorInvalidValue;
     switch (kv_format) {
-        case KVQ_KV_INT8: return launch_q_f<KVQ_KV_INT8>(p, final_out, waves, stream);
-        case KVQ_KV_FP8_E4M3: return launch_q_f<KVQ_KV_FP8_E4M3>(p, final_out, waves, stream);
-        case KVQ_KV_INT4: return launch_q_f<KVQ_KV_INT4>(p, final_out, waves, stream);
+        case KVQ_KV_INT8: return launch_q_f<KVQ_KV_INT8>(p, final_out, waves, ring, stream);
+        case KVQ_KV_FP8_E4M3:
+            return launch_q_f<KVQ_KV_FP8_E4M3>(p, final_out, waves, ring, stream);
+        case KVQ_KV_INT4: return launch_q_f<KVQ_KV_INT4>(p, final_out, waves, ring, stream);
         default: return hipErrorInvalidValue;
     }
 }

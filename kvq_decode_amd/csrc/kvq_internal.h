@@ -44,8 +44,9 @@ hipError_t launch_decode(const DecodeParams& p, int kv_format, int head_dim, boo
                          int waves_per_group, int pipeline, hipStream_t stream);
 
 // Quantized formats (decode_q.hip); head_dim 128 only.
+// `ring` = chunks of loads in flight per wave: 1, 2 or 4.
 hipError_t launch_decode_q(const DecodeParams& p, int kv_format, int head_dim, bool final_out,
-                           int waves_per_group, hipStream_t stream);
+                           int waves_per_group, int ring, hipStream_t stream);
 
 hipError_t launch_merge(const float* o_part, const float* lse, void* out, int64_t o_sb,
                         int64_t o_sh, int batch, int q_heads, int head_dim, int num_splits,

@@ -151,6 +151,17 @@ def test_single_pass_rejects(field, value, status):
     assert _lib.lib().kvq_decode_single(ctypes.byref(a), None) == status
 
 
+def test_quantized_tuning_limits():
+    """Quantized kernels: up to 8 waves per workgroup and 1, 2 or 4 chunks in flight."""
+    L = _lib.lib()
+    for field, value in (("waves_per_group", 16), ("pipeline", 3), ("pipeline", 8)):
+        a = good_args()
+        a.kv_format = 3
+        a.k_scale = a.k_zero = a.v_scale = a.v_zero = 1 << 43
+        setattr(a, field, value)
+        assert L.kvq_decode_single(ctypes.byref(a), None) == _lib.KVQ_ERR_UNSUPPORTED, field
+
+
 def test_split_rejects_bad_split_geometry():
     L = _lib.lib()
     a = good_args()

@@ -106,10 +106,11 @@ def test_decode_matches_fp32_attention_over_dequantized_cache(fmt, bs, num_split
 
 @pytest.mark.parametrize("fmt", FORMATS)
 def test_decode_group8_and_mqa_heads(fmt):
-    """Other GQA groups over a quantized cache: 8 q heads per kv head, and MQA."""
+    """Other GQA groups over a quantized cache: 8 q heads per kv head, MQA, and 16 q heads
+    per kv head (past 8 the kernel runs its two-chain variant)."""
     from kvq_decode_amd import paged_decode_attention
     from kvq_decode_amd.quant import quantize_paged_cache
-    for Hq, Hkv in ((16, 2), (8, 1)):
+    for Hq, Hkv in ((16, 2), (8, 1), (32, 2)):
         q, kc, vc, bt, sl = make([700, 3], 16, Hq=Hq, Hkv=Hkv, seed=2)
         qc = quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt)
         host = {n: getattr(qc, n).cpu().numpy() for n in
@@ -149,6 +150,59 @@ def test_code_layout_does_not_change_results(fmt):
         g = getattr(dst, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
         w = getattr(qc, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
         assert np.array_equal(g, w), name
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_ring_depths_and_workgroup_shapes(fmt):
+    """Every (waves per workgroup, loads in flight) variant is within tolerance, and the
+    ring depth never changes a result bit (same arithmetic in the same order)."""
+    from kvq_decode_amd import paged_decode_attention
+    from kvq_decode_amd.quant import quantize_paged_cache
+    q, kc, vc, bt, sl = make([1, 129, 300, 2049, 700], 16, seed=5)
+    qc = quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt)
+    host = {n: getattr(qc, n).cpu().numpy() for n in
+            ("k_codes", "v_codes", "k_scale", "k_zero", "v_scale", "v_zero")}
+    kd, vd = kivi.dequantize_paged_cache(host, bt, sl, fmt)
+    ref = paged_decode_attention_ref(q.astype(np.float32), kd, vd, bt, sl, out_dtype=np.float32)
+    for splits in (1, 3):
+        by_ring = {}
+        for waves in (1, 2, 4, 8):
+            for ring in (1, 2, 4):
+                out = paged_decode_attention(gpu(q), qc.k_codes, qc.v_codes, gpu(bt), gpu(sl),
+                                             num_splits=splits, waves_per_group=waves,
+                                             pipeline=ring, **qc.decode_kwargs())
+                check_close(out, ref, f"{fmt} splits={splits} waves={waves} ring={ring}")
+                by_ring.setdefault(waves, []).append(out)
+        for waves, outs in by_ring.items():
+            assert all(torch.equal(outs[0], o) for o in outs[1:]), (fmt, splits, waves)
+
+
+@pytest.mark.parametrize("k_group", [16, 32, 64, 256])
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_other_k_group_sizes(fmt, k_group):
+    """K scale groups of 1, 2, 4 and 16 chunks (the default 128 tokens is 8): quantizer
+    bit-exact and decode within tolerance, for every ring depth."""
+    from kvq_decode_amd import paged_decode_attention
+    from kvq_decode_amd.quant import quantize_paged_cache
+    q, kc, vc, bt, sl = make([5, 300, 1000], 16, seed=6)
+    qc = quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt, k_group=k_group)
+    want = kivi.quantize_paged_cache(kc, vc, bt, sl, fmt, group=k_group)
+    slots = valid_slots(bt, sl, 16)
+    for name in ("k_codes", "v_codes"):
+        g = getattr(qc, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
+        assert np.array_equal(g, want[name][slots[:, 0], slots[:, 1]]), name
+    lead = lead_blocks(bt, sl, 16, k_group)
+    for name in ("k_scale", "k_zero"):
+        g = getattr(qc, name).cpu().numpy()[lead].view(np.uint16)
+        assert np.array_equal(g, want[name][lead].view(np.uint16)), name
+    host = {n: getattr(qc, n).cpu().numpy() for n in
+            ("k_codes", "v_codes", "k_scale", "k_zero", "v_scale", "v_zero")}
+    kd, vd = kivi.dequantize_paged_cache(host, bt, sl, fmt, group=k_group)
+    ref = paged_decode_attention_ref(q.astype(np.float32), kd, vd, bt, sl, out_dtype=np.float32)
+    for ring in (1, 2, 4):
+        out = paged_decode_attention(gpu(q), qc.k_codes, qc.v_codes, gpu(bt), gpu(sl),
+                                     num_splits=2, pipeline=ring, **qc.decode_kwargs())
+        check_close(out, ref, f"{fmt} k_group={k_group} ring={ring}")
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
