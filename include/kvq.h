@@ -116,12 +116,15 @@ int kvq_choose_num_splits(int32_t batch, int32_t kv_heads, int32_t block_size,
 /* MI355X work plan used when the caller gives no split count; takes the place of the
  * heuristic above (triton_fp16.py:175-180) on this hardware. It sizes the decomposition
  * in waves, because a workgroup here holds several waves that combine through LDS:
- *   per_pair = pow2_floor(T * cu_count / (batch * kv_heads)), T = 4 waves per CU (fp16)
- *              or 8 (quantized), raised to pow2_floor(cdiv(chunks, C)) (C = 256 chunks per wave
+ *   per_pair = pow2_floor(T * cu_count / (batch * kv_heads)), T = 2 waves per CU (fp16)
+ *              or 8 (quantized), raised to pow2_floor(cdiv(chunks, C)) (C = 512 chunks per wave
  *              for fp16, 64 for quantized; uneven sequence lengths then still balance),
  *              capped at pow2_floor(chunks / 4); chunks = max_pages * block_size / 16
- *   waves = min(4, per_pair), splits = per_pair / waves
- * Measured optimum on MI355X for batch 1..64 and 32k..128k contexts. Writes both outputs
+ *   waves = min(Wmax, per_pair) with Wmax = 2 (fp16) or 4 (quantized),
+ *   splits = per_pair / waves
+ * fp16 streams fastest with about 2 waves per CU, each 2 chunks (16 KB) ahead, spread
+ * over at least one workgroup per CU; more waves in flight lower the achieved bandwidth
+ * (measured on MI355X for batch 1..16 and 32k..128k contexts). Writes both outputs
  * (splits before kvq_normalize_splits); returns KVQ_OK or an error. */
 int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t max_pages,
                     int32_t kv_format, int32_t cu_count, int32_t* splits_out,

@@ -73,6 +73,12 @@ int check_decode_args(const kvq_decode_args* a, bool need_out) {
         return KVQ_ERR_ALIGNMENT;
     if (a->v_stride_blk % vec || a->v_stride_tok % vec || a->v_stride_head % vec)
         return KVQ_ERR_ALIGNMENT;
+    // Block offsets are 32 x 32 -> 64-bit products of the block index and the block
+    // stride in bytes, which must therefore stay below 2^32.
+    const int64_t esz = a->kv_format == KVQ_KV_F16 ? 2 : 1;
+    if (a->k_stride_blk < 0 || a->v_stride_blk < 0 ||
+        a->k_stride_blk * esz >= (int64_t(1) << 32) || a->v_stride_blk * esz >= (int64_t(1) << 32))
+        return KVQ_ERR_UNSUPPORTED;
     // Lane offsets inside a 16-token chunk are 32-bit byte offsets.
     const int64_t lim = int64_t(1) << 30;
     if (a->k_stride_tok < 0 || a->v_stride_tok < 0 || 16 * a->k_stride_tok + a->head_dim > lim ||
@@ -121,9 +127,15 @@ kvq::DecodeParams make_params(const kvq_decode_args* a) {
 
 int64_t lds_bytes(const kvq_decode_args* a, int waves) {
     const int group = a->q_heads / a->kv_heads;
-    // quantized: a 512-byte K-scale slot per wave and 4 KB of q in k-operand order
-    const int64_t stage = a->kv_format == KVQ_KV_F16 ? 0 : 128 * int64_t(waves) + 1024;
-    return int64_t(4) * (int64_t(waves) * group * a->head_dim + 32 * waves + stage);
+    const int64_t combine = int64_t(4) * (int64_t(waves) * group * a->head_dim + 32 * waves);
+    // fp16: the waves' K staging tiles (16 rows of head_dim halves each), which the
+    // combine reuses; quantized: a 512-byte K-scale slot per wave and 4 KB of q in
+    // k-operand order after the combine's region
+    if (a->kv_format == KVQ_KV_F16) {
+        const int64_t stage = int64_t(waves) * 32 * a->head_dim;
+        return combine > stage ? combine : stage;
+    }
+    return combine + int64_t(4) * (128 * int64_t(waves) + 1024);
 }
 
 // Waves per workgroup: the caller's choice if given, else as many as give each wave at
@@ -145,18 +157,21 @@ int pick_waves(const kvq_decode_args* a, int pages_per_split) {
     return w;
 }
 
-// Loads in flight per wave, in 16-token chunks. fp16: the caller's 1 or 2, else 2 up to
-// head_dim 128 (a second chunk in registers still fits without spilling) and 1 above.
-// Quantized: the caller's 1, 2 or 4, else 2 for INT4 (1 KB per chunk and wave; the
-// kernel then fits 4 waves per SIMD) and 4 for INT8 / FP8 (2 KB, 2 waves per SIMD).
+// Loads in flight per wave, in 16-token chunks (the depth of the kernels' register
+// ring): the caller's 1, 2 or 4 (fp16 head_dim 256: 1 or 2), else
+//   fp16: 2 (8 KB per chunk and wave at head_dim 128);
+//   INT4: 2 (1 KB per chunk and wave; the kernel then fits 4 waves per SIMD);
+//   INT8 / FP8: 4 (2 KB, 2 waves per SIMD).
 // Returns 0 when invalid.
 int pick_pipeline(const kvq_decode_args* a) {
-    if (a->kv_format != KVQ_KV_F16) {
-        if (a->pipeline == 0) return a->kv_format == KVQ_KV_INT4 ? 2 : 4;
-        return (a->pipeline == 1 || a->pipeline == 2 || a->pipeline == 4) ? a->pipeline : 0;
+    const int r = a->pipeline;
+    if (r == 0) {
+        if (a->kv_format == KVQ_KV_F16) return 2;
+        return a->kv_format == KVQ_KV_INT4 ? 2 : 4;
     }
-    if (a->pipeline == 0) return a->head_dim <= 128 ? 2 : 1;
-    return (a->pipeline == 1 || a->pipeline == 2) ? a->pipeline : 0;
+    if (r != 1 && r != 2 && r != 4) return 0;
+    if (r == 4 && a->kv_format == KVQ_KV_F16 && a->head_dim > 128) return 0;
+    return r;
 }
 
 int hip_status(hipError_t e) { return e == hipSuccess ? KVQ_OK : KVQ_ERR_HIP; }
@@ -256,14 +271,15 @@ int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t
     if (kv_format < KVQ_KV_F16 || kv_format > KVQ_KV_INT4) return KVQ_ERR_FORMAT;
     const bool quant = kv_format != KVQ_KV_F16;
     const int64_t chunks = int64_t(max_pages) * (block_size / 16);
-    const int64_t waves_per_cu = quant ? 8 : 4;
-    const int64_t chunks_per_wave = quant ? 64 : 256;
+    const int64_t waves_per_cu = quant ? 8 : 2;
+    const int64_t chunks_per_wave = quant ? 64 : 512;
     int64_t per_pair = pow2_floor(waves_per_cu * cu_count / (int64_t(batch) * kv_heads));
     const int64_t balance = pow2_floor(cdiv(chunks, chunks_per_wave));
     if (per_pair < balance) per_pair = balance;
     const int64_t cap = pow2_floor(chunks / 4);
     if (per_pair > cap) per_pair = cap;
-    const int64_t waves = per_pair < 4 ? per_pair : 4;
+    const int64_t max_waves = quant ? 4 : 2;
+    const int64_t waves = per_pair < max_waves ? per_pair : max_waves;
     *waves_out = int32_t(waves);
     *splits_out = int32_t(per_pair / waves);
     return KVQ_OK;

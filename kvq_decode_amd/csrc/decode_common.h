@@ -52,40 +52,6 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // result is unchanged; the common chunk needs no cross-lane max and no rescale.
 constexpr float kLazyMax = 8.0f;
 
-// Block-table entries of 128 consecutive pages, one per lane in two registers: `cur`
-// holds pages [base, base + 64), `nxt` the following 64, loaded one window ahead. A wave
-// reads its page's physical block with v_readlane from `cur`, a register no load has
-// written since it was swapped in, so the read never waits on the chunk loads in flight
-// (a window reloaded in a branch right before the read would make the compiler wait for
-// every outstanding load). Pages only move forward, by less than 64 per call.
-struct PageWindow {
-    int base;
-    int cur, nxt;
-};
-
-__device__ __forceinline__ int window_entry(const DecodeParams& p, int b, int page, int n_pages) {
-    return page < n_pages ? p.bt[(int64_t)b * p.bt_sb + page] : 0;
-}
-
-__device__ __forceinline__ void window_load(const DecodeParams& p, int b, int base, int n_pages,
-                                            PageWindow& w) {
-    const int lane = __lane_id();
-    w.base = base;
-    w.cur = window_entry(p, b, base + lane, n_pages);
-    w.nxt = window_entry(p, b, base + 64 + lane, n_pages);
-}
-
-__device__ __forceinline__ int window_phys(const DecodeParams& p, int b, int page, int n_pages,
-                                           PageWindow& w) {
-    if (page - w.base >= 64) {
-        w.cur = w.nxt;
-        w.base += 64;
-        w.nxt = window_entry(p, b, w.base + 64 + __lane_id(), n_pages);
-    }
-    const int phys = __builtin_amdgcn_readlane(w.cur, page - w.base);
-    return min(max(phys, 0), p.num_blocks - 1);
-}
-
 // Physical blocks of the P chunks c .. c + P - 1 (lane j < P) and of the first pages of
 // their K groups (lane P + j), chunks clamped to `last` so the load is issued on every
 // path. Used one ring ahead: the compiler's wait for this register then counts the

@@ -197,27 +197,34 @@ __device__ __forceinline__ QLaneOff lane_offsets(const DecodeParams& p, int i16,
     return o;
 }
 
+// Cache policy of the loads that stream the cache once (codes, V scale/zero): NT, the
+// streaming hint (buffer_load ... nt); measured on MI355X it lifts a plain streaming read
+// from about 6.3 to 7.0 TB/s. The K group scales, which every chunk of the group reloads,
+// keep the default policy.
+constexpr int kNT = 2;
+
 template <int FMT>
 __device__ __forceinline__ void load_chunk_q(const DecodeParams& p, int kvh, int c,
                                              const QLaneOff& lo, int phys, int lead,
                                              ChunkQ<FMT>& ch) {
     typedef QFmt<FMT> Q;
     const int slot = (c & ((1 << p.cpp_shift) - 1)) << 4;
-    const char* kpage = (const char*)p.k + block_offset(phys, p.k_sblk) + (int64_t)kvh * p.k_sh;
-    const char* vpage = (const char*)p.v + block_offset(phys, p.v_sblk) + (int64_t)kvh * p.v_sh;
+    const char* kpage = (const char*)p.k + block_offset(phys, p.k_sblk) +
+                        ((int64_t)slot * p.k_stok + (int64_t)kvh * p.k_sh);
+    const char* vpage = (const char*)p.v + block_offset(phys, p.v_sblk) +
+                        ((int64_t)slot * p.v_stok + (int64_t)kvh * p.v_sh);
     const auto rk = page_rsrc(kpage), rv = page_rsrc(vpage);
-    const int ks = slot * (int)p.k_stok, vsl = slot * (int)p.v_stok;
 #pragma unroll
     for (int j = 0; j < Q::KLOADS; ++j)
-        ch.k[j] = __builtin_amdgcn_raw_buffer_load_b128(rk, lo.k + 64 * j, ks, 0);
+        ch.k[j] = __builtin_amdgcn_raw_buffer_load_b128(rk, lo.k + 64 * j, 0, kNT);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         if constexpr (Q::VBYTES == 8) {
-            const u2 x = __builtin_amdgcn_raw_buffer_load_b64(rv, lo.v[r], vsl, 0);
+            const u2 x = __builtin_amdgcn_raw_buffer_load_b64(rv, lo.v[r], 0, kNT);
             ch.v[r][0] = x[0];
             ch.v[r][Q::VBYTES / 4 - 1] = x[1];
         } else {
-            ch.v[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, lo.v[r], vsl, 0);
+            ch.v[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, lo.v[r], 0, kNT);
         }
     }
     // V scale/zero of tokens slot + 4g .. +3 (4 consecutive halves; slots past the
@@ -226,8 +233,8 @@ __device__ __forceinline__ void load_chunk_q(const DecodeParams& p, int kvh, int
                           (uint32_t)(2 * p.block_size);
     const auto rvs = page_rsrc((const char*)p.v_scale + vrow);
     const auto rvz = page_rsrc((const char*)p.v_zero + vrow);
-    ch.vs = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rvs, lo.vs, 2 * slot, 0));
-    ch.vz = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rvz, lo.vs, 2 * slot, 0));
+    ch.vs = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rvs, lo.vs, 2 * slot, kNT));
+    ch.vz = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rvz, lo.vs, 2 * slot, kNT));
     // K group scale/zero, stored with the group's first page `lead`
     const uint64_t krow = ((uint64_t)(uint32_t)lead * (uint32_t)p.kv_heads + kvh) * 256u;
     const auto rks = page_rsrc((const char*)p.k_scale + krow);

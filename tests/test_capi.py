@@ -74,17 +74,18 @@ def test_plan_decode():
     16), its caps, and its argument errors."""
     from kvq_decode_amd.ops import plan_decode
     cases = [  # batch, max_pages, format -> (splits, waves)
-        (8, 2048, "fp16", (4, 4)),      # 4 waves/CU: 16 per (sequence, kv head)
-        (16, 2048, "fp16", (2, 4)),
-        (1, 8192, "fp16", (32, 4)),     # 128 per pair
+        (8, 2048, "fp16", (4, 2)),      # 2 waves/CU: 8 per (sequence, kv head)
+        (16, 2048, "fp16", (2, 2)),
+        (1, 8192, "fp16", (32, 2)),     # 64 per pair
+        (64, 2048, "fp16", (2, 2)),     # raised to 4 per pair: <= 512 chunks per wave
         (16, 2048, "int4", (8, 4)),     # <= 64 chunks per wave for quantized
         (64, 2048, "int8", (8, 4)),
-        (64, 64, "fp16", (1, 2)),       # 2 per pair from 4 waves/CU
+        (64, 64, "fp16", (1, 1)),       # 1 per pair from 2 waves/CU
         (2, 3, "fp16", (1, 1)),         # at least 4 chunks per wave
     ]
     for batch, pages, fmt, want in cases:
         assert plan_decode(batch, 8, 16, pages, 256, fmt) == want, (batch, pages, fmt)
-    assert plan_decode(1, 8, 32, 4096, 256, "fp16") == (32, 4)  # 2 chunks per page
+    assert plan_decode(1, 8, 32, 4096, 256, "fp16") == (32, 2)  # 2 chunks per page
     L = _lib.lib()
     s, w = ctypes.c_int32(), ctypes.c_int32()
     assert L.kvq_plan_decode(0, 8, 16, 64, 0, 256, ctypes.byref(s), ctypes.byref(w)) == \
@@ -141,6 +142,8 @@ BAD_CASES = [
     ("k_stride_tok", 1 << 27, _lib.KVQ_ERR_UNSUPPORTED),   # 32-bit lane offsets
     ("waves_per_group", 3, _lib.KVQ_ERR_UNSUPPORTED),
     ("pipeline", 5, _lib.KVQ_ERR_UNSUPPORTED),
+    ("k_stride_blk", 1 << 31, _lib.KVQ_ERR_UNSUPPORTED),   # 2^32-byte block stride
+    ("v_stride_blk", -16 * 8 * 128, _lib.KVQ_ERR_UNSUPPORTED),
 ]
 
 
@@ -160,6 +163,15 @@ def test_quantized_tuning_limits():
         a.k_scale = a.k_zero = a.v_scale = a.v_zero = 1 << 43
         setattr(a, field, value)
         assert L.kvq_decode_single(ctypes.byref(a), None) == _lib.KVQ_ERR_UNSUPPORTED, field
+
+
+def test_fp16_ring_depth_limits():
+    """fp16: ring depth 1, 2 or 4 up to head_dim 128; head_dim 256 takes 1 or 2."""
+    L = _lib.lib()
+    a = good_args()
+    a.head_dim, a.q_stride_b, a.q_stride_h = 256, 32 * 256, 256
+    a.pipeline = 4
+    assert L.kvq_decode_single(ctypes.byref(a), None) == _lib.KVQ_ERR_UNSUPPORTED
 
 
 def test_split_rejects_bad_split_geometry():

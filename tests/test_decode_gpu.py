@@ -119,17 +119,37 @@ def test_nan_garbage_in_unused_slots(num_splits):
     check_close(out, ref, f"nan-garbage splits={num_splits}")
 
 
-@pytest.mark.parametrize("waves,pipeline", [(1, 1), (2, 2), (4, 1), (8, 2), (16, 1), (16, 2)])
+@pytest.mark.parametrize("waves,pipeline", [(1, 1), (2, 2), (4, 1), (8, 2), (16, 1), (16, 2),
+                                            (1, 4), (4, 4), (8, 4), (16, 4)])
 def test_workgroup_shapes_agree(waves, pipeline):
-    """Every (waves per workgroup, pipeline depth) kernel variant gives the same result."""
+    """Every (waves per workgroup, ring depth) kernel variant gives the oracle's result,
+    and the ring depth never changes a bit (it only reorders loads)."""
     from kvq_decode_amd import paged_decode_attention
-    q, kc, vc, bt, sl = make(32, 8, 128, 16, [3000, 77, 1])
+    q, kc, vc, bt, sl = make(32, 8, 128, 16, [3000, 77, 1, 16 * 37])
     ref = paged_decode_attention_ref(q, kc, vc, bt, sl, out_dtype=np.float32)
     args = to_gpu(q, kc, vc, bt, sl)
     for splits in (1, 6):
         out = paged_decode_attention(*args, num_splits=splits, waves_per_group=waves,
                                      pipeline=pipeline)
         check_close(out, ref, f"waves={waves} pipe={pipeline} splits={splits}")
+        base = paged_decode_attention(*args, num_splits=splits, waves_per_group=waves,
+                                      pipeline=1)
+        assert torch.equal(out, base), f"ring depth {pipeline} changed bits (splits={splits})"
+
+
+@pytest.mark.parametrize("D", [32, 64, 256])
+@pytest.mark.parametrize("pipeline", [1, 2, 4])
+def test_ring_depths_other_head_dims(D, pipeline):
+    """The ring's loads for head_dim 32 / 64 / 256 (4-, 8- and 32-byte V rows per lane)."""
+    from kvq_decode_amd import paged_decode_attention
+    if D == 256 and pipeline == 4:
+        pytest.skip("ring depth 4 is built up to head_dim 128")
+    q, kc, vc, bt, sl = make(16, 4, D, 32, [1000, 45, 16, 300])
+    ref = paged_decode_attention_ref(q, kc, vc, bt, sl, out_dtype=np.float32)
+    args = to_gpu(q, kc, vc, bt, sl)
+    for splits in (1, 5):
+        out = paged_decode_attention(*args, num_splits=splits, pipeline=pipeline)
+        check_close(out, ref, f"D={D} pipe={pipeline} splits={splits}")
 
 
 def _baseline_case(B, ctx, pool, seed=0):
