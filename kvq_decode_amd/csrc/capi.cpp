@@ -61,6 +61,20 @@ int check_decode_args(const kvq_decode_args* a, bool need_out) {
         if (!aligned16(a->k_scale) || !aligned16(a->k_zero) || !aligned16(a->v_scale) ||
             !aligned16(a->v_zero))
             return KVQ_ERR_ALIGNMENT;
+        // The quantized kernels address each kv head's codes and scales through 32-bit
+        // offsets from the head's base: every offset must stay below 2^32 bytes.
+        const int64_t lim32 = int64_t(1) << 32;
+        const int64_t row = a->kv_format == KVQ_KV_INT4 ? a->head_dim / 2 : a->head_dim;
+        if (a->k_stride_blk < 0 || a->v_stride_blk < 0 || a->k_stride_tok < 0 ||
+            a->v_stride_tok < 0)
+            return KVQ_ERR_UNSUPPORTED;
+        if (int64_t(a->num_blocks - 1) * a->k_stride_blk +
+                    int64_t(a->block_size - 1) * a->k_stride_tok + row >= lim32 ||
+            int64_t(a->num_blocks - 1) * a->v_stride_blk +
+                    int64_t(a->block_size - 1) * a->v_stride_tok + row >= lim32 ||
+            int64_t(a->num_blocks) * a->kv_heads * 256 >= lim32 ||
+            int64_t(a->num_blocks) * a->kv_heads * 2 * a->block_size >= lim32)
+            return KVQ_ERR_UNSUPPORTED;
     }
     // Vector loads: 16-byte aligned bases and row strides that keep every row aligned.
     const int64_t vec = a->kv_format == KVQ_KV_F16 ? 8 : 16;  // elements per 16 bytes
@@ -78,6 +92,10 @@ int check_decode_args(const kvq_decode_args* a, bool need_out) {
     const int64_t esz = a->kv_format == KVQ_KV_F16 ? 2 : 1;
     if (a->k_stride_blk < 0 || a->v_stride_blk < 0 ||
         a->k_stride_blk * esz >= (int64_t(1) << 32) || a->v_stride_blk * esz >= (int64_t(1) << 32))
+        return KVQ_ERR_UNSUPPORTED;
+    // A token's offset inside its block is a 32-bit byte offset.
+    if (int64_t(a->block_size) * a->k_stride_tok * esz >= (int64_t(1) << 31) ||
+        int64_t(a->block_size) * a->v_stride_tok * esz >= (int64_t(1) << 31))
         return KVQ_ERR_UNSUPPORTED;
     // Lane offsets inside a 16-token chunk are 32-bit byte offsets.
     const int64_t lim = int64_t(1) << 30;
@@ -129,13 +147,14 @@ int64_t lds_bytes(const kvq_decode_args* a, int waves) {
     const int group = a->q_heads / a->kv_heads;
     const int64_t combine = int64_t(4) * (int64_t(waves) * group * a->head_dim + 32 * waves);
     // fp16: the waves' K staging tiles (16 rows of head_dim halves each), which the
-    // combine reuses; quantized: a 512-byte K-scale slot per wave and 4 KB of q in
-    // k-operand order after the combine's region
+    // combine reuses; quantized: region 0 (combine or K tiles), a 512-byte K-scale slot
+    // per wave and 4 KB of q in k-operand order
     if (a->kv_format == KVQ_KV_F16) {
         const int64_t stage = int64_t(waves) * 32 * a->head_dim;
         return combine > stage ? combine : stage;
     }
-    return combine + int64_t(4) * (128 * int64_t(waves) + 1024);
+    return int64_t(4) * (kvq::quant_lds_region0(waves, group, a->kv_format) + 128 * int64_t(waves) +
+                         1024);
 }
 
 // Waves per workgroup: the caller's choice if given, else as many as give each wave at
@@ -306,6 +325,9 @@ int kvq_decode_split(const kvq_decode_args* args, int32_t num_splits, int32_t pa
     if (st != KVQ_OK) return st;
     if (!o_part || !lse) return KVQ_ERR_NULL_POINTER;
     if (num_splits < 1 || pages_per_split < 1 || num_splits > 65535) return KVQ_ERR_SPLITS;
+    // the 1-D decode grid: kv_heads * (splits * batch rounded up to a multiple of 8)
+    if ((int64_t(num_splits) * args->batch + 7) / 8 * 8 * args->kv_heads > INT32_MAX)
+        return KVQ_ERR_UNSUPPORTED;
     if (int64_t(num_splits) * pages_per_split < args->max_blocks) return KVQ_ERR_SPLITS;
     const int waves = pick_waves(args, pages_per_split);
     const int pipe = pick_pipeline(args);
@@ -335,6 +357,7 @@ int kvq_decode_merge(const float* o_part, const float* lse, void* out, int64_t o
 int kvq_decode_single(const kvq_decode_args* args, kvq_stream_t stream) {
     int st = check_decode_args(args, true);
     if (st != KVQ_OK) return st;
+    if ((int64_t(args->batch) + 7) / 8 * 8 * args->kv_heads > INT32_MAX) return KVQ_ERR_UNSUPPORTED;
     const int waves = pick_waves(args, args->max_blocks);
     const int pipe = pick_pipeline(args);
     if (waves == 0 || pipe == 0) return KVQ_ERR_UNSUPPORTED;

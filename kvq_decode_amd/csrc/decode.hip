@@ -209,7 +209,9 @@ void decode_f16_kernel(const DecodeParams p) {
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int kvh = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
+    const WgCoord wc = wg_coord(p, FINAL ? 1 : p.num_splits);
+    if (!wc.live) return;
+    const int kvh = wc.kvh, split = wc.split, b = wc.b;
     const int i16 = lane & 15, g = lane >> 4;
     const int G = p.group;
     const bool head_ok = i16 < G;
@@ -331,7 +333,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ o_
 
 template <int D, int W, bool FINAL, int P>
 static hipError_t launch_f16(const DecodeParams& p, hipStream_t stream) {
-    const dim3 grid(p.kv_heads, FINAL ? 1 : p.num_splits, p.batch);
+    const dim3 grid(decode_grid(p.kv_heads, FINAL ? 1 : p.num_splits, p.batch));
     // the larger of the cross-wave combine ([W][G][D] + [W][16] m, l floats) and the
     // waves' K staging tiles (32 * D bytes each)
     const size_t combine = sizeof(float) * (W * p.group * D + 2 * W * 16);

@@ -81,6 +81,39 @@ __device__ __forceinline__ uint64_t block_offset(int phys, int64_t stride) {
     return (uint64_t)(uint32_t)phys * (uint32_t)stride;
 }
 
+// XCD-aware workgroup order. MI355X dispatches the workgroups of a launch to its 8 XCDs
+// round-robin by linear id, and each XCD has its own L2. A (kv head, split, sequence) grid
+// with the head fastest would put the kv heads of one (sequence, split) on 8 different
+// XCDs, so a cache line they share (the quantized caches' V scales: 4 heads per 128-byte
+// line) would be fetched by several L2s. The decode kernels run a 1-D grid of kv_heads *
+// U8 workgroups instead (U = splits * batch units, U8 rounded up to a multiple of 8),
+// numbered id = 8 * (kvh + kv_heads * (u / 8)) + u % 8: every kv head of unit u runs on
+// XCD u % 8, back to back. Workgroups past the last unit exit at once.
+constexpr int kXcds = 8;
+
+struct WgCoord {
+    int kvh, split, b;
+    bool live;
+};
+
+__device__ __forceinline__ WgCoord wg_coord(const DecodeParams& p, int splits) {
+    const int i = blockIdx.x;
+    const int q = i / kXcds;
+    WgCoord c;
+    c.kvh = q % p.kv_heads;
+    const int u = (q / p.kv_heads) * kXcds + i % kXcds;
+    c.split = u % splits;
+    c.b = u / splits;
+    c.live = c.b < p.batch;
+    return c;
+}
+
+// Workgroups of the 1-D decode grid (see wg_coord).
+inline unsigned decode_grid(int kv_heads, int splits, int batch) {
+    const long units = ((long)splits * batch + kXcds - 1) / kXcds * kXcds;
+    return (unsigned)(units * kv_heads);
+}
+
 // Online-softmax state of one wave: running reference max m and partial sum l of its
 // lane (head l%16, tokens 4g..4g+3 of every chunk), and O^T accumulator tiles.
 template <int D>

@@ -4,21 +4,37 @@
 // started"); its byte model (src/bpt/roofline.py:6-9, 22-31) fixes the format's costs.
 //
 // Same workgroup/wave decomposition and MFMA layouts as the fp16 kernel (decode.hip); the
-// dequantization is folded into the two products instead of being applied per element:
+// dequantization is folded into the two products instead of being applied per element.
 //
-//   code c -> fp16 h exactly, with c = F * (h - B):
-//     INT8  h = 1024 + c  (v_perm with 0x64 bytes; F = 1, B = 1024)
-//     INT4  h = 1 + c/64  (nibble into mantissa bits 4-7 of 1.0; F = 64, B = 1)
-//     FP8   h = f(c)      (v_cvt_scalef32_pk_f16_fp8, exact; F = 1, B = 0)
+//   code c -> fp16 h, exactly and without a bias: h = c * w / F
+//     INT8  h = c * 2^-24: the code is the mantissa of an fp16 subnormal (one v_perm per
+//           two codes); F = 2^24, w = 1
+//     INT4  nibbles masked in place: low nibbles (even codes) c * 2^-24 (w = 1), high
+//           nibbles (odd codes) c * 2^-20 (w = 16); F = 2^24. Five VALU ops per 8 codes
+//     FP8   h = f(c) (v_cvt_scalef32_pk_f16_fp8, exact OCP e4m3fn); F = 1, w = 1
+//   MI355X's MFMAs take fp16 subnormal inputs exactly (measured: a 32-term product sum of
+//   subnormal A operands agrees with an exact sum to fp32 rounding).
 //   K (x = c * s_d + z_d, per channel d):
-//     q.k = sum_d q'_d c_d + sum_d q_d z_d,  q' = q * s = hi + lo (two fp16 parts,
-//           recomputed per K group)
-//         = F * (sum_d q'_d h_d + C),  C = sum_d q_d z_d / F - B * sum_d q'_d
-//     -> MFMA chains on h (with hi, then lo) with C as the accumulator input, then * F.
+//     q.k = sum_d q'_d c_d + C = F * sum_d (q'_d / w_d) h_d + C,   q' = q * s,
+//     C = sum_d q_d z_d.  q'' = q' / w is held as hi + lo fp16 parts (recomputed per K
+//     group); the MFMA chains give R = sum q'' h, and the log2-domain score is
+//     R * (F * scale * log2 e) + C * scale * log2 e.
 //   V (x = c * s_t + z_t, per token t):
-//     sum_t p_t x_td = F * sum_t p''_t h_td + corr,  p'' = fp16(p * s_t),
-//     corr = sum_t (p_t z_t - F * B * p''_t)     (fp32, per head, rescaled with l)
-//     -> the PV MFMA takes p'' as its B operand; corr is added once at the end.
+//     sum_t p_t x_td = (F / w_d) * sum_t p''_t h_td + sum_t p_t z_t,  p'' = p * s_t as
+//     hi + lo fp16 parts (the PV MFMA's B operand); the second sum is one fp32 scalar per
+//     head (`corr`), added once at the end.
+//
+// Two kernels:
+//   decode_q2_kernel (1 to 4 q heads per kv head): the 16 MFMA columns hold 2 chunks x
+//     4 heads x {hi, lo}. Column j: head j & 3, chunk (j >> 2) & 1 of the pair, part j >> 3.
+//     The QK product runs the 4 k-steps of both chunks into one accumulator against
+//     block-masked Q operands (zero in the other chunk's columns), so one softmax pass
+//     covers 32 tokens, and the PV product contracts both chunks in one 16x16x32 MFMA per
+//     tile: k-slots 8g + r hold the first chunk's token 4g + r, 8g + 4 + r the second's;
+//     each lane's p sits in the half of its own chunk, zeros in the other. The two chunks'
+//     softmax streams of a head (columns j, j ^ 4) are merged once at the end.
+//   decode_q_kernel (5 to 16 heads): one chunk per step; up to 8 heads the columns hold
+//     {hi, lo} x 8 heads (one QK chain), above that two chains.
 // Only head_dim 128 is built for the quantized formats.
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -37,76 +53,51 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
     return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
-constexpr uint32_t kMagicI8 = 0x64646464u;   // 0x64bb = fp16 1024 + bb
-constexpr uint32_t kMagicI4 = 0x3C003C00u;   // fp16 1.0; nibble n at bits 4-7 -> 1 + n/64
-constexpr uint32_t kNib = 0x00F000F0u;
-
-// Two int8 codes -> halves (1024 + c): bytes 0,1 (lo) or 2,3 (hi) of x.
-__device__ __forceinline__ uint32_t i8_lo(uint32_t x) { return perm(kMagicI8, x, 0x04010400u); }
-__device__ __forceinline__ uint32_t i8_hi(uint32_t x) { return perm(kMagicI8, x, 0x04030402u); }
-
-// The nibble mask and the 1.0 pattern, held in registers the compiler cannot see through,
-// so (x & mask) | magic becomes one v_and_or_b32 (VOP3 takes no literal constants here)
-// instead of a v_and_b32 + v_or_b32 pair with literals.
-struct I4Consts {
-    uint32_t nib, magic;
-};
-
-__device__ __forceinline__ I4Consts i4_consts() {
-    I4Consts c{kNib, kMagicI4};
-    asm volatile("" : "+v"(c.nib), "+v"(c.magic));
-    return c;
+// Byte e of a and byte e of b as the low bytes of two halves: [a.e, 0, b.e, 0].
+__device__ __forceinline__ uint32_t pair_bytes(uint32_t a, uint32_t b, int e) {
+    return perm(b, a, 0x0C040C00u + 0x00010001u * (uint32_t)e);
 }
 
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
-    return (x & m) | o;
-}
-
-// Nibbles of one dword (byte j = codes 2j (low), 2j+1 (high)) -> 8 halves 1 + c/64 in the
-// order codes {0,4, 1,5, 2,6, 3,7}.
-__device__ __forceinline__ u4v i4_dword(uint32_t x, I4Consts k) {
-    u4v r;
-    r[0] = and_or(x << 4, k.nib, k.magic);
-    r[1] = and_or(x, k.nib, k.magic);
-    r[2] = and_or(x >> 4, k.nib, k.magic);
-    r[3] = and_or(x >> 8, k.nib, k.magic);
-    return r;
-}
+// Initial reference max of an online-softmax stream: finite, so that a stream that has
+// seen no token yet (m = kM0, l = 0) rescales by exp2(kM0 - m') = 0 or 1 without NaN, and
+// masked scores (-inf) give p = 0.
+constexpr float kM0 = -1e30f;
 
 template <int FMT>
 struct QFmt;
 
-// INT8 / FP8 share the byte layout: K rows of 128 bytes, lane (token l%16, g) loads bytes
-// [64j + 16g, +16) for j = 0, 1; k-step st = 2j + u uses dwords 2u, 2u+1, i.e. channels
-// 64*(st/2) + 16g + 8*(st%2) + e in order. V: 8 bytes per token row per lane.
+// INT8 / FP8 share the byte layout: K rows of 128 bytes; after the LDS staging (kstage_q)
+// lane (token l%16, g) holds bytes [64j + 16g, +16) for j = 0, 1; k-step st = 2j + u uses
+// dwords 2u, 2u+1, i.e. channels 64*(st/2) + 16g + 8*(st%2) + e in order. V: 8 bytes per
+// token row per lane, tile t = byte t of the lane's 8.
 template <>
 struct QFmt<KVQ_KV_INT8> {
-    static constexpr float F = 1.f, B = 1024.f;
+    static constexpr float F = 16777216.f;  // 2^24
     static constexpr int KLOADS = 2, VBYTES = 8;
     __device__ static int chan_base(int st, int g) { return 64 * (st >> 1) + 16 * g + 8 * (st & 1); }
     static constexpr bool permuted() { return false; }
-    __device__ static h8 kop(const u4v* kr, int st, I4Consts) {
+    __device__ static h8 kop(const u4v* kr, int st) {
         const u4v x = kr[st >> 1];
         const uint32_t d0 = x[2 * (st & 1)], d1 = x[2 * (st & 1) + 1];
         u4v o;
-        o[0] = i8_lo(d0);
-        o[1] = i8_hi(d0);
-        o[2] = i8_lo(d1);
-        o[3] = i8_hi(d1);
+        o[0] = perm(0u, d0, 0x0C010C00u);
+        o[1] = perm(0u, d0, 0x0C030C02u);
+        o[2] = perm(0u, d1, 0x0C010C00u);
+        o[3] = perm(0u, d1, 0x0C030C02u);
         return __builtin_bit_cast(h8, o);
     }
-    // V^T operand halves of tile pairs: tiles 4k..4k+3 of token pair (ra, rb).
-    __device__ static void vpair(uint32_t a, uint32_t b, uint32_t* out4) {
-        const uint32_t y0 = perm(b, a, 0x05010400u), y1 = perm(b, a, 0x07030602u);
-        out4[0] = i8_lo(y0);
-        out4[1] = i8_hi(y0);
-        out4[2] = i8_lo(y1);
-        out4[3] = i8_hi(y1);
+    // V^T operand dwords: tile t of token pairs (0, 1) and (2, 3) of the lane's 4 rows.
+    __device__ static void vtiles(const uint32_t (*v)[2], uint32_t* a01, uint32_t* a23) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            a01[t] = pair_bytes(v[0][t >> 2], v[1][t >> 2], t & 3);
+            a23[t] = pair_bytes(v[2][t >> 2], v[3][t >> 2], t & 3);
+        }
     }
 };
 
 // FP8: gfx950 converts OCP e4m3fn to fp16 exactly in hardware (two codes per
-// v_cvt_scalef32_pk_f16_fp8, scale 1.0), so h = f(c) with F = 1, B = 0.
+// v_cvt_scalef32_pk_f16_fp8, scale 1.0), so h = f(c) with F = 1.
 __device__ __forceinline__ uint32_t f8_lo(uint32_t x) {
     return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 1.0f, false));
 }
@@ -116,11 +107,11 @@ __device__ __forceinline__ uint32_t f8_hi(uint32_t x) {
 
 template <>
 struct QFmt<KVQ_KV_FP8_E4M3> {
-    static constexpr float F = 1.f, B = 0.f;
+    static constexpr float F = 1.f;
     static constexpr int KLOADS = 2, VBYTES = 8;
     __device__ static int chan_base(int st, int g) { return 64 * (st >> 1) + 16 * g + 8 * (st & 1); }
     static constexpr bool permuted() { return false; }
-    __device__ static h8 kop(const u4v* kr, int st, I4Consts) {
+    __device__ static h8 kop(const u4v* kr, int st) {
         const u4v x = kr[st >> 1];
         const uint32_t d0 = x[2 * (st & 1)], d1 = x[2 * (st & 1) + 1];
         u4v o;
@@ -130,36 +121,55 @@ struct QFmt<KVQ_KV_FP8_E4M3> {
         o[3] = f8_hi(d1);
         return __builtin_bit_cast(h8, o);
     }
-    __device__ static void vpair(uint32_t a, uint32_t b, uint32_t* out4) {
-        const uint32_t y0 = perm(b, a, 0x05010400u), y1 = perm(b, a, 0x07030602u);
-        out4[0] = f8_lo(y0);
-        out4[1] = f8_hi(y0);
-        out4[2] = f8_lo(y1);
-        out4[3] = f8_hi(y1);
+    __device__ static void vtiles(const uint32_t (*v)[2], uint32_t* a01, uint32_t* a23) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            // bytes [a0, b0, a1, b1] and [a2, b2, a3, b3] of token pairs, two codes per cvt
+            const uint32_t x0 = perm(v[1][k], v[0][k], 0x05010400u);
+            const uint32_t x1 = perm(v[1][k], v[0][k], 0x07030602u);
+            const uint32_t y0 = perm(v[3][k], v[2][k], 0x05010400u);
+            const uint32_t y1 = perm(v[3][k], v[2][k], 0x07030602u);
+            a01[4 * k + 0] = f8_lo(x0);
+            a01[4 * k + 1] = f8_hi(x0);
+            a01[4 * k + 2] = f8_lo(x1);
+            a01[4 * k + 3] = f8_hi(x1);
+            a23[4 * k + 0] = f8_lo(y0);
+            a23[4 * k + 1] = f8_hi(y0);
+            a23[4 * k + 2] = f8_lo(y1);
+            a23[4 * k + 3] = f8_hi(y1);
+        }
     }
 };
 
 // INT4: K rows of 64 bytes, lane (token, g) loads bytes [16g, +16) (channels [32g, +32));
-// k-step st uses dword st, halves in code order {0,4,1,5,2,6,3,7} of channels 32g + 8st.
-// V: 4 bytes (8 channels) per token row per lane.
+// k-step st uses dword st: halves in code order {0,4, 1,5, 2,6, 3,7} of channels 32g + 8st,
+// the odd codes at 2^-20 (w = 16). V: 4 bytes (8 codes) per token row per lane; tile t =
+// code t of the lane's 8, odd tiles at 2^-20.
 template <>
 struct QFmt<KVQ_KV_INT4> {
-    static constexpr float F = 64.f, B = 1.f;
+    static constexpr float F = 16777216.f;  // 2^24
     static constexpr int KLOADS = 1, VBYTES = 4;
     __device__ static int chan_base(int st, int g) { return 32 * g + 8 * st; }
     static constexpr bool permuted() { return true; }
-    __device__ static h8 kop(const u4v* kr, int st, I4Consts k) {
-        return __builtin_bit_cast(h8, i4_dword(kr[0][st], k));
+    __device__ static h8 kop(const u4v* kr, int st) {
+        const uint32_t x = kr[0][st], y = x >> 8;
+        u4v o;
+        o[0] = x & 0x000F000Fu;
+        o[1] = x & 0x00F000F0u;
+        o[2] = y & 0x000F000Fu;
+        o[3] = y & 0x00F000F0u;
+        return __builtin_bit_cast(h8, o);
     }
-    // Tiles 0..3 (channels 0..3 of the lane's 8) or 4..7 of token pair (ra, rb) from the
-    // dwords a, b holding each token's 8 codes.
-    __device__ static void vpair_half(uint32_t a, uint32_t b, uint32_t sel, uint32_t* out4,
-                                      I4Consts k) {
-        const uint32_t y = perm(b, a, sel);  // low 16 bits: ra's 4 codes, high: rb's
-        out4[0] = and_or(y << 4, k.nib, k.magic);
-        out4[1] = and_or(y, k.nib, k.magic);
-        out4[2] = and_or(y >> 4, k.nib, k.magic);
-        out4[3] = and_or(y >> 8, k.nib, k.magic);
+    __device__ static void vtiles(const uint32_t (*v)[1], uint32_t* a01, uint32_t* a23) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t x = pair_bytes(v[0][0], v[1][0], k);
+            const uint32_t y = pair_bytes(v[2][0], v[3][0], k);
+            a01[2 * k] = x & 0x000F000Fu;
+            a01[2 * k + 1] = x & 0x00F000F0u;
+            a23[2 * k] = y & 0x000F000Fu;
+            a23[2 * k + 1] = y & 0x00F000F0u;
+        }
     }
 };
 
@@ -176,71 +186,109 @@ struct ChunkQ {
 };
 
 // Per-lane byte offsets of a chunk's loads inside its page (the page base and the slot
-// are wave-uniform): K row min(l%16, last) bytes [16g, +16) (+64 per further load), V rows
-// min(4g + r, last) bytes [VBYTES * (l%16), +VBYTES), V scales of tokens 4g..4g+3, and
-// channels 2l, 2l+1 of the K group scales. `last` = valid tokens - 1 of the chunk.
+// are wave-uniform), `last` = valid tokens - 1 of the chunk:
+//   K, INT4 (64-byte rows): row min(l%16, last) bytes [16g, +16) - one load instruction
+//     covers all 16 rows;
+//   K, INT8 / FP8 (128-byte rows): load j row min(8j + l/8, last), bytes [16(l%8), +16) -
+//     each instruction covers 8 whole rows (every 128-byte line in one instruction); the
+//     rows reach the k-operand layout through the wave's LDS tile (kstage_q);
+//   V rows min(4g + r, last) bytes [VBYTES * (l%16), +VBYTES), V scales of tokens
+//   4g..4g+3, and channels 2l, 2l+1 of the K group scales.
 struct QLaneOff {
-    uint32_t k, v[4], vs, ks;
+    uint32_t k[2], v[4], vs, ks;
 };
 
 template <int FMT>
 __device__ __forceinline__ QLaneOff lane_offsets(const DecodeParams& p, int i16, int g,
                                                  int last) {
     typedef QFmt<FMT> Q;
+    const int lane = __lane_id();
     QLaneOff o;
-    o.k = (uint32_t)(min(i16, last) * (int)p.k_stok + 16 * g);
+    if constexpr (Q::KLOADS == 1) {
+        o.k[0] = o.k[1] = (uint32_t)(min(i16, last) * (int)p.k_stok + 16 * g);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            o.k[j] = (uint32_t)(min(8 * j + (lane >> 3), last) * (int)p.k_stok + 16 * (lane & 7));
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r)
         o.v[r] = (uint32_t)(min(4 * g + r, last) * (int)p.v_stok + Q::VBYTES * i16);
     o.vs = 8 * g;
-    o.ks = 4 * __lane_id();
+    o.ks = 4 * lane;
     return o;
 }
 
-// Cache policy of the loads that stream the cache once (codes, V scale/zero): NT, the
-// streaming hint (buffer_load ... nt); measured on MI355X it lifts a plain streaming read
-// from about 6.3 to 7.0 TB/s. The K group scales, which every chunk of the group reloads,
-// keep the default policy.
+// Buffer resources of one kv head's data, made once per wave (the head offset folded
+// into each base), and the strides a chunk's offset needs. Every offset from these bases
+// is below 2^32 bytes (checked on the host), so a chunk's loads take its offset as one
+// 32-bit scalar (soffset) plus the lane's 32-bit offset (voffset): a few scalar
+// multiplies per chunk and no vector address arithmetic.
+struct QBase {
+    __amdgpu_buffer_rsrc_t k, v, vs, vz, ks, kz;
+    uint32_t k_sblk, v_sblk, k_stok, v_stok;
+    uint32_t vs_blk, ks_blk;  // bytes per block of the V / K scale tensors
+    uint32_t cmask;           // 16-token chunks per page - 1
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rsrc(const void* base, int64_t off) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>((const char*)base + off), (short)0,
+                                             -1, 0x00020000);
+}
+
+__device__ __forceinline__ QBase q_base(const DecodeParams& p, int kvh) {
+    QBase B;
+    B.k = head_rsrc(p.k, (int64_t)kvh * p.k_sh);
+    B.v = head_rsrc(p.v, (int64_t)kvh * p.v_sh);
+    B.vs = head_rsrc(p.v_scale, (int64_t)kvh * 2 * p.block_size);
+    B.vz = head_rsrc(p.v_zero, (int64_t)kvh * 2 * p.block_size);
+    B.ks = head_rsrc(p.k_scale, (int64_t)kvh * 256);
+    B.kz = head_rsrc(p.k_zero, (int64_t)kvh * 256);
+    B.k_sblk = (uint32_t)p.k_sblk;
+    B.v_sblk = (uint32_t)p.v_sblk;
+    B.k_stok = (uint32_t)p.k_stok;
+    B.v_stok = (uint32_t)p.v_stok;
+    B.vs_blk = (uint32_t)(p.kv_heads * 2 * p.block_size);
+    B.ks_blk = (uint32_t)(p.kv_heads * 256);
+    B.cmask = (1u << p.cpp_shift) - 1;
+    return B;
+}
+
+// Cache policy of the loads that stream the cache once (codes, V scale/zero): nt, the
+// streaming hint; measured on MI355X it lifts a plain streaming read from about 6.3 to
+// 7.0 TB/s. The K group scales, which every chunk of the group reloads, keep the default
+// policy.
 constexpr int kNT = 2;
 
 template <int FMT>
-__device__ __forceinline__ void load_chunk_q(const DecodeParams& p, int kvh, int c,
-                                             const QLaneOff& lo, int phys, int lead,
-                                             ChunkQ<FMT>& ch) {
+__device__ __forceinline__ void load_chunk_q(const QBase& B, int c, const QLaneOff& lo, int phys,
+                                             int lead, ChunkQ<FMT>& ch) {
     typedef QFmt<FMT> Q;
-    const int slot = (c & ((1 << p.cpp_shift) - 1)) << 4;
-    const char* kpage = (const char*)p.k + block_offset(phys, p.k_sblk) +
-                        ((int64_t)slot * p.k_stok + (int64_t)kvh * p.k_sh);
-    const char* vpage = (const char*)p.v + block_offset(phys, p.v_sblk) +
-                        ((int64_t)slot * p.v_stok + (int64_t)kvh * p.v_sh);
-    const auto rk = page_rsrc(kpage), rv = page_rsrc(vpage);
+    const uint32_t slot = ((uint32_t)c & B.cmask) << 4;
+    const uint32_t ko = (uint32_t)phys * B.k_sblk + slot * B.k_stok;
+    const uint32_t vo = (uint32_t)phys * B.v_sblk + slot * B.v_stok;
 #pragma unroll
     for (int j = 0; j < Q::KLOADS; ++j)
-        ch.k[j] = __builtin_amdgcn_raw_buffer_load_b128(rk, lo.k + 64 * j, 0, kNT);
+        ch.k[j] = __builtin_amdgcn_raw_buffer_load_b128(B.k, lo.k[j], ko, kNT);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         if constexpr (Q::VBYTES == 8) {
-            const u2 x = __builtin_amdgcn_raw_buffer_load_b64(rv, lo.v[r], 0, kNT);
+            const u2 x = __builtin_amdgcn_raw_buffer_load_b64(B.v, lo.v[r], vo, kNT);
             ch.v[r][0] = x[0];
             ch.v[r][Q::VBYTES / 4 - 1] = x[1];
         } else {
-            ch.v[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, lo.v[r], 0, kNT);
+            ch.v[r][0] = __builtin_amdgcn_raw_buffer_load_b32(B.v, lo.v[r], vo, kNT);
         }
     }
     // V scale/zero of tokens slot + 4g .. +3 (4 consecutive halves; slots past the
-    // sequence hold garbage and are masked in chunk_q).
-    const uint64_t vrow = ((uint64_t)(uint32_t)phys * (uint32_t)p.kv_heads + kvh) *
-                          (uint32_t)(2 * p.block_size);
-    const auto rvs = page_rsrc((const char*)p.v_scale + vrow);
-    const auto rvz = page_rsrc((const char*)p.v_zero + vrow);
-    ch.vs = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rvs, lo.vs, 2 * slot, kNT));
-    ch.vz = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rvz, lo.vs, 2 * slot, kNT));
+    // sequence hold garbage and are masked by selects, never multiplied)
+    const uint32_t so = (uint32_t)phys * B.vs_blk + 2 * slot;
+    ch.vs = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(B.vs, lo.vs, so, kNT));
+    ch.vz = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(B.vz, lo.vs, so, kNT));
     // K group scale/zero, stored with the group's first page `lead`
-    const uint64_t krow = ((uint64_t)(uint32_t)lead * (uint32_t)p.kv_heads + kvh) * 256u;
-    const auto rks = page_rsrc((const char*)p.k_scale + krow);
-    const auto rkz = page_rsrc((const char*)p.k_zero + krow);
-    ch.ks2 = __builtin_amdgcn_raw_buffer_load_b32(rks, lo.ks, 0, 0);
-    ch.kz2 = __builtin_amdgcn_raw_buffer_load_b32(rkz, lo.ks, 0, 0);
+    const uint32_t go = (uint32_t)lead * B.ks_blk;
+    ch.ks2 = __builtin_amdgcn_raw_buffer_load_b32(B.ks, lo.ks, go, 0);
+    ch.kz2 = __builtin_amdgcn_raw_buffer_load_b32(B.kz, lo.ks, go, 0);
 }
 
 // Half-row rotation: lane l reads lane (l & ~15) | ((l + 8) & 15), i.e. column n of a
@@ -250,93 +298,91 @@ __device__ __forceinline__ float ror8(float x) {
                                                       false));
 }
 
-// q' = q * s would lose 2^-12 relative per channel in fp16 - enough to move logits by
-// ~1e-3 on outlier channels - so it is kept as hi + lo: hi = fp16(q s) (v_pk_mul_f16),
-// lo = fma(q, s, -hi) rounded once (v_pk_fma_f16: q s - hi is exact).
-// C = sum q z / F - B * sum (hi + lo) (v_dot2_f32_f16).
-// SPLIT (at most 8 heads per kv head): the MFMA's 16 columns hold hi in column h and lo
-// in column h + 8, so one QK^T chain gives both parts (summed across the half rows
-// after the MFMAs); lanes of columns >= 8 take C = 0. Otherwise hi and lo run in two
-// chains over columns [0, G).
-// The group's scales (lane l holds channels 2l, 2l+1) pass through the wave's 512-byte
-// LDS slot `stage` to reach every lane in k-operand order; `qsh` points at the lane's
-// q in k-operand order (head l % 8 when SPLIT) in LDS, 64 h8 apart per k-step.
-template <int FMT, bool SPLIT>
+// INT8 / FP8 K rows (16 rows of 128 bytes, loaded 8 whole rows per instruction) to the
+// k-operand layout (lane (tok = l%16, g) holds bytes [64j + 16g, +16) of row tok) through
+// the wave's 2 KB LDS tile. 16-byte piece j of row r sits at slot j ^ (r >> 1): the row
+// writes (16 lanes = 2 rows x 8 pieces) and the operand reads (16 lanes = 16 rows, one
+// piece) each touch 16 distinct 16-byte slots modulo 256 bytes - no bank conflicts.
+__device__ __forceinline__ void kstage_q(const u4v* rows, char* kst, int g, u4v* kr) {
+    const int lane = __lane_id();
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int row = 8 * j + (lane >> 3);
+        *(u4v*)(kst + row * 128 + 16 * ((lane & 7) ^ (row >> 1))) = rows[j];
+    }
+    const int tok = lane & 15;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) kr[j] = *(const u4v*)(kst + tok * 128 + 16 * ((4 * j + g) ^ (tok >> 1)));
+}
+
+// The chunk's K codes in k-operand order.
+template <int FMT>
+__device__ __forceinline__ void k_operand(const ChunkQ<FMT>& ch, char* kst, int g,
+                                          u4v* kr) {
+    if constexpr (QFmt<FMT>::KLOADS == 2) {
+        kstage_q(ch.k, kst, g, kr);
+    } else {
+        kr[0] = ch.k[0];
+    }
+}
+
+// q'' = q * s / w of the K group whose scales lane l holds for channels 2l, 2l+1 (s2, z2),
+// as hi + lo fp16 parts: hi = fp16(q s') (v_pk_mul_f16), lo = fma(q, s', -hi) rounded once
+// (v_pk_fma_f16: q s' - hi is exact), s' = s / w. For INT4 the odd channels' s / 16 is
+// exact unless it falls below the fp16 normal range, where its error stays under 2^-25 -
+// at most 16 * 15 * 2^-25 |q| (about 7e-6 |q|) in the score. One fp16 rounding of q s
+// alone would move logits by ~1e-3 on outlier channels. The lane keeps the part `lo_part`
+// selects for the head whose q `qsh` points at (q in k-operand order in LDS, 64 h8 apart
+// per k-step). The scales pass through the wave's 512-byte LDS slot `stage` to reach every
+// lane in k-operand order (INT4: written there in the permuted order, two halves per
+// lane). Returns C = sum_d q_d z_d of that head (all 128 channels).
+template <int FMT>
 __device__ __forceinline__ float make_qprime(uint32_t s2, uint32_t z2, uint32_t* stage, int g,
-                                             const h8* qsh, h8* qhi, h8* qlo) {
+                                             const h8* qsh, bool lo_part, h8* val) {
     typedef QFmt<FMT> Q;
     const int lane = __lane_id();
-    const bool upper = SPLIT && (lane & 8);
-    stage[lane] = s2;
-    stage[64 + lane] = z2;
-    const _Float16* ss = (const _Float16*)stage;
-    const _Float16* zz = (const _Float16*)(stage + 64);
-    float qz = 0.f, qs = 0.f;
-    const h2 one = {(_Float16)1.f, (_Float16)1.f};
+    _Float16* ss = (_Float16*)stage;
+    _Float16* zz = (_Float16*)(stage + 64);
+    if constexpr (Q::permuted()) {
+        // channels 2l (even: w = 1) and 2l + 1 (odd: w = 16) of block l / 4 sit at k-order
+        // positions {0, 4, 1, 5}[l % 4] and {2, 6, 3, 7}[l % 4] of that block
+        h2 sv2 = __builtin_bit_cast(h2, s2);
+        sv2[1] *= (_Float16)0.0625f;
+        const h2 zv2 = __builtin_bit_cast(h2, z2);
+        const int j = lane & 3, blk = 8 * (lane >> 2);
+        const int p0 = blk + ((j & 2) ? 1 : 0) + 4 * (j & 1);
+        const int p1 = p0 + 2;
+        ss[p0] = sv2[0];
+        ss[p1] = sv2[1];
+        zz[p0] = zv2[0];
+        zz[p1] = zv2[1];
+    } else {
+        stage[lane] = s2;
+        stage[64 + lane] = z2;
+    }
+    float qz = 0.f;
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
-        h8 sv = *(const h8*)(ss + Q::chan_base(st, g));
-        h8 zv = *(const h8*)(zz + Q::chan_base(st, g));
-        if constexpr (Q::permuted()) {
-            sv = __builtin_shufflevector(sv, sv, 0, 4, 1, 5, 2, 6, 3, 7);
-            zv = __builtin_shufflevector(zv, zv, 0, 4, 1, 5, 2, 6, 3, 7);
-        }
+        const h8 sv = *(const h8*)(ss + Q::chan_base(st, g));
+        const h8 zv = *(const h8*)(zz + Q::chan_base(st, g));
         const h8 qv = qsh[64 * st];
         const h8 hi = qv * sv;
         const h8 lo = __builtin_elementwise_fma(qv, sv, -hi);
-        if constexpr (SPLIT) {
-            qhi[st] = upper ? lo : hi;
-        } else {
-            qhi[st] = hi;
-            qlo[st] = lo;
-        }
+        val[st] = lo_part ? lo : hi;
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
             const h2 qa = {qv[e], qv[e + 1]};
             const h2 za = {zv[e], zv[e + 1]};
-            const h2 ha = {hi[e], hi[e + 1]};
-            const h2 la = {lo[e], lo[e + 1]};
             qz = __builtin_amdgcn_fdot2(qa, za, qz, false);
-            qs = __builtin_amdgcn_fdot2(ha, one, qs, false);
-            qs = __builtin_amdgcn_fdot2(la, one, qs, false);
         }
     }
-    qz = rows_sum(qz);
-    qs = rows_sum(qs);
-    return upper ? 0.f : qz * (1.f / Q::F) - Q::B * qs;
+    return rows_sum(qz);
 }
 
-template <int FMT, bool MASK, bool SPLIT>
-__device__ __forceinline__ void chunk_q(const ChunkQ<FMT>& ch, const h8* qhi, const h8* qlo,
-                                        float cinit, float sl2f, int valid, int g,
-                                        SoftmaxState<128>& st, float& corr, I4Consts k4) {
-    typedef QFmt<FMT> Q;
-    float s2[4];
-    if constexpr (SPLIT) {
-        // one chain; column h + 8 holds the lo part of head h: s = C[h] + C[h + 8] in
-        // both lanes of the pair
-        f4 sc = (f4)cinit;
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(Q::kop(ch.k, k, k4), qhi[k], sc, 0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s2[r] = (sc[r] + ror8(sc[r])) * sl2f;
-    } else {
-        // hi and lo parts in two independent MFMA chains (half the dependent-chain latency)
-        f4 sh = (f4)cinit, sl = (f4)0.f;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const h8 kh = Q::kop(ch.k, k, k4);
-            sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qhi[k], sh, 0, 0, 0);
-            sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qlo[k], sl, 0, 0, 0);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s2[r] = (sh[r] + sl[r]) * sl2f;
-    }
-    if (MASK) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s2[r] = 4 * g + r < valid ? s2[r] : -INFINITY;
-    }
+// Online-softmax update of one lane for scores s2 (log2 domain, masked scores -inf):
+// rescales the state when a score passes the lazy reference max, returns p = 2^(s2 - m).
+__device__ __forceinline__ void softmax_step(float* s2, SoftmaxState<128>& st, float& corr,
+                                             float* pr) {
     const float lm = fmaxf(fmaxf(s2[0], s2[1]), fmaxf(s2[2], s2[3]));
     if (__builtin_amdgcn_ballot_w64(lm > st.m + kLazyMax) != 0) {  // rare: the max moved
         const float mn = fmaxf(st.m, rows_max(lm));
@@ -347,120 +393,242 @@ __device__ __forceinline__ void chunk_q(const ChunkQ<FMT>& ch, const h8* qhi, co
 #pragma unroll
         for (int t = 0; t < 8; ++t) st.acc[t] *= alpha;
     }
-    float pr[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(s2[r] - st.m);
     st.l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-    // p s_t feeds the MFMA as two fp16 parts, hi = fp16(p s_t) (fma with +0 is the
-    // product: p, s >= 0; v_fma_mix_f32 on the fp16 scale) and lo = fp16(p s_t - hi): one
-    // fp16 rounding of p s_t would be an error of up to 2^-11 (V - z) when one token
-    // dominates. corr accumulates p z (v_fma_mix_f32) and -F B (hi + lo) (exact
-    // products, v_dot2_f32_f16) in fp32.
-    h4 phi, plo;
+}
+
+// p s_t as hi + lo fp16 parts, hi = fp16(p s_t) (fma with +0 is the product: p, s >= 0;
+// v_fma_mix on the fp16 scale) and lo = fp16(p s_t - hi): one fp16 rounding of p s_t
+// would be an error of up to 2^-11 (V - z) when one token dominates. corr accumulates
+// p z_t in fp32. Rows r with !ok (past the sequence: garbage scales) give 0.
+template <bool MASK>
+__device__ __forceinline__ void pv_weights(const float* pr, h4 vs, h4 vz, int valid, int g,
+                                           h4& phi, h4& plo, float& corr) {
     float cadd = 0.f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const bool ok = !MASK || 4 * g + r < valid;
-        const float sv = (float)ch.vs[r];
+        const float sv = (float)vs[r];
         const _Float16 hi = (_Float16)__builtin_fmaf(pr[r], sv, 0.f);
         phi[r] = ok ? hi : (_Float16)0.f;
         plo[r] = ok ? (_Float16)__builtin_fmaf(pr[r], sv, -(float)hi) : (_Float16)0.f;
-        cadd = __builtin_fmaf(pr[r], ok ? (float)ch.vz[r] : 0.f, cadd);
-    }
-    if constexpr (Q::B != 0.f) {
-        const h2 fb = {(_Float16)(-Q::F * Q::B), (_Float16)(-Q::F * Q::B)};
-        cadd = __builtin_amdgcn_fdot2(__builtin_shufflevector(phi, phi, 0, 1), fb, cadd, false);
-        cadd = __builtin_amdgcn_fdot2(__builtin_shufflevector(phi, phi, 2, 3), fb, cadd, false);
-        cadd = __builtin_amdgcn_fdot2(__builtin_shufflevector(plo, plo, 0, 1), fb, cadd, false);
-        cadd = __builtin_amdgcn_fdot2(__builtin_shufflevector(plo, plo, 2, 3), fb, cadd, false);
+        cadd = __builtin_fmaf(pr[r], ok ? (float)vz[r] : 0.f, cadd);
     }
     corr += cadd;
-    // V^T operands: tiles t of token pairs (0,1) and (2,3).
-    uint32_t a01[8], a23[8];
-    if constexpr (FMT == KVQ_KV_INT4) {
-        QFmt<KVQ_KV_INT4>::vpair_half(ch.v[0][0], ch.v[1][0], 0x05040100u, a01, k4);
-        QFmt<KVQ_KV_INT4>::vpair_half(ch.v[0][0], ch.v[1][0], 0x07060302u, a01 + 4, k4);
-        QFmt<KVQ_KV_INT4>::vpair_half(ch.v[2][0], ch.v[3][0], 0x05040100u, a23, k4);
-        QFmt<KVQ_KV_INT4>::vpair_half(ch.v[2][0], ch.v[3][0], 0x07060302u, a23 + 4, k4);
-    } else {
+}
+
+// One chunk, 5 to 16 q heads per kv head (decode_q_kernel). SPLIT (at most 8 heads): the
+// MFMA's 16 columns hold hi in column h and lo in column h + 8, so one QK^T chain gives
+// both parts (summed across the half rows after the MFMAs) and one PV chain takes p''
+// hi / lo the same way. Otherwise hi and lo run in two chains over columns [0, G).
+template <int FMT, bool MASK, bool SPLIT>
+__device__ __forceinline__ void chunk_q(const ChunkQ<FMT>& ch, const h8* qhi, const h8* qlo,
+                                        float csl, float sl2f, int valid, int g, char* kst,
+                                        SoftmaxState<128>& st, float& corr) {
+    typedef QFmt<FMT> Q;
+    u4v kr[Q::KLOADS];
+    k_operand<FMT>(ch, kst, g, kr);
+    float s2[4];
+    if constexpr (SPLIT) {
+        f4 sc = (f4)0.f;
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            Q::vpair(ch.v[0][k], ch.v[1][k], a01 + 4 * k);
-            Q::vpair(ch.v[2][k], ch.v[3][k], a23 + 4 * k);
+        for (int k = 0; k < 4; ++k)
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(Q::kop(kr, k), qhi[k], sc, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s2[r] = __builtin_fmaf(sc[r] + ror8(sc[r]), sl2f, csl);
+    } else {
+        // hi and lo parts in two independent MFMA chains (half the dependent-chain latency)
+        f4 sh = (f4)0.f, sl = (f4)0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const h8 kh = Q::kop(kr, k);
+            sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qhi[k], sh, 0, 0, 0);
+            sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qlo[k], sl, 0, 0, 0);
         }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s2[r] = __builtin_fmaf(sh[r] + sl[r], sl2f, csl);
     }
+    if (MASK) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s2[r] = 4 * g + r < valid ? s2[r] : -INFINITY;
+    }
+    float pr[4];
+    softmax_step(s2, st, corr, pr);
+    h4 phi, plo;
+    pv_weights<MASK>(pr, ch.vs, ch.vz, valid, g, phi, plo, corr);
+    uint32_t a01[8], a23[8];
+    Q::vtiles(ch.v, a01, a23);
     if constexpr (SPLIT) {
         // column h takes p hi, column h + 8 p lo (the lanes of a pair hold the same p)
         const h4 pop = (__lane_id() & 8) ? plo : phi;
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             u2 w = {a01[t], a23[t]};
-            const h4 a = __builtin_bit_cast(h4, w);
-            st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pop, st.acc[t], 0, 0, 0);
+            st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, w), pop,
+                                                               st.acc[t], 0, 0, 0);
         }
     } else {
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             u2 w = {a01[t], a23[t]};
-            const h4 a = __builtin_bit_cast(h4, w);
-            st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, phi, st.acc[t], 0, 0, 0);
+            st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, w), phi,
+                                                               st.acc[t], 0, 0, 0);
         }
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             u2 w = {a01[t], a23[t]};
-            const h4 a = __builtin_bit_cast(h4, w);
-            st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, plo, st.acc[t], 0, 0, 0);
+            st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, w), plo,
+                                                               st.acc[t], 0, 0, 0);
         }
+    }
+}
+
+// A chunk pair (chunks a, b) of one K group, 1 to 4 q heads per kv head
+// (decode_q2_kernel). `slot` = the lane column's chunk (0: a, 1: b). Both chunks' QK
+// products run against the same q'' operand (column j: head j & 3, part j >> 3) into two
+// accumulators; each column keeps its own chunk's. csl = C * scale * log2 e of the group.
+// MASK: tokens at or past valid_a / valid_b of their chunk are masked (valid_b = 0: no
+// second chunk).
+template <int FMT, bool MASK>
+__device__ __forceinline__ void chunk_pair(const ChunkQ<FMT>& ca, const ChunkQ<FMT>& cb,
+                                           const h8* qv, float csl, float sl2f, int valid_a,
+                                           int valid_b, int g, int slot, bool lo_part,
+                                           char* kst, SoftmaxState<128>& st, float& corr) {
+    typedef QFmt<FMT> Q;
+    f4 sa = (f4)0.f, sb = (f4)0.f;
+    {
+        u4v kr[Q::KLOADS];
+        k_operand<FMT>(ca, kst, g, kr);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(Q::kop(kr, k), qv[k], sa, 0, 0, 0);
+        k_operand<FMT>(cb, kst, g, kr);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(Q::kop(kr, k), qv[k], sb, 0, 0, 0);
+    }
+    float s2[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float x = slot ? sb[r] : sa[r];
+        s2[r] = __builtin_fmaf(x + ror8(x), sl2f, csl);
+    }
+    const int valid = slot ? valid_b : valid_a;
+    if (MASK) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s2[r] = 4 * g + r < valid ? s2[r] : -INFINITY;
+    }
+    float pr[4];
+    softmax_step(s2, st, corr, pr);
+    const u2 vs2 = slot ? __builtin_bit_cast(u2, cb.vs) : __builtin_bit_cast(u2, ca.vs);
+    const u2 vz2 = slot ? __builtin_bit_cast(u2, cb.vz) : __builtin_bit_cast(u2, ca.vz);
+    h4 phi, plo;
+    pv_weights<MASK>(pr, __builtin_bit_cast(h4, vs2), __builtin_bit_cast(h4, vz2), valid, g, phi,
+                     plo, corr);
+    // B operand: k-slots 8g + r (chunk a's token 4g + r) and 8g + 4 + r (chunk b's); the
+    // lane's p in its chunk's half, zeros in the other
+    const u2 pw = __builtin_bit_cast(u2, lo_part ? plo : phi);
+    u4v pbw;
+    pbw[0] = slot ? 0u : pw[0];
+    pbw[1] = slot ? 0u : pw[1];
+    pbw[2] = slot ? pw[0] : 0u;
+    pbw[3] = slot ? pw[1] : 0u;
+    const h8 pb = __builtin_bit_cast(h8, pbw);
+    uint32_t a01[8], a23[8], b01[8], b23[8];
+    Q::vtiles(ca.v, a01, a23);
+    Q::vtiles(cb.v, b01, b23);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const u4v w = {a01[t], a23[t], b01[t], b23[t]};
+        st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, w), pb,
+                                                           st.acc[t], 0, 0, 0);
+    }
+}
+
+// INT4 V tiles hold odd codes at 2^-20 (w = 16): their accumulators carry F / 16.
+template <int FMT>
+__device__ __forceinline__ void tile_weights(SoftmaxState<128>& st) {
+    if constexpr (FMT == KVQ_KV_INT4) {
+#pragma unroll
+        for (int t = 1; t < 8; t += 2) st.acc[t] *= 0.0625f;
+    }
+}
+
+// Writes q in this format's k-operand order (zero for heads >= G) to LDS for the
+// once-per-K-group q'' products: [4 k-steps][64 lanes] h8, lane (g, head i16).
+template <int FMT>
+__device__ __forceinline__ void stage_q(const DecodeParams& p, int b, int kvh, int i16, int g,
+                                        h8* qsh) {
+    typedef QFmt<FMT> Q;
+    const int G = p.group;
+    const bool head_ok = i16 < G;
+    const _Float16* qrow = (const _Float16*)p.q + (int64_t)b * p.q_sb +
+                           (int64_t)(kvh * G + (head_ok ? i16 : 0)) * p.q_sh;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        h8 x = *(const h8*)(qrow + Q::chan_base(st, g));
+        if constexpr (Q::permuted()) x = __builtin_shufflevector(x, x, 0, 4, 1, 5, 2, 6, 3, 7);
+        qsh[64 * st + __lane_id()] = head_ok ? x : (h8)(_Float16)0;
     }
 }
 
 // P-deep register ring: chunk c + P is loaded while chunk c computes, the block-table
 // entries of chunks c + 2P .. c + 3P - 1 meanwhile. Every chunk carries its own K group's
-// scales, so any group size works with any P.
+// scales, so any group size works with any P. 5 to 16 q heads per kv head.
 template <int FMT, int W, bool FINAL, int P, bool SPLIT>
 __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) {
     typedef QFmt<FMT> Q;
     constexpr int D = 128, DV = 8;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int kvh = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
+    const WgCoord wc = wg_coord(p, FINAL ? 1 : p.num_splits);
+    if (!wc.live) return;
+    const int kvh = wc.kvh, split = wc.split, b = wc.b;
     const int i16 = lane & 15, g = lane >> 4;
     const int G = p.group;
-    const bool head_ok = i16 < G;
     const WaveRange wr = wave_range<W>(p, b, split, wave);
     const int seq_len = wr.seq_len, w_lo = wr.w_lo, w_hi = wr.w_hi;
     const int kgs = p.k_group_shift;  // log2 of 16-token chunks per K group
-    const I4Consts k4 = i4_consts();
+    const QBase base = q_base(p, kvh);
 
-    // q in this format's k-operand order (zero for padded heads), kept in LDS for the
-    // once-per-K-group q' products: [4 k-steps][64 lanes] h8, written by wave 0.
+    // LDS: [region 0][K-scale slots, 512 B per wave][q, 4 KB] (launch_q). Region 0 holds
+    // the cross-wave combine after the chunk loop and, before it, the INT8 / FP8 waves'
+    // 2 KB K tiles.
     extern __shared__ float smem[];
-    h8* qsh = (h8*)(smem + W * G * D + 2 * W * 16 + W * 128);
-    if (wave == 0) {
-        const _Float16* qrow = (const _Float16*)p.q + (int64_t)b * p.q_sb +
-                               (int64_t)(kvh * G + (head_ok ? i16 : 0)) * p.q_sh;
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            h8 x = *(const h8*)(qrow + Q::chan_base(st, g));
-            if constexpr (Q::permuted()) x = __builtin_shufflevector(x, x, 0, 4, 1, 5, 2, 6, 3, 7);
-            qsh[64 * st + lane] = head_ok ? x : (h8)(_Float16)0;
-        }
-    }
+    const int r0 = quant_lds_region0(W, G, FMT);
+    char* kst = (char*)smem + wave * 2048;
+    h8* qsh = (h8*)(smem + r0 + W * 128);
+    if (wave == 0) stage_q<FMT>(p, b, kvh, i16, g, qsh);
     __syncthreads();
     qsh += SPLIT ? (lane & ~8) : lane;  // SPLIT: columns h and h + 8 read head h
 
     SoftmaxState<D> st;
 #pragma unroll
     for (int t = 0; t < DV; ++t) st.acc[t] = (f4)0.f;
-    st.m = -INFINITY;
+    st.m = kM0;
     st.l = 0.f;
-    float corr = 0.f, cinit = 0.f;
-    const float sl2f = p.scale_log2 * Q::F;
-    h8 qhi[4], qlo[SPLIT ? 1 : 4];
+    float corr = 0.f, csl = 0.f;
+    const float sl2 = p.scale_log2, sl2f = sl2 * Q::F;
+    h8 qhi[4], qlo[4];
+    const bool upper = SPLIT && (lane & 8);
 
+    uint32_t* stage = (uint32_t*)(smem + r0) + wave * 128;
     auto valid_of = [&](int c) { return min(seq_len - (c << 4), 16); };
+    // q'' of chunk ch's K group into the operands (hi / lo by column in SPLIT; both chains
+    // otherwise) and C * scale * log2 e into csl
+    auto new_group = [&](const ChunkQ<FMT>& ch) {
+        h8 v[4];
+        if constexpr (SPLIT) {
+            csl = make_qprime<FMT>(ch.ks2, ch.kz2, stage, g, qsh, upper, v) * sl2;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) qhi[k] = v[k];
+        } else {
+            csl = make_qprime<FMT>(ch.ks2, ch.kz2, stage, g, qsh, false, qhi) * sl2;
+            make_qprime<FMT>(ch.ks2, ch.kz2, stage, g, qsh, true, qlo);
+        }
+    };
 
-    uint32_t* stage = (uint32_t*)(smem + W * G * D + 2 * W * 16) + wave * 128;
     // The ring covers the wave's fully valid chunks [w_lo, r_hi); the sequence's partial
     // last chunk (at most one per sequence) is handled once after it. Every load in the
     // ring is issued on every path (chunks past r_hi - 1 re-read chunk r_hi - 1 and are
@@ -477,7 +645,7 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
         // ring's waits (vmcnt counts the loads issued after the awaited one) drain it.
 #pragma unroll
         for (int i = 0; i < P; ++i) {
-            load_chunk_q<FMT>(p, kvh, min(w_lo + i, last), lo,
+            load_chunk_q<FMT>(base, min(w_lo + i, last), lo,
                               __builtin_amdgcn_readlane(pg_cur, i),
                               __builtin_amdgcn_readlane(pg_cur, P + i), ring[i]);
             __builtin_amdgcn_sched_barrier(0);
@@ -489,11 +657,10 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
             for (int i = 0; i < P; ++i) {
                 const int c = c0 + i;
                 if (c < r_hi) {
-                    if (c == w_lo || (c & gmask) == 0)
-                        cinit = make_qprime<FMT, SPLIT>(ring[i].ks2, ring[i].kz2, stage, g, qsh, qhi, qlo);
-                    chunk_q<FMT, false, SPLIT>(ring[i], qhi, qlo, cinit, sl2f, 16, g, st, corr, k4);
+                    if (c == w_lo || (c & gmask) == 0) new_group(ring[i]);
+                    chunk_q<FMT, false, SPLIT>(ring[i], qhi, qlo, csl, sl2f, 16, g, kst, st, corr);
                 }
-                load_chunk_q<FMT>(p, kvh, min(c + P, last), lo,
+                load_chunk_q<FMT>(base, min(c + P, last), lo,
                                   __builtin_amdgcn_readlane(pg_cur, i),
                                   __builtin_amdgcn_readlane(pg_cur, P + i), ring[i]);
             }
@@ -504,11 +671,10 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
         const int valid = valid_of(c);
         const int pg = chunk_pages<1>(p, b, c, c, kgs);
         ChunkQ<FMT> ch;
-        load_chunk_q<FMT>(p, kvh, c, lane_offsets<FMT>(p, i16, g, valid - 1),
+        load_chunk_q<FMT>(base, c, lane_offsets<FMT>(p, i16, g, valid - 1),
                           __builtin_amdgcn_readlane(pg, 0), __builtin_amdgcn_readlane(pg, 1), ch);
-        if (c == w_lo || (c & gmask) == 0)
-            cinit = make_qprime<FMT, SPLIT>(ch.ks2, ch.kz2, stage, g, qsh, qhi, qlo);
-        chunk_q<FMT, true, SPLIT>(ch, qhi, qlo, cinit, sl2f, valid, g, st, corr, k4);
+        if (c == w_lo || (c & gmask) == 0) new_group(ch);
+        chunk_q<FMT, true, SPLIT>(ch, qhi, qlo, csl, sl2f, valid, g, kst, st, corr);
     }
 
     if constexpr (SPLIT) {  // add the lo columns into the hi columns
@@ -517,49 +683,190 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
 #pragma unroll
             for (int r = 0; r < 4; ++r) st.acc[t][r] += ror8(st.acc[t][r]);
     }
+    tile_weights<FMT>(st);
+    if constexpr (Q::KLOADS == 2) __syncthreads();  // every wave is done with its K tile
     combine_store<D, W, FINAL>(p, st.acc, Q::F, rows_sum(corr), st.m, rows_sum(st.l), wave, i16,
                                g, kvh, split, b);
 }
 
+// Chunk pairs, 1 to 4 q heads per kv head, K groups of at least 2 chunks. Pairs are
+// (2i, 2i + 1) in absolute chunk index, so both chunks of a pair share their K group; a
+// wave's odd leading chunk, odd trailing full chunk and the sequence's partial last chunk
+// run as single-chunk steps. P-deep ring over the pairs (P = 4 or 8 chunks: while a pair
+// computes, P - 2 chunks are in flight); the ring depth never changes the arithmetic.
+template <int FMT, int W, bool FINAL, int P>
+__global__ __launch_bounds__(W * 64) void decode_q2_kernel(const DecodeParams p) {
+    static_assert(P == 4 || P == 8, "a pair computes while P - 2 chunks are in flight");
+    typedef QFmt<FMT> Q;
+    constexpr int D = 128, DV = 8;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const WgCoord wc = wg_coord(p, FINAL ? 1 : p.num_splits);
+    if (!wc.live) return;
+    const int kvh = wc.kvh, split = wc.split, b = wc.b;
+    const int i16 = lane & 15, g = lane >> 4;
+    const int G = p.group;
+    const int slot = (i16 >> 2) & 1;   // the column's chunk of the pair
+    const bool lo_part = i16 >= 8;     // the column holds the lo parts
+    const WaveRange wr = wave_range<W>(p, b, split, wave);
+    const int seq_len = wr.seq_len, w_lo = wr.w_lo, w_hi = wr.w_hi;
+    const int kgs = p.k_group_shift;
+    const QBase base = q_base(p, kvh);
+
+    extern __shared__ float smem[];
+    const int r0 = quant_lds_region0(W, G, FMT);
+    char* kst = (char*)smem + wave * 2048;
+    h8* qsh = (h8*)(smem + r0 + W * 128);
+    if (wave == 0) stage_q<FMT>(p, b, kvh, i16, g, qsh);
+    __syncthreads();
+    qsh += (lane & 48) | (lane & 3);  // column j reads head j & 3
+    uint32_t* stage = (uint32_t*)(smem + r0) + wave * 128;
+
+    SoftmaxState<D> st;
+#pragma unroll
+    for (int t = 0; t < DV; ++t) st.acc[t] = (f4)0.f;
+    st.m = kM0;
+    st.l = 0.f;
+    float corr = 0.f, csl = 0.f;
+    const float sl2 = p.scale_log2, sl2f = sl2 * Q::F;
+    h8 qv[4];
+    int gq = -1;  // the K group whose q'' qv holds
+
+    auto group = [&](const ChunkQ<FMT>& ch, int gi) {
+        if (gi != gq) {
+            csl = make_qprime<FMT>(ch.ks2, ch.kz2, stage, g, qsh, lo_part, qv) * sl2;
+            gq = gi;
+        }
+    };
+    // chunk c alone (in the first chunk's columns), its first `valid` tokens
+    auto single = [&](int c, int valid) {
+        const int pg = chunk_pages<1>(p, b, c, c, kgs);
+        ChunkQ<FMT> ch;
+        load_chunk_q<FMT>(base, c, lane_offsets<FMT>(p, i16, g, valid - 1),
+                          __builtin_amdgcn_readlane(pg, 0), __builtin_amdgcn_readlane(pg, 1), ch);
+        group(ch, c >> kgs);
+        chunk_pair<FMT, true>(ch, ch, qv, csl, sl2f, valid, 0, g, slot, lo_part, kst, st, corr);
+    };
+
+    const int r_hi = min(w_hi, wr.c_full);  // fully valid chunks [w_lo, r_hi)
+    int c_first = w_lo;
+    if ((w_lo & 1) && w_lo < r_hi) {
+        single(w_lo, 16);
+        c_first = w_lo + 1;
+    }
+    // pairs [c_first, e_hi); an empty wave or split has r_hi < w_lo and runs nothing
+    const int e_hi = c_first + (max(r_hi - c_first, 0) & ~1);
+    if (c_first < e_hi) {
+        const QLaneOff lo = lane_offsets<FMT>(p, i16, g, 15);
+        const int last = e_hi - 1;
+        ChunkQ<FMT> ring[P];
+        int pg_cur = chunk_pages<P>(p, b, c_first, last, kgs);
+        int pg_nxt = chunk_pages<P>(p, b, c_first + P, last, kgs);
+        // Issued slot by slot: a slot's loads moved behind a later slot's would make the
+        // ring's waits (vmcnt counts the loads issued after the awaited one) drain it.
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            load_chunk_q<FMT>(base, min(c_first + i, last), lo,
+                              __builtin_amdgcn_readlane(pg_cur, i),
+                              __builtin_amdgcn_readlane(pg_cur, P + i), ring[i]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        for (int c0 = c_first; c0 < e_hi; c0 += P) {
+            pg_cur = pg_nxt;
+            pg_nxt = chunk_pages<P>(p, b, c0 + 2 * P, last, kgs);
+#pragma unroll
+            for (int i = 0; i < P; i += 2) {
+                const int c = c0 + i;
+                if (c < e_hi) {
+                    group(ring[i], c >> kgs);
+                    chunk_pair<FMT, false>(ring[i], ring[i + 1], qv, csl, sl2f, 16, 16, g, slot,
+                                           lo_part, kst, st, corr);
+                }
+#pragma unroll
+                for (int j = i; j < i + 2; ++j)
+                    load_chunk_q<FMT>(base, min(c0 + j + P, last), lo,
+                                      __builtin_amdgcn_readlane(pg_cur, j),
+                                      __builtin_amdgcn_readlane(pg_cur, P + j), ring[j]);
+            }
+        }
+    }
+    if (e_hi < r_hi) single(e_hi, 16);
+    if (w_lo <= r_hi && r_hi < w_hi)  // this wave owns the partial last chunk c_full
+        single(r_hi, min(seq_len - (r_hi << 4), 16));
+
+    // hi + lo columns, then the two chunk streams of each head (columns j, j ^ 4)
+#pragma unroll
+    for (int t = 0; t < DV; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) st.acc[t][r] += ror8(st.acc[t][r]);
+    {
+        const float m_o = __shfl_xor(st.m, 4), l_o = __shfl_xor(st.l, 4);
+        const float c_o = __shfl_xor(corr, 4);
+        const float M = fmaxf(st.m, m_o);
+        const float wa = fast_exp2(st.m - M), wb = fast_exp2(m_o - M);
+        st.l = wa * st.l + wb * l_o;
+        corr = wa * corr + wb * c_o;
+#pragma unroll
+        for (int t = 0; t < DV; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                st.acc[t][r] = wa * st.acc[t][r] + wb * __shfl_xor(st.acc[t][r], 4);
+        st.m = M;
+    }
+    tile_weights<FMT>(st);
+    if constexpr (Q::KLOADS == 2) __syncthreads();  // every wave is done with its K tile
+    combine_store<D, W, FINAL>(p, st.acc, Q::F, rows_sum(corr), st.m, rows_sum(st.l), wave, i16,
+                               g, kvh, split, b);
+}
+
+// LDS: region 0 (the cross-wave combine, or the INT8 / FP8 K tiles), one 512-byte K-scale
+// slot per wave, then q in k-operand order (4 KB)
+template <int W>
+static size_t q_shmem(const DecodeParams& p, int fmt) {
+    return sizeof(float) * (quant_lds_region0(W, p.group, fmt) + W * 128) + 4096;
+}
+
 template <int FMT, int W, bool FINAL, int P, bool SPLIT>
 static hipError_t launch_q(const DecodeParams& p, hipStream_t stream) {
-    const dim3 grid(p.kv_heads, FINAL ? 1 : p.num_splits, p.batch);
-    // cross-wave combine ([W][G][128] + [W][16] m, l), one 512-byte K-scale slot per wave,
-    // then q in k-operand order (4 KB)
-    const size_t shmem = sizeof(float) * (W * p.group * 128 + 2 * W * 16 + W * 128) + 4096;
-    hipLaunchKernelGGL((decode_q_kernel<FMT, W, FINAL, P, SPLIT>), grid, dim3(W * 64), shmem,
-                       stream, p);
+    const dim3 grid(decode_grid(p.kv_heads, FINAL ? 1 : p.num_splits, p.batch));
+    hipLaunchKernelGGL((decode_q_kernel<FMT, W, FINAL, P, SPLIT>), grid, dim3(W * 64),
+                       q_shmem<W>(p, FMT), stream, p);
     return hipGetLastError();
 }
 
-// Up to 8 heads per kv head: hi / lo parts in the two column halves of one MFMA chain,
-// any ring depth. 9 to 16 heads: two chains, ring depth 4.
-template <int FMT, bool FINAL, int P>
-static hipError_t launch_q_w(const DecodeParams& p, int waves, hipStream_t stream) {
-    if (p.group > 8) {
-        switch (waves) {
-            case 1: return launch_q<FMT, 1, FINAL, 4, false>(p, stream);
-            case 2: return launch_q<FMT, 2, FINAL, 4, false>(p, stream);
-            case 4: return launch_q<FMT, 4, FINAL, 4, false>(p, stream);
-            case 8: return launch_q<FMT, 8, FINAL, 4, false>(p, stream);
-            default: return hipErrorInvalidValue;
-        }
-    }
-    switch (waves) {
-        case 1: return launch_q<FMT, 1, FINAL, P, true>(p, stream);
-        case 2: return launch_q<FMT, 2, FINAL, P, true>(p, stream);
-        case 4: return launch_q<FMT, 4, FINAL, P, true>(p, stream);
-        case 8: return launch_q<FMT, 8, FINAL, P, true>(p, stream);
+template <int FMT, int W, bool FINAL, int P>
+static hipError_t launch_q2(const DecodeParams& p, hipStream_t stream) {
+    const dim3 grid(decode_grid(p.kv_heads, FINAL ? 1 : p.num_splits, p.batch));
+    hipLaunchKernelGGL((decode_q2_kernel<FMT, W, FINAL, P>), grid, dim3(W * 64),
+                       q_shmem<W>(p, FMT), stream, p);
+    return hipGetLastError();
+}
+
+// 1 to 4 heads per kv head and K groups of at least 2 chunks: chunk pairs, ring 1 or 2 ->
+// 4 chunks, 4 -> 8. Up to 8 heads otherwise: hi / lo parts in the two column halves of
+// one MFMA chain, any ring depth. 9 to 16 heads: two chains, ring depth 4.
+template <int FMT, bool FINAL, int W>
+static hipError_t launch_q_g(const DecodeParams& p, int ring, hipStream_t stream) {
+    if (p.group <= 4 && p.k_group_chunks >= 2)
+        return ring == 4 ? launch_q2<FMT, W, FINAL, 8>(p, stream)
+                         : launch_q2<FMT, W, FINAL, 4>(p, stream);
+    if (p.group > 8) return launch_q<FMT, W, FINAL, 4, false>(p, stream);
+    switch (ring) {
+        case 1: return launch_q<FMT, W, FINAL, 1, true>(p, stream);
+        case 2: return launch_q<FMT, W, FINAL, 2, true>(p, stream);
+        case 4: return launch_q<FMT, W, FINAL, 4, true>(p, stream);
         default: return hipErrorInvalidValue;
     }
 }
 
 template <int FMT, bool FINAL>
-static hipError_t launch_q_p(const DecodeParams& p, int waves, int ring, hipStream_t stream) {
-    switch (ring) {
-        case 1: return launch_q_w<FMT, FINAL, 1>(p, waves, stream);
-        case 2: return launch_q_w<FMT, FINAL, 2>(p, waves, stream);
-        case 4: return launch_q_w<FMT, FINAL, 4>(p, waves, stream);
+static hipError_t launch_q_w(const DecodeParams& p, int waves, int ring, hipStream_t stream) {
+    if (ring != 1 && ring != 2 && ring != 4) return hipErrorInvalidValue;
+    switch (waves) {
+        case 1: return launch_q_g<FMT, FINAL, 1>(p, ring, stream);
+        case 2: return launch_q_g<FMT, FINAL, 2>(p, ring, stream);
+        case 4: return launch_q_g<FMT, FINAL, 4>(p, ring, stream);
+        case 8: return launch_q_g<FMT, FINAL, 8>(p, ring, stream);
         default: return hipErrorInvalidValue;
     }
 }
@@ -567,8 +874,8 @@ static hipError_t launch_q_p(const DecodeParams& p, int waves, int ring, hipStre
 template <int FMT>
 static hipError_t launch_q_f(const DecodeParams& p, bool final_out, int waves, int ring,
                              hipStream_t stream) {
-    return final_out ? launch_q_p<FMT, true>(p, waves, ring, stream)
-                     : launch_q_p<FMT, false>(p, waves, ring, stream);
+    return final_out ? launch_q_w<FMT, true>(p, waves, ring, stream)
+                     : launch_q_w<FMT, false>(p, waves, ring, stream);
 }
 
 hipError_t launch_decode_q(const DecodeParams& p, int kv_format, int head_dim, bool final_out,

@@ -43,6 +43,15 @@ struct DecodeParams {
 hipError_t launch_decode(const DecodeParams& p, int kv_format, int head_dim, bool final_out,
                          int waves_per_group, int pipeline, hipStream_t stream);
 
+// Floats of LDS region 0 of the quantized decode kernel (decode_q.hip) with `waves` waves
+// per workgroup: the cross-wave combine ([waves][group][128] accumulators + [waves][16] m
+// and l), or the INT8 / FP8 waves' 2 KB K tiles if larger (they use it before the combine).
+__host__ __device__ inline int quant_lds_region0(int waves, int group, int kv_format) {
+    const int combine = waves * group * 128 + 2 * waves * 16;
+    const int tiles = kv_format == KVQ_KV_INT4 ? 0 : waves * 512;
+    return combine > tiles ? combine : tiles;
+}
+
 // Quantized formats (decode_q.hip); head_dim 128 only.
 // `ring` = chunks of loads in flight per wave: 1, 2 or 4.
 hipError_t launch_decode_q(const DecodeParams& p, int kv_format, int head_dim, bool final_out,

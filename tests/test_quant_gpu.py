@@ -106,11 +106,12 @@ def test_decode_matches_fp32_attention_over_dequantized_cache(fmt, bs, num_split
 
 @pytest.mark.parametrize("fmt", FORMATS)
 def test_decode_group8_and_mqa_heads(fmt):
-    """Other GQA groups over a quantized cache: 8 q heads per kv head, MQA, and 16 q heads
-    per kv head (past 8 the kernel runs its two-chain variant)."""
+    """Other GQA groups over a quantized cache: 1, 2 and 3 q heads per kv head (the
+    chunk-pair kernel with padded head columns), 5 and 8 (one QK chain with hi / lo
+    columns), MQA, and 16 (two chains)."""
     from kvq_decode_amd import paged_decode_attention
     from kvq_decode_amd.quant import quantize_paged_cache
-    for Hq, Hkv in ((16, 2), (8, 1), (32, 2)):
+    for Hq, Hkv in ((8, 8), (4, 2), (6, 2), (10, 2), (16, 2), (8, 1), (32, 2)):
         q, kc, vc, bt, sl = make([700, 3], 16, Hq=Hq, Hkv=Hkv, seed=2)
         qc = quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt)
         host = {n: getattr(qc, n).cpu().numpy() for n in
