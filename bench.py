@@ -279,12 +279,20 @@ def _pmc_means(csv_dir, name_has):
     return sum(vals.values()) / len(vals), len(vals)
 
 
+def stage1_kernel(fmt_name, group=HQ // HKV):
+    """Name of the stage-1 kernel for a format: decode_f16_kernel, or for quantized
+    caches decode_q2_kernel (1 to 4 q heads per kv head) / decode_q_kernel."""
+    if fmt_name == "fp16":
+        return "decode_f16_kernel"
+    return "decode_q2_kernel" if group <= 4 else "decode_q_kernel"
+
+
 def traffic_summary(config, pmc_dir):
     """Writes profiles/decode_split_<config>_traffic.txt from four rocprofv3 --pmc runs
     under pmc_dir: copy_fetch/, copy_write/ (calibrate_copy) and fetch/, write/
     (profile_run). Counter values are scaled by the copy's known bytes per counter unit."""
     B, ctx, pool, fmt_name, desc = CONFIGS[config]
-    kernel = "decode_f16_kernel" if fmt_name == "fp16" else "decode_q_kernel"
+    kernel = stage1_kernel(fmt_name)
     cf, _ = _pmc_means(os.path.join(pmc_dir, "copy_fetch"), "copy")
     cw, _ = _pmc_means(os.path.join(pmc_dir, "copy_write"), "copy")
     kf, n = _pmc_means(os.path.join(pmc_dir, "fetch"), kernel)
@@ -363,7 +371,7 @@ def run_config(config, steps, warmup, splits=None, waves=0, pipeline=0, flushed=
         f"{stage1_ms * 1e3:.1f} us" + (f", flushed median {flushed_ms * 1e3:.1f} us" if flushed else ""))
     tbs = nbytes / (wall_ms * 1e-3) / 1e12
     achieved = nbytes / (stage1_ms * 1e-3) / 1e9
-    kernel = "decode_f16_kernel" if fmt_name == "fp16" else "decode_q_kernel"
+    kernel = stage1_kernel(fmt_name)
     res = {
         "value": round(tbs, 4), "ms_per_step": round(wall_ms, 5),
         "us_per_step": round(wall_ms * 1e3, 2),
@@ -460,7 +468,7 @@ def main():
         result = {"metric": METRIC, "value": res.pop("value"), "unit": "TB/s", "n_gpus": 1,
                   "steps": args.steps, "warmup": args.warmup, **res,
                   "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-                  "dtype": "fp16",
+                  "dtype": CONFIGS[name][3],
                   "data": "synthetic: q, K, V ~ N(0,1) fp16 (quantized configs: K with 4 "
                           "outlier channels x10 per kv head), random-permutation block "
                           "table, seed 0"}

@@ -93,9 +93,10 @@ typedef struct kvq_decode_args {
     const void* v_zero;
     int32_t waves_per_group;  /* tuning: waves per (kv head, split) workgroup, one of
                                  1, 2, 4, 8, 16; 0 = the library's choice */
-    int32_t pipeline;         /* tuning: 16-token chunks of loads in flight per wave:
-                                 fp16 1 or 2, quantized 1, 2 or 4 (more chunks in flight,
-                                 fewer waves per SIMD); 0 = the library's choice */
+    int32_t pipeline;         /* tuning: depth of the load ring in 16-token chunks, 1, 2
+                                 or 4 (fp16 head_dim 256: 1 or 2); deeper rings keep more
+                                 loads in flight with fewer waves per SIMD; 0 = the
+                                 library's choice (2) */
 } kvq_decode_args;
 
 /* Library version string, e.g. "kvq 0.1.0 gfx950". */
@@ -117,15 +118,18 @@ int kvq_choose_num_splits(int32_t batch, int32_t kv_heads, int32_t block_size,
  * heuristic above (triton_fp16.py:175-180) on this hardware. It sizes the decomposition
  * in waves, because a workgroup here holds several waves that combine through LDS:
  *   per_pair = pow2_floor(T * cu_count / (batch * kv_heads)), T = 2 waves per CU (fp16)
- *              or 8 (quantized), raised to pow2_floor(cdiv(chunks, C)) (C = 512 chunks per wave
- *              for fp16, 64 for quantized; uneven sequence lengths then still balance),
- *              capped at pow2_floor(chunks / 4); chunks = max_pages * block_size / 16
- *   waves = min(Wmax, per_pair) with Wmax = 2 (fp16) or 4 (quantized),
+ *              or 4 (quantized), raised to pow2_floor(cdiv(chunks, C)) (C = 512 chunks per
+ *              wave for fp16; quantized 256, or 64 when batch * kv_heads > cu_count, so that
+ *              uneven sequence lengths still balance), capped at pow2_floor(chunks / 4);
+ *              chunks = max_pages * block_size / 16
+ *   waves = min(Wmax, per_pair) with Wmax = 2 (fp16) or 1 (quantized),
  *   splits = per_pair / waves
  * fp16 streams fastest with about 2 waves per CU, each 2 chunks (16 KB) ahead, spread
- * over at least one workgroup per CU; more waves in flight lower the achieved bandwidth
- * (measured on MI355X for batch 1..16 and 32k..128k contexts). Writes both outputs
- * (splits before kvq_normalize_splits); returns KVQ_OK or an error. */
+ * over at least one workgroup per CU; more waves in flight lower the achieved bandwidth.
+ * The quantized kernels run best with single-wave workgroups, about 4 per CU for uniform
+ * lengths and small partitions for large ragged batches (all measured on MI355X for batch
+ * 1..64 and 32k..128k contexts). Writes both outputs (splits before
+ * kvq_normalize_splits); returns KVQ_OK or an error. */
 int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t max_pages,
                     int32_t kv_format, int32_t cu_count, int32_t* splits_out,
                     int32_t* waves_out);

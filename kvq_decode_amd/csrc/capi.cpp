@@ -140,6 +140,9 @@ kvq::DecodeParams make_params(const kvq_decode_args* a) {
     p.k_group_shift = a->kv_format == KVQ_KV_F16 ? 0 : ilog2(a->k_group / 16);
     p.k_group_pages = a->kv_format == KVQ_KV_F16 ? 0 : a->k_group / a->block_size;
     p.scale_log2 = a->scale * 1.4426950408889634f;
+    // grouped XCD order for the quantized caches, whose kv heads share V-scale lines;
+    // plain for fp16 (measured about 1% faster there)
+    p.xcd_group = a->kv_format != KVQ_KV_F16;
     return p;
 }
 
@@ -177,17 +180,12 @@ int pick_waves(const kvq_decode_args* a, int pages_per_split) {
 }
 
 // Loads in flight per wave, in 16-token chunks (the depth of the kernels' register
-// ring): the caller's 1, 2 or 4 (fp16 head_dim 256: 1 or 2), else
-//   fp16: 2 (8 KB per chunk and wave at head_dim 128);
-//   INT4: 2 (1 KB per chunk and wave; the kernel then fits 4 waves per SIMD);
-//   INT8 / FP8: 4 (2 KB, 2 waves per SIMD).
-// Returns 0 when invalid.
+// ring): the caller's 1, 2 or 4 (fp16 head_dim 256: 1 or 2), else 2 (measured best for
+// every format on MI355X; the chunk-pair kernel of the quantized formats keeps one pair
+// in flight at depths 1 and 2, three at 4). Returns 0 when invalid.
 int pick_pipeline(const kvq_decode_args* a) {
     const int r = a->pipeline;
-    if (r == 0) {
-        if (a->kv_format == KVQ_KV_F16) return 2;
-        return a->kv_format == KVQ_KV_INT4 ? 2 : 4;
-    }
+    if (r == 0) return 2;
     if (r != 1 && r != 2 && r != 4) return 0;
     if (r == 4 && a->kv_format == KVQ_KV_F16 && a->head_dim > 128) return 0;
     return r;
@@ -290,14 +288,18 @@ int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t
     if (kv_format < KVQ_KV_F16 || kv_format > KVQ_KV_INT4) return KVQ_ERR_FORMAT;
     const bool quant = kv_format != KVQ_KV_F16;
     const int64_t chunks = int64_t(max_pages) * (block_size / 16);
-    const int64_t waves_per_cu = quant ? 8 : 2;
-    const int64_t chunks_per_wave = quant ? 64 : 512;
-    int64_t per_pair = pow2_floor(waves_per_cu * cu_count / (int64_t(batch) * kv_heads));
+    const int64_t pairs = int64_t(batch) * kv_heads;
+    const int64_t waves_per_cu = quant ? 4 : 2;
+    // quantized: 256-chunk partitions while (sequence, kv head) pairs alone do not fill
+    // the CUs, 64-chunk partitions beyond (large batches, where ragged lengths need small
+    // work items to balance)
+    const int64_t chunks_per_wave = quant ? (pairs > cu_count ? 64 : 256) : 512;
+    int64_t per_pair = pow2_floor(waves_per_cu * cu_count / pairs);
     const int64_t balance = pow2_floor(cdiv(chunks, chunks_per_wave));
     if (per_pair < balance) per_pair = balance;
     const int64_t cap = pow2_floor(chunks / 4);
     if (per_pair > cap) per_pair = cap;
-    const int64_t max_waves = quant ? 4 : 2;
+    const int64_t max_waves = quant ? 1 : 2;
     const int64_t waves = per_pair < max_waves ? per_pair : max_waves;
     *waves_out = int32_t(waves);
     *splits_out = int32_t(per_pair / waves);

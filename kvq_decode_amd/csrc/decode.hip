@@ -333,7 +333,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ o_
 
 template <int D, int W, bool FINAL, int P>
 static hipError_t launch_f16(const DecodeParams& p, hipStream_t stream) {
-    const dim3 grid(decode_grid(p.kv_heads, FINAL ? 1 : p.num_splits, p.batch));
+    const dim3 grid(decode_grid(p.xcd_group, p.kv_heads, FINAL ? 1 : p.num_splits, p.batch));
     // the larger of the cross-wave combine ([W][G][D] + [W][16] m, l floats) and the
     // waves' K staging tiles (32 * D bytes each)
     const size_t combine = sizeof(float) * (W * p.group * D + 2 * W * 16);

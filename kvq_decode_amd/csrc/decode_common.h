@@ -82,13 +82,18 @@ __device__ __forceinline__ uint64_t block_offset(int phys, int64_t stride) {
 }
 
 // XCD-aware workgroup order. MI355X dispatches the workgroups of a launch to its 8 XCDs
-// round-robin by linear id, and each XCD has its own L2. A (kv head, split, sequence) grid
-// with the head fastest would put the kv heads of one (sequence, split) on 8 different
-// XCDs, so a cache line they share (the quantized caches' V scales: 4 heads per 128-byte
-// line) would be fetched by several L2s. The decode kernels run a 1-D grid of kv_heads *
-// U8 workgroups instead (U = splits * batch units, U8 rounded up to a multiple of 8),
-// numbered id = 8 * (kvh + kv_heads * (u / 8)) + u % 8: every kv head of unit u runs on
-// XCD u % 8, back to back. Workgroups past the last unit exit at once.
+// round-robin by linear id, and each XCD has its own L2. The decode kernels run a 1-D grid
+// and map its ids to (kv head, split, sequence) units (U = splits * batch of them) in one
+// of two orders, chosen by the host (DecodeParams::xcd_group):
+//   plain:   id = kvh + kv_heads * u, the kv heads of a unit spread over the XCDs (fp16,
+//            whose heads share no cache lines);
+//   grouped: every kv head of a unit on one XCD, back to back, so that a line they share
+//            (the quantized caches' V scales: 4 heads per 128-byte line) is fetched by one
+//            L2. With a split count that is a multiple of 8, split s of sequence b runs on
+//            XCD (s + b) % 8 - a sequence's early splits, the ones short sequences have,
+//            land on different XCDs for different sequences; otherwise unit u runs on XCD
+//            u % 8 (U rounded up to a multiple of 8; workgroups past the last unit exit).
+// Fewer than 8 units always take the plain order, which spreads them over all XCDs.
 constexpr int kXcds = 8;
 
 struct WgCoord {
@@ -98,19 +103,34 @@ struct WgCoord {
 
 __device__ __forceinline__ WgCoord wg_coord(const DecodeParams& p, int splits) {
     const int i = blockIdx.x;
-    const int q = i / kXcds;
     WgCoord c;
-    c.kvh = q % p.kv_heads;
-    const int u = (q / p.kv_heads) * kXcds + i % kXcds;
-    c.split = u % splits;
-    c.b = u / splits;
+    if (!p.xcd_group || splits * p.batch < kXcds) {
+        c.kvh = i % p.kv_heads;
+        const int u = i / p.kv_heads;
+        c.split = u % splits;
+        c.b = u / splits;
+    } else {
+        const int x = i % kXcds, q = i / kXcds;
+        c.kvh = q % p.kv_heads;
+        const int j = q / p.kv_heads;
+        if (splits % kXcds == 0) {
+            const int per = splits / kXcds;
+            c.b = j / per;
+            c.split = ((x - c.b) & (kXcds - 1)) + kXcds * (j % per);
+        } else {
+            const int u = j * kXcds + x;
+            c.split = u % splits;
+            c.b = u / splits;
+        }
+    }
     c.live = c.b < p.batch;
     return c;
 }
 
 // Workgroups of the 1-D decode grid (see wg_coord).
-inline unsigned decode_grid(int kv_heads, int splits, int batch) {
-    const long units = ((long)splits * batch + kXcds - 1) / kXcds * kXcds;
+inline unsigned decode_grid(bool xcd_group, int kv_heads, int splits, int batch) {
+    const long u = (long)splits * batch;
+    const long units = (!xcd_group || u < kXcds) ? u : (u + kXcds - 1) / kXcds * kXcds;
     return (unsigned)(units * kv_heads);
 }
 

@@ -828,7 +828,7 @@ static size_t q_shmem(const DecodeParams& p, int fmt) {
 
 template <int FMT, int W, bool FINAL, int P, bool SPLIT>
 static hipError_t launch_q(const DecodeParams& p, hipStream_t stream) {
-    const dim3 grid(decode_grid(p.kv_heads, FINAL ? 1 : p.num_splits, p.batch));
+    const dim3 grid(decode_grid(p.xcd_group, p.kv_heads, FINAL ? 1 : p.num_splits, p.batch));
     hipLaunchKernelGGL((decode_q_kernel<FMT, W, FINAL, P, SPLIT>), grid, dim3(W * 64),
                        q_shmem<W>(p, FMT), stream, p);
     return hipGetLastError();
@@ -836,7 +836,7 @@ static hipError_t launch_q(const DecodeParams& p, hipStream_t stream) {
 
 template <int FMT, int W, bool FINAL, int P>
 static hipError_t launch_q2(const DecodeParams& p, hipStream_t stream) {
-    const dim3 grid(decode_grid(p.kv_heads, FINAL ? 1 : p.num_splits, p.batch));
+    const dim3 grid(decode_grid(p.xcd_group, p.kv_heads, FINAL ? 1 : p.num_splits, p.batch));
     hipLaunchKernelGGL((decode_q2_kernel<FMT, W, FINAL, P>), grid, dim3(W * 64),
                        q_shmem<W>(p, FMT), stream, p);
     return hipGetLastError();

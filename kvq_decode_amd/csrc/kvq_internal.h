@@ -36,6 +36,7 @@ struct DecodeParams {
     int32_t k_group_pages;   // pages per K scale group
     int32_t num_splits, pages_per_split;
     float scale_log2;        // softmax scale * log2(e)
+    int32_t xcd_group;       // workgroup order (decode_common.h wg_coord): 0 plain, 1 grouped
 };
 
 // Launches the decode kernel for the format/head_dim in `fmt`/`head_dim`. `final_out`
