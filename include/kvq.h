@@ -60,7 +60,11 @@ typedef enum kvq_status {
  *                                               channel), z = min, s = (max-min)/15
  *   k_scale, k_zero  fp16 [nb, Hkv, D]: group g of sequence b lives in block
  *                    block_table[b][g * k_group / block_size]
- *   v_scale, v_zero  fp16 [nb, Hkv, block_size]: one pair per token slot           */
+ *   v_scale, v_zero  fp16 [nb, Hkv, block_size]: one pair per token slot
+ * Scale and zero are stored interleaved: one fp16 [nb, Hkv, D, 2] (K) and one
+ * [nb, Hkv, block_size, 2] (V) tensor of (scale, zero) pairs, so that a decode loads both
+ * of a token (V) or a channel (K) with one access. k_scale / v_scale point at element 0
+ * of that tensor and k_zero / v_zero one element (2 bytes) after it.                  */
 typedef enum kvq_kv_format {
     KVQ_KV_F16 = 0,
     KVQ_KV_INT8 = 1,
@@ -87,10 +91,10 @@ typedef struct kvq_decode_args {
     float scale;              /* softmax scale; the reference defaults to 1/sqrt(head_dim) */
     int32_t kv_format;        /* kvq_kv_format */
     int32_t k_group;          /* tokens per K scale group (quantized formats; 128) */
-    const void* k_scale;      /* fp16 [num_blocks, kv_heads, head_dim], contiguous */
-    const void* k_zero;
-    const void* v_scale;      /* fp16 [num_blocks, kv_heads, block_size], contiguous */
-    const void* v_zero;
+    const void* k_scale;      /* fp16 (scale, zero) pairs [num_blocks, kv_heads, head_dim, 2] */
+    const void* k_zero;       /* = k_scale + 2 bytes */
+    const void* v_scale;      /* fp16 (scale, zero) pairs [num_blocks, kv_heads, block_size, 2] */
+    const void* v_zero;       /* = v_scale + 2 bytes */
     int32_t waves_per_group;  /* tuning: waves per (kv head, split) workgroup, one of
                                  1, 2, 4, 8, 16; 0 = the library's choice */
     int32_t pipeline;         /* tuning: depth of the load ring in 16-token chunks, 1, 2

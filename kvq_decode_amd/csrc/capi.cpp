@@ -30,6 +30,15 @@ int64_t pow2_floor(int64_t x) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// The zero of each quantized scale pair is the fp16 right after its scale (interleaved
+// (scale, zero) storage, include/kvq.h).
+bool scale_pairs(const kvq_decode_args* a) {
+    const uintptr_t ks = reinterpret_cast<uintptr_t>(a->k_scale);
+    const uintptr_t vs = reinterpret_cast<uintptr_t>(a->v_scale);
+    return reinterpret_cast<uintptr_t>(a->k_zero) == ks + 2 &&
+           reinterpret_cast<uintptr_t>(a->v_zero) == vs + 2;
+}
+
 // Checks shared by every entry point that reads the caches. `need_out` is false for
 // stage 1, which writes the workspace instead of args->out.
 int check_decode_args(const kvq_decode_args* a, bool need_out) {
@@ -58,9 +67,8 @@ int check_decode_args(const kvq_decode_args* a, bool need_out) {
         if (a->k_group < a->block_size || a->k_group % a->block_size != 0 ||
             !is_pow2(a->k_group) || a->k_group / a->block_size > 64)
             return KVQ_ERR_UNSUPPORTED;
-        if (!aligned16(a->k_scale) || !aligned16(a->k_zero) || !aligned16(a->v_scale) ||
-            !aligned16(a->v_zero))
-            return KVQ_ERR_ALIGNMENT;
+        if (!scale_pairs(a)) return KVQ_ERR_FORMAT;
+        if (!aligned16(a->k_scale) || !aligned16(a->v_scale)) return KVQ_ERR_ALIGNMENT;
         // The quantized kernels address each kv head's codes and scales through 32-bit
         // offsets from the head's base: every offset must stay below 2^32 bytes.
         const int64_t lim32 = int64_t(1) << 32;
@@ -72,8 +80,8 @@ int check_decode_args(const kvq_decode_args* a, bool need_out) {
                     int64_t(a->block_size - 1) * a->k_stride_tok + row >= lim32 ||
             int64_t(a->num_blocks - 1) * a->v_stride_blk +
                     int64_t(a->block_size - 1) * a->v_stride_tok + row >= lim32 ||
-            int64_t(a->num_blocks) * a->kv_heads * 256 >= lim32 ||
-            int64_t(a->num_blocks) * a->kv_heads * 2 * a->block_size >= lim32)
+            int64_t(a->num_blocks) * a->kv_heads * 4 * a->head_dim >= lim32 ||
+            int64_t(a->num_blocks) * a->kv_heads * 4 * a->block_size >= lim32)
             return KVQ_ERR_UNSUPPORTED;
     }
     // Vector loads: 16-byte aligned bases and row strides that keep every row aligned.
@@ -200,6 +208,7 @@ int check_quant_args(const kvq_decode_args* a) {
     if (!a->k_cache || !a->v_cache || !a->block_table || !a->seq_lens) return KVQ_ERR_NULL_POINTER;
     if (a->kv_format < KVQ_KV_INT8 || a->kv_format > KVQ_KV_INT4) return KVQ_ERR_FORMAT;
     if (!a->k_scale || !a->k_zero || !a->v_scale || !a->v_zero) return KVQ_ERR_FORMAT;
+    if (!scale_pairs(a)) return KVQ_ERR_FORMAT;
     if (a->batch < 1 || a->kv_heads < 1 || a->max_blocks < 1 || a->num_blocks < 1)
         return KVQ_ERR_SHAPE;
     if (!is_pow2(a->block_size) || a->block_size < 16) return KVQ_ERR_SHAPE;

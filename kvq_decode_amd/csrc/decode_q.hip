@@ -173,16 +173,17 @@ struct QFmt<KVQ_KV_INT4> {
     }
 };
 
-// Raw codes of one 16-token chunk as held by one lane, the 4 tokens' V scale/zero, and
-// (lane l) channels 2l, 2l+1 of the scale/zero of the chunk's K group. The group data is
-// loaded with every chunk, not only with a group's first one: loads issued on every path
+// Raw codes of one 16-token chunk as held by one lane, the (scale, zero) pairs of its 4
+// tokens (vsz[r]: token 4g + r, scale in the low half), and (lane l) the pairs of channels
+// 2l, 2l+1 of the chunk's K group (ksz). The group data is loaded with every chunk that
+// may start a group's use, not only with a group's first one: loads issued on every path
 // keep the compiler's wait counts exact, so no chunk waits for loads it does not use.
 template <int FMT>
 struct ChunkQ {
     u4v k[QFmt<FMT>::KLOADS];
     uint32_t v[4][QFmt<FMT>::VBYTES / 4];
-    h4 vs, vz;
-    uint32_t ks2, kz2;
+    u4v vsz;
+    u2 ksz;
 };
 
 // Per-lane byte offsets of a chunk's loads inside its page (the page base and the slot
@@ -192,8 +193,8 @@ struct ChunkQ {
 //   K, INT8 / FP8 (128-byte rows): load j row min(8j + l/8, last), bytes [16(l%8), +16) -
 //     each instruction covers 8 whole rows (every 128-byte line in one instruction); the
 //     rows reach the k-operand layout through the wave's LDS tile (kstage_q);
-//   V rows min(4g + r, last) bytes [VBYTES * (l%16), +VBYTES), V scales of tokens
-//   4g..4g+3, and channels 2l, 2l+1 of the K group scales.
+//   V rows min(4g + r, last) bytes [VBYTES * (l%16), +VBYTES), the V (scale, zero) pairs
+//   of tokens 4g..4g+3 (16 bytes), and the K group's pairs of channels 2l, 2l+1 (8 bytes).
 struct QLaneOff {
     uint32_t k[2], v[4], vs, ks;
 };
@@ -214,8 +215,8 @@ __device__ __forceinline__ QLaneOff lane_offsets(const DecodeParams& p, int i16,
 #pragma unroll
     for (int r = 0; r < 4; ++r)
         o.v[r] = (uint32_t)(min(4 * g + r, last) * (int)p.v_stok + Q::VBYTES * i16);
-    o.vs = 8 * g;
-    o.ks = 4 * lane;
+    o.vs = 16 * g;
+    o.ks = 8 * lane;
     return o;
 }
 
@@ -225,9 +226,9 @@ __device__ __forceinline__ QLaneOff lane_offsets(const DecodeParams& p, int i16,
 // 32-bit scalar (soffset) plus the lane's 32-bit offset (voffset): a few scalar
 // multiplies per chunk and no vector address arithmetic.
 struct QBase {
-    __amdgpu_buffer_rsrc_t k, v, vs, vz, ks, kz;
+    __amdgpu_buffer_rsrc_t k, v, vs, ks;  // codes, and the (scale, zero) pair tensors
     uint32_t k_sblk, v_sblk, k_stok, v_stok;
-    uint32_t vs_blk, ks_blk;  // bytes per block of the V / K scale tensors
+    uint32_t vs_blk, ks_blk;  // bytes per block of the V / K pair tensors
     uint32_t cmask;           // 16-token chunks per page - 1
 };
 
@@ -240,16 +241,14 @@ __device__ __forceinline__ QBase q_base(const DecodeParams& p, int kvh) {
     QBase B;
     B.k = head_rsrc(p.k, (int64_t)kvh * p.k_sh);
     B.v = head_rsrc(p.v, (int64_t)kvh * p.v_sh);
-    B.vs = head_rsrc(p.v_scale, (int64_t)kvh * 2 * p.block_size);
-    B.vz = head_rsrc(p.v_zero, (int64_t)kvh * 2 * p.block_size);
-    B.ks = head_rsrc(p.k_scale, (int64_t)kvh * 256);
-    B.kz = head_rsrc(p.k_zero, (int64_t)kvh * 256);
+    B.vs = head_rsrc(p.v_scale, (int64_t)kvh * 4 * p.block_size);
+    B.ks = head_rsrc(p.k_scale, (int64_t)kvh * 4 * 128);
     B.k_sblk = (uint32_t)p.k_sblk;
     B.v_sblk = (uint32_t)p.v_sblk;
     B.k_stok = (uint32_t)p.k_stok;
     B.v_stok = (uint32_t)p.v_stok;
-    B.vs_blk = (uint32_t)(p.kv_heads * 2 * p.block_size);
-    B.ks_blk = (uint32_t)(p.kv_heads * 256);
+    B.vs_blk = (uint32_t)(p.kv_heads * 4 * p.block_size);
+    B.ks_blk = (uint32_t)(p.kv_heads * 4 * 128);
     B.cmask = (1u << p.cpp_shift) - 1;
     return B;
 }
@@ -260,7 +259,8 @@ __device__ __forceinline__ QBase q_base(const DecodeParams& p, int kvh) {
 // policy.
 constexpr int kNT = 2;
 
-template <int FMT>
+// WITH_K: also load the K group's (scale, zero) pairs (ch.ksz).
+template <int FMT, bool WITH_K = true>
 __device__ __forceinline__ void load_chunk_q(const QBase& B, int c, const QLaneOff& lo, int phys,
                                              int lead, ChunkQ<FMT>& ch) {
     typedef QFmt<FMT> Q;
@@ -280,15 +280,15 @@ __device__ __forceinline__ void load_chunk_q(const QBase& B, int c, const QLaneO
             ch.v[r][0] = __builtin_amdgcn_raw_buffer_load_b32(B.v, lo.v[r], vo, kNT);
         }
     }
-    // V scale/zero of tokens slot + 4g .. +3 (4 consecutive halves; slots past the
-    // sequence hold garbage and are masked by selects, never multiplied)
-    const uint32_t so = (uint32_t)phys * B.vs_blk + 2 * slot;
-    ch.vs = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(B.vs, lo.vs, so, kNT));
-    ch.vz = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(B.vz, lo.vs, so, kNT));
-    // K group scale/zero, stored with the group's first page `lead`
-    const uint32_t go = (uint32_t)lead * B.ks_blk;
-    ch.ks2 = __builtin_amdgcn_raw_buffer_load_b32(B.ks, lo.ks, go, 0);
-    ch.kz2 = __builtin_amdgcn_raw_buffer_load_b32(B.kz, lo.ks, go, 0);
+    // V (scale, zero) pairs of tokens slot + 4g .. +3 (16 bytes; slots past the sequence
+    // hold garbage and are masked by selects, never multiplied)
+    const uint32_t so = (uint32_t)phys * B.vs_blk + 4 * slot;
+    ch.vsz = __builtin_amdgcn_raw_buffer_load_b128(B.vs, lo.vs, so, kNT);
+    // K group (scale, zero) pairs, stored with the group's first page `lead`
+    if constexpr (WITH_K) {
+        const uint32_t go = (uint32_t)lead * B.ks_blk;
+        ch.ksz = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(B.ks, lo.ks, go, 0));
+    }
 }
 
 // Half-row rotation: lane l reads lane (l & ~15) | ((l + 8) & 15), i.e. column n of a
@@ -337,10 +337,13 @@ __device__ __forceinline__ void k_operand(const ChunkQ<FMT>& ch, char* kst, int 
 // lane in k-operand order (INT4: written there in the permuted order, two halves per
 // lane). Returns C = sum_d q_d z_d of that head (all 128 channels).
 template <int FMT>
-__device__ __forceinline__ float make_qprime(uint32_t s2, uint32_t z2, uint32_t* stage, int g,
-                                             const h8* qsh, bool lo_part, h8* val) {
+__device__ __forceinline__ float make_qprime(u2 ksz, uint32_t* stage, int g, const h8* qsh,
+                                             bool lo_part, h8* val) {
     typedef QFmt<FMT> Q;
     const int lane = __lane_id();
+    // (s, z) pairs of channels 2l, 2l+1 -> the two scales and the two zeros
+    const uint32_t s2 = perm(ksz[1], ksz[0], 0x05040100u);
+    const uint32_t z2 = perm(ksz[1], ksz[0], 0x07060302u);
     _Float16* ss = (_Float16*)stage;
     _Float16* zz = (_Float16*)(stage + 64);
     if constexpr (Q::permuted()) {
@@ -403,17 +406,20 @@ __device__ __forceinline__ void softmax_step(float* s2, SoftmaxState<128>& st, f
 // would be an error of up to 2^-11 (V - z) when one token dominates. corr accumulates
 // p z_t in fp32. Rows r with !ok (past the sequence: garbage scales) give 0.
 template <bool MASK>
-__device__ __forceinline__ void pv_weights(const float* pr, h4 vs, h4 vz, int valid, int g,
-                                           h4& phi, h4& plo, float& corr) {
+__device__ __forceinline__ void pv_weights(const float* pr, u4v vsz, int valid, int g, h4& phi,
+                                           h4& plo, float& corr) {
     float cadd = 0.f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const bool ok = !MASK || 4 * g + r < valid;
-        const float sv = (float)vs[r];
+        // element copied out first: a bit cast of the subscript itself reads element 0
+        const uint32_t pair = vsz[r];
+        const h2 sz = __builtin_bit_cast(h2, pair);
+        const float sv = (float)sz[0];
         const _Float16 hi = (_Float16)__builtin_fmaf(pr[r], sv, 0.f);
         phi[r] = ok ? hi : (_Float16)0.f;
         plo[r] = ok ? (_Float16)__builtin_fmaf(pr[r], sv, -(float)hi) : (_Float16)0.f;
-        cadd = __builtin_fmaf(pr[r], ok ? (float)vz[r] : 0.f, cadd);
+        cadd = __builtin_fmaf(pr[r], ok ? (float)sz[1] : 0.f, cadd);
     }
     corr += cadd;
 }
@@ -456,7 +462,7 @@ __device__ __forceinline__ void chunk_q(const ChunkQ<FMT>& ch, const h8* qhi, co
     float pr[4];
     softmax_step(s2, st, corr, pr);
     h4 phi, plo;
-    pv_weights<MASK>(pr, ch.vs, ch.vz, valid, g, phi, plo, corr);
+    pv_weights<MASK>(pr, ch.vsz, valid, g, phi, plo, corr);
     uint32_t a01[8], a23[8];
     Q::vtiles(ch.v, a01, a23);
     if constexpr (SPLIT) {
@@ -521,11 +527,9 @@ __device__ __forceinline__ void chunk_pair(const ChunkQ<FMT>& ca, const ChunkQ<F
     }
     float pr[4];
     softmax_step(s2, st, corr, pr);
-    const u2 vs2 = slot ? __builtin_bit_cast(u2, cb.vs) : __builtin_bit_cast(u2, ca.vs);
-    const u2 vz2 = slot ? __builtin_bit_cast(u2, cb.vz) : __builtin_bit_cast(u2, ca.vz);
+    const u4v vsz = slot ? cb.vsz : ca.vsz;
     h4 phi, plo;
-    pv_weights<MASK>(pr, __builtin_bit_cast(h4, vs2), __builtin_bit_cast(h4, vz2), valid, g, phi,
-                     plo, corr);
+    pv_weights<MASK>(pr, vsz, valid, g, phi, plo, corr);
     // B operand: k-slots 8g + r (chunk a's token 4g + r) and 8g + 4 + r (chunk b's); the
     // lane's p in its chunk's half, zeros in the other
     const u2 pw = __builtin_bit_cast(u2, lo_part ? plo : phi);
@@ -620,12 +624,12 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
     auto new_group = [&](const ChunkQ<FMT>& ch) {
         h8 v[4];
         if constexpr (SPLIT) {
-            csl = make_qprime<FMT>(ch.ks2, ch.kz2, stage, g, qsh, upper, v) * sl2;
+            csl = make_qprime<FMT>(ch.ksz, stage, g, qsh, upper, v) * sl2;
 #pragma unroll
             for (int k = 0; k < 4; ++k) qhi[k] = v[k];
         } else {
-            csl = make_qprime<FMT>(ch.ks2, ch.kz2, stage, g, qsh, false, qhi) * sl2;
-            make_qprime<FMT>(ch.ks2, ch.kz2, stage, g, qsh, true, qlo);
+            csl = make_qprime<FMT>(ch.ksz, stage, g, qsh, false, qhi) * sl2;
+            make_qprime<FMT>(ch.ksz, stage, g, qsh, true, qlo);
         }
     };
 
@@ -734,7 +738,7 @@ __global__ __launch_bounds__(W * 64) void decode_q2_kernel(const DecodeParams p)
 
     auto group = [&](const ChunkQ<FMT>& ch, int gi) {
         if (gi != gq) {
-            csl = make_qprime<FMT>(ch.ks2, ch.kz2, stage, g, qsh, lo_part, qv) * sl2;
+            csl = make_qprime<FMT>(ch.ksz, stage, g, qsh, lo_part, qv) * sl2;
             gq = gi;
         }
     };
@@ -764,11 +768,16 @@ __global__ __launch_bounds__(W * 64) void decode_q2_kernel(const DecodeParams p)
         int pg_nxt = chunk_pages<P>(p, b, c_first + P, last, kgs);
         // Issued slot by slot: a slot's loads moved behind a later slot's would make the
         // ring's waits (vmcnt counts the loads issued after the awaited one) drain it.
+        // a pair's K group is its first chunk's: odd slots skip the K pair load
 #pragma unroll
         for (int i = 0; i < P; ++i) {
-            load_chunk_q<FMT>(base, min(c_first + i, last), lo,
-                              __builtin_amdgcn_readlane(pg_cur, i),
-                              __builtin_amdgcn_readlane(pg_cur, P + i), ring[i]);
+            if (i % 2 == 0)
+                load_chunk_q<FMT, true>(base, min(c_first + i, last), lo,
+                                        __builtin_amdgcn_readlane(pg_cur, i),
+                                        __builtin_amdgcn_readlane(pg_cur, P + i), ring[i]);
+            else
+                load_chunk_q<FMT, false>(base, min(c_first + i, last), lo,
+                                         __builtin_amdgcn_readlane(pg_cur, i), 0, ring[i]);
             __builtin_amdgcn_sched_barrier(0);
         }
         for (int c0 = c_first; c0 < e_hi; c0 += P) {
@@ -782,11 +791,11 @@ __global__ __launch_bounds__(W * 64) void decode_q2_kernel(const DecodeParams p)
                     chunk_pair<FMT, false>(ring[i], ring[i + 1], qv, csl, sl2f, 16, 16, g, slot,
                                            lo_part, kst, st, corr);
                 }
-#pragma unroll
-                for (int j = i; j < i + 2; ++j)
-                    load_chunk_q<FMT>(base, min(c0 + j + P, last), lo,
-                                      __builtin_amdgcn_readlane(pg_cur, j),
-                                      __builtin_amdgcn_readlane(pg_cur, P + j), ring[j]);
+                load_chunk_q<FMT, true>(base, min(c0 + i + P, last), lo,
+                                        __builtin_amdgcn_readlane(pg_cur, i),
+                                        __builtin_amdgcn_readlane(pg_cur, P + i), ring[i]);
+                load_chunk_q<FMT, false>(base, min(c0 + i + 1 + P, last), lo,
+                                         __builtin_amdgcn_readlane(pg_cur, i + 1), 0, ring[i + 1]);
             }
         }
     }

@@ -145,12 +145,12 @@ __global__ __launch_bounds__(128) void quant_k_kernel(const QuantParams p) {
                        (int64_t)(t % p.block_size) * p.k_stok + (int64_t)kvh * p.k_sh;
         store_pair<FMT>(row, j, encode<FMT>(x0, q0), encode<FMT>(x1, q1));
     }
+    // (scale, zero) pairs of channels 2j, 2j + 1: one 8-byte store
     const int lead = phys_of(p, b, t0 / p.block_size);
     const int64_t sz = ((int64_t)lead * p.kv_heads + kvh) * D + 2 * j;
-    p.k_scale[sz] = (_Float16)q0.s;
-    p.k_scale[sz + 1] = (_Float16)q1.s;
-    p.k_zero[sz] = (_Float16)q0.z;
-    p.k_zero[sz + 1] = (_Float16)q1.z;
+    typedef _Float16 h4q __attribute__((ext_vector_type(4)));
+    const h4q pairs = {(_Float16)q0.s, (_Float16)q0.z, (_Float16)q1.s, (_Float16)q1.z};
+    *(h4q*)(p.k_scale + 2 * sz) = pairs;
 }
 
 // V: one token row (D channels of one kv head) per 16 lanes, each lane D/16 channels.
@@ -191,8 +191,8 @@ __global__ __launch_bounds__(256) void quant_v_kernel(const QuantParams p) {
         store_pair<FMT>(row, (lane16 * PER + e) / 2, encode<FMT>(x[e], q), encode<FMT>(x[e + 1], q));
     if (lane16 == 0) {
         const int64_t sz = ((int64_t)phys * p.kv_heads + kvh) * p.block_size + slot;
-        p.v_scale[sz] = (_Float16)q.s;
-        p.v_zero[sz] = (_Float16)q.z;
+        typedef _Float16 h2q __attribute__((ext_vector_type(2)));
+        *(h2q*)(p.v_scale + 2 * sz) = h2q{(_Float16)q.s, (_Float16)q.z};
     }
 }
 

@@ -96,6 +96,26 @@ def workspace_shapes(batch: int, q_heads: int, head_dim: int, splits: int):
     return (batch, q_heads, splits, head_dim), (batch, q_heads, splits)
 
 
+def check_scale_pairs(scale: torch.Tensor, zero: torch.Tensor, shape, name: str) -> None:
+    """The scale / zero tensors of a quantized cache are views of one interleaved fp16
+    [..., 2] tensor of (scale, zero) pairs (include/kvq.h): element strides
+    (2 * prod(shape[1:]), ..., 2) and the zero one element after the scale."""
+    shape = tuple(shape)
+    want = []
+    acc = 2
+    for n in reversed(shape):
+        want.append(acc)
+        acc *= n
+    want = tuple(reversed(want))
+    for t in (scale, zero):
+        _require(t is not None, f"{name}_scale / {name}_zero are required for a quantized cache")
+        _require(t.dtype == torch.float16 and tuple(t.shape) == shape and t.stride() == want,
+                 f"{name}_scale / {name}_zero must be fp16 {shape} views of an interleaved "
+                 f"(scale, zero) tensor {shape + (2,)} (strides {want})")
+    _require(zero.data_ptr() == scale.data_ptr() + 2,
+             f"{name}_zero must be the element after {name}_scale (interleaved pairs)")
+
+
 def _ptr(t: Optional[torch.Tensor]) -> int:
     return 0 if t is None else t.data_ptr()
 
@@ -177,13 +197,8 @@ def paged_decode_attention(
                  "quantized caches hold uint8 codes")
         _require(Dc == (D // 2 if kv_format == "int4" else D),
                  "code cache last dim must be head_dim (head_dim/2 for int4)")
-        for name, t, shape in (("k_scale", k_scale, (k_cache.shape[0], Hkv, D)),
-                               ("k_zero", k_zero, (k_cache.shape[0], Hkv, D)),
-                               ("v_scale", v_scale, (k_cache.shape[0], Hkv, block_size)),
-                               ("v_zero", v_zero, (k_cache.shape[0], Hkv, block_size))):
-            _require(t is not None, f"{name} is required for kv_format={kv_format}")
-            _require(t.dtype == torch.float16 and tuple(t.shape) == shape and t.is_contiguous(),
-                     f"{name} must be contiguous float16 of shape {shape}")
+        check_scale_pairs(k_scale, k_zero, (k_cache.shape[0], Hkv, D), "k")
+        check_scale_pairs(v_scale, v_zero, (k_cache.shape[0], Hkv, block_size), "v")
     else:
         _require(k_cache.dtype == v_cache.dtype == torch.float16,
                  "q, k_cache and v_cache must all be float16")

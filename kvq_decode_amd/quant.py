@@ -12,6 +12,9 @@ channel over groups of `k_group` tokens, values per token. Storage (include/kvq.
     k_scale, k_zero   fp16 [num_blocks, Hkv, D]  - group g of sequence b lives in block
                       block_table[b, g * k_group // block_size]
     v_scale, v_zero   fp16 [num_blocks, Hkv, block_size]
+                      both pairs are strided views of interleaved storage, one fp16
+                      [..., 2] tensor of (scale, zero) per channel (K) / token (V): a
+                      decode reads both of a token with one access
 """
 import ctypes
 from typing import NamedTuple, Optional
@@ -20,7 +23,7 @@ import torch
 
 from kvq_decode_amd import _lib
 from kvq_decode_amd._lib import KV_FORMATS, DecodeArgs
-from kvq_decode_amd.ops import DEFAULT_K_GROUP, KvqArgumentError, _require
+from kvq_decode_amd.ops import DEFAULT_K_GROUP, KvqArgumentError, _require, check_scale_pairs
 
 QUANT_FORMATS = ("int8", "fp8_e4m3", "int4")
 
@@ -55,9 +58,9 @@ def allocate_quantized_cache(num_blocks: int, block_size: int, kv_heads: int, he
     shape = (num_blocks, kv_heads, block_size, dc)
     kc = torch.empty(shape, dtype=torch.uint8, device=device).permute(0, 2, 1, 3)
     vc = torch.empty(shape, dtype=torch.uint8, device=device).permute(0, 2, 1, 3)
-    ks = torch.empty((num_blocks, kv_heads, head_dim), dtype=torch.float16, device=device)
-    vs = torch.empty((num_blocks, kv_heads, block_size), dtype=torch.float16, device=device)
-    return QuantizedKVCache(kc, vc, ks, torch.empty_like(ks), vs, torch.empty_like(vs),
+    ksz = torch.empty((num_blocks, kv_heads, head_dim, 2), dtype=torch.float16, device=device)
+    vsz = torch.empty((num_blocks, kv_heads, block_size, 2), dtype=torch.float16, device=device)
+    return QuantizedKVCache(kc, vc, ksz[..., 0], ksz[..., 1], vsz[..., 0], vsz[..., 1],
                             kv_format, k_group)
 
 
@@ -90,10 +93,8 @@ def _check_cache(cache: QuantizedKVCache, block_table, seq_lens, head_dim):
     nb, bs, hkv, dc = cache.k_codes.shape
     _require(dc == (head_dim // 2 if cache.kv_format == "int4" else head_dim),
              "code cache width does not match head_dim")
-    _require(cache.k_scale.shape == (nb, hkv, head_dim) and cache.k_scale.is_contiguous(),
-             "k_scale must be contiguous [num_blocks, Hkv, D]")
-    _require(cache.v_scale.shape == (nb, hkv, bs) and cache.v_scale.is_contiguous(),
-             "v_scale must be contiguous [num_blocks, Hkv, block_size]")
+    check_scale_pairs(cache.k_scale, cache.k_zero, (nb, hkv, head_dim), "k")
+    check_scale_pairs(cache.v_scale, cache.v_zero, (nb, hkv, bs), "v")
     _require(cache.k_group % bs == 0, "k_group must be a multiple of block_size")
     dev = cache.k_codes.device
     _require(dev.type == "cuda", "kvq runs on the GPU only (no CPU fallback)")

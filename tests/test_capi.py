@@ -154,13 +154,63 @@ def test_single_pass_rejects(field, value, status):
     assert _lib.lib().kvq_decode_single(ctypes.byref(a), None) == status
 
 
+def set_scale_pairs(a, base=1 << 43):
+    """Fake (never dereferenced) interleaved (scale, zero) pair pointers."""
+    a.k_scale, a.k_zero = base, base + 2
+    a.v_scale, a.v_zero = base + (1 << 30), base + (1 << 30) + 2
+
+
+def test_scale_pairs_must_interleave():
+    """Quantized caches: each zero must be the fp16 right after its scale (interleaved
+    pairs); separate scale and zero tensors are a format error."""
+    L = _lib.lib()
+    a = good_args()
+    a.kv_format = 3
+    set_scale_pairs(a)
+    a.waves_per_group = 16  # unsupported for quantized: proves the pair check passed
+    assert L.kvq_decode_single(ctypes.byref(a), None) == _lib.KVQ_ERR_UNSUPPORTED
+    for field, value in (("k_zero", (1 << 43) + 16), ("v_zero", (1 << 43) + (1 << 30))):
+        b = good_args()
+        b.kv_format = 3
+        set_scale_pairs(b)
+        setattr(b, field, value)
+        assert L.kvq_decode_single(ctypes.byref(b), None) == _lib.KVQ_ERR_FORMAT, field
+        assert L.kvq_quantize_cache(ctypes.byref(b), 1 << 40, 1 << 40, 0, 0, 0, None) == \
+            _lib.KVQ_ERR_FORMAT, field
+
+
+def test_op_requires_interleaved_scale_pairs():
+    """The Python op accepts scale / zero tensors only as views of one interleaved
+    (scale, zero) tensor; separate tensors are rejected before any device work."""
+    import torch
+    from kvq_decode_amd import KvqArgumentError, paged_decode_attention
+    nb, bs, hkv, d, B = 4, 16, 2, 128, 1
+    q = torch.zeros(B, 4, d, dtype=torch.float16)
+    kc = torch.zeros(nb, bs, hkv, d // 2, dtype=torch.uint8)
+    bt = torch.zeros(B, nb, dtype=torch.int32)
+    sl = torch.ones(B, dtype=torch.int32)
+    ksz = torch.zeros(nb, hkv, d, 2, dtype=torch.float16)
+    vsz = torch.zeros(nb, hkv, bs, 2, dtype=torch.float16)
+    good = dict(kv_format="int4", k_scale=ksz[..., 0], k_zero=ksz[..., 1],
+                v_scale=vsz[..., 0], v_zero=vsz[..., 1])
+    with pytest.raises(KvqArgumentError, match="GPU only"):  # the pair check passed
+        paged_decode_attention(q, kc, kc, bt, sl, **good)
+    bad = dict(good, k_scale=torch.zeros(nb, hkv, d, dtype=torch.float16),
+               k_zero=torch.zeros(nb, hkv, d, dtype=torch.float16))
+    with pytest.raises(KvqArgumentError, match="interleaved"):
+        paged_decode_attention(q, kc, kc, bt, sl, **bad)
+    swapped = dict(good, v_scale=vsz[..., 1], v_zero=vsz[..., 0])
+    with pytest.raises(KvqArgumentError, match="interleaved"):
+        paged_decode_attention(q, kc, kc, bt, sl, **swapped)
+
+
 def test_quantized_tuning_limits():
     """Quantized kernels: up to 8 waves per workgroup and 1, 2 or 4 chunks in flight."""
     L = _lib.lib()
     for field, value in (("waves_per_group", 16), ("pipeline", 3), ("pipeline", 8)):
         a = good_args()
         a.kv_format = 3
-        a.k_scale = a.k_zero = a.v_scale = a.v_zero = 1 << 43
+        set_scale_pairs(a)
         setattr(a, field, value)
         assert L.kvq_decode_single(ctypes.byref(a), None) == _lib.KVQ_ERR_UNSUPPORTED, field
 
@@ -194,7 +244,7 @@ def test_merge_and_quantize_reject():
     assert L.kvq_quantize_cache(ctypes.byref(a), 1 << 40, 1 << 40, 0, 0, 0, None) == \
         _lib.KVQ_ERR_FORMAT
     a.kv_format = 3
-    a.k_scale = a.k_zero = a.v_scale = a.v_zero = 1 << 43
+    set_scale_pairs(a)
     a.k_group = 100  # not a multiple of block_size
     assert L.kvq_quantize_cache(ctypes.byref(a), 1 << 40, 1 << 40, 0, 0, 0, None) == \
         _lib.KVQ_ERR_UNSUPPORTED

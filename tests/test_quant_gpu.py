@@ -130,7 +130,7 @@ def test_code_layout_does_not_change_results(fmt):
     strides, so the same codes stored token-major (the fp16 cache's layout) and written
     by the quantizer into a token-major cache give bit-identical outputs."""
     from kvq_decode_amd import paged_decode_attention
-    from kvq_decode_amd.quant import QuantizedKVCache, quantize_paged_cache
+    from kvq_decode_amd.quant import allocate_quantized_cache, quantize_paged_cache
     q, kc, vc, bt, sl = make([1, 37, 300, 2049], 16, seed=4)
     qc = quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt)
     assert not qc.k_codes.is_contiguous()
@@ -143,8 +143,9 @@ def test_code_layout_does_not_change_results(fmt):
                                    num_splits=splits, **tm.decode_kwargs())
         assert torch.equal(a, b)
     # the quantizer writes through the destination's strides too
-    dst = QuantizedKVCache(torch.zeros_like(tm.k_codes), torch.zeros_like(tm.v_codes),
-                           *[torch.zeros_like(t) for t in qc[2:6]], fmt, qc.k_group)
+    nb, bs, hkv, _ = kc.shape
+    dst = allocate_quantized_cache(nb, bs, hkv, 128, fmt, "cuda", qc.k_group)._replace(
+        k_codes=torch.zeros_like(tm.k_codes), v_codes=torch.zeros_like(tm.v_codes))
     quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt, out=dst)
     slots = valid_slots(bt, sl, 16)
     for name in ("k_codes", "v_codes"):
