@@ -193,6 +193,28 @@ int kvq_quantize_cache(const kvq_decode_args* args, const void* k_src, const voi
 int kvq_quantize_append(const kvq_decode_args* args, const void* k_new, const void* v_new,
                         void* k_resid, kvq_stream_t stream);
 
+/* fp16 append, the unquantized counterpart of kvq_quantize_append. For each sequence b
+ * the token at position p = seq_lens[b] - 1 is new: k_new / v_new fp16 [batch, kv_heads,
+ * head_dim] (contiguous) are copied into slot p % block_size of block
+ * block_table[b][p / block_size] of args->k_cache / v_cache - the page addressing the
+ * reference's builder scatters with (reference.py:75-79). args->seq_lens must already
+ * count the new token; args->kv_format must be KVQ_KV_F16 (q, out and the split fields
+ * are not used). A position outside the block table or a block outside the pool writes
+ * nothing. */
+int kvq_append_kv(const kvq_decode_args* args, const void* k_new, const void* v_new,
+                  kvq_stream_t stream);
+
+/* vLLM's reshape_and_cache for fp16 caches (the reference has no write path; its layout
+ * is vLLM's, reference.py:3-8). Row t of k_new / v_new (element strides new_stride_tok,
+ * new_stride_head; head_dim contiguous) goes to flat slot s = slot_mapping[t] =
+ * block * block_size + offset of args->k_cache / v_cache. s < 0 marks a padding token
+ * and s >= num_blocks * block_size is outside the pool: neither writes anything. Uses
+ * only the cache fields, kv_heads, head_dim, block_size and num_blocks of args. */
+int kvq_reshape_and_cache(const kvq_decode_args* args, const void* k_new, const void* v_new,
+                          int64_t new_stride_tok, int64_t new_stride_head,
+                          const int64_t* slot_mapping, int32_t num_tokens,
+                          kvq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,6 +15,7 @@ from kvq_decode_amd.ops import (  # noqa: F401
     workspace_shapes,
 )
 from kvq_decode_amd._lib import KvqError, version  # noqa: F401
+from kvq_decode_amd import library  # noqa: F401  (registers torch.ops.kvq.*)
 
 __all__ = [
     "paged_decode_attention",

@@ -36,6 +36,8 @@ EXPORTED_SYMBOLS = (
     "kvq_paged_decode",
     "kvq_quantize_cache",
     "kvq_quantize_append",
+    "kvq_append_kv",
+    "kvq_reshape_and_cache",
 )
 
 _i32 = ctypes.c_int32
@@ -107,6 +109,10 @@ def lib():
         L.kvq_quantize_cache.argtypes = [args_p, _vp, _vp, _i64, _i64, _i64, _vp]
         L.kvq_quantize_append.restype = ctypes.c_int
         L.kvq_quantize_append.argtypes = [args_p, _vp, _vp, _vp, _vp]
+        L.kvq_append_kv.restype = ctypes.c_int
+        L.kvq_append_kv.argtypes = [args_p, _vp, _vp, _vp]
+        L.kvq_reshape_and_cache.restype = ctypes.c_int
+        L.kvq_reshape_and_cache.argtypes = [args_p, _vp, _vp, _i64, _i64, _vp, _i32, _vp]
         _lib = L
     return _lib
 

@@ -17,7 +17,7 @@ INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_PATH = os.path.join(PKG_DIR, "libkvq.so")
 
 ARCH = "gfx950"
-SOURCES = ["capi.cpp", "decode.hip", "decode_q.hip", "quant.hip"]
+SOURCES = ["capi.cpp", "decode.hip", "decode_q.hip", "quant.hip", "append.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -252,6 +252,55 @@ kvq::QuantParams make_quant_params(const kvq_decode_args* a) {
     return p;
 }
 
+// Checks for the fp16 append entry points: args->k_cache / v_cache are the destinations
+// (kv_format fp16); the new rows are read with 16-byte loads.
+int check_append_args(const kvq_decode_args* a, const void* k_new, const void* v_new,
+                      int64_t n_stok, int64_t n_sh) {
+    if (!a || !k_new || !v_new || !a->k_cache || !a->v_cache) return KVQ_ERR_NULL_POINTER;
+    if (a->kv_format != KVQ_KV_F16) return KVQ_ERR_FORMAT;
+    if (a->kv_heads < 1 || a->num_blocks < 1) return KVQ_ERR_SHAPE;
+    if (!is_pow2(a->head_dim) || a->head_dim < 16) return KVQ_ERR_SHAPE;
+    if (!is_pow2(a->block_size) || a->block_size < 16) return KVQ_ERR_SHAPE;
+    if (n_stok < 0 || n_sh < 0 || a->k_stride_blk < 0 || a->k_stride_tok < 0 ||
+        a->k_stride_head < 0 || a->v_stride_blk < 0 || a->v_stride_tok < 0 ||
+        a->v_stride_head < 0)
+        return KVQ_ERR_SHAPE;
+    if (!aligned16(k_new) || !aligned16(v_new) || !aligned16(a->k_cache) ||
+        !aligned16(a->v_cache))
+        return KVQ_ERR_ALIGNMENT;
+    if (n_stok % 8 || n_sh % 8 || a->k_stride_blk % 8 || a->k_stride_tok % 8 ||
+        a->k_stride_head % 8 || a->v_stride_blk % 8 || a->v_stride_tok % 8 ||
+        a->v_stride_head % 8)
+        return KVQ_ERR_ALIGNMENT;
+    return KVQ_OK;
+}
+
+kvq::AppendParams make_append_params(const kvq_decode_args* a, const void* k_new,
+                                     const void* v_new, int64_t n_stok, int64_t n_sh) {
+    kvq::AppendParams p{};
+    p.k_new = static_cast<const _Float16*>(k_new);
+    p.v_new = static_cast<const _Float16*>(v_new);
+    p.n_stok = n_stok;
+    p.n_sh = n_sh;
+    p.k = static_cast<_Float16*>(const_cast<void*>(a->k_cache));
+    p.v = static_cast<_Float16*>(const_cast<void*>(a->v_cache));
+    p.k_sblk = a->k_stride_blk;
+    p.k_stok = a->k_stride_tok;
+    p.k_sh = a->k_stride_head;
+    p.v_sblk = a->v_stride_blk;
+    p.v_stok = a->v_stride_tok;
+    p.v_sh = a->v_stride_head;
+    p.bt = a->block_table;
+    p.bt_sb = a->bt_stride_b;
+    p.seq_lens = a->seq_lens;
+    p.kv_heads = a->kv_heads;
+    p.head_dim = a->head_dim;
+    p.block_size = a->block_size;
+    p.max_blocks = a->max_blocks;
+    p.num_blocks = a->num_blocks;
+    return p;
+}
+
 }  // namespace
 
 extern "C" {
@@ -421,6 +470,37 @@ int kvq_quantize_append(const kvq_decode_args* args, const void* k_new, const vo
     p.k_resid = static_cast<_Float16*>(k_resid);
     return hip_status(kvq::launch_quantize_append(p, args->kv_format,
                                                   reinterpret_cast<hipStream_t>(stream)));
+}
+
+int kvq_append_kv(const kvq_decode_args* args, const void* k_new, const void* v_new,
+                  kvq_stream_t stream) {
+    if (!args) return KVQ_ERR_NULL_POINTER;
+    const int64_t row = int64_t(args->kv_heads) * args->head_dim;
+    int st = check_append_args(args, k_new, v_new, row, args->head_dim);
+    if (st != KVQ_OK) return st;
+    if (!args->block_table || !args->seq_lens) return KVQ_ERR_NULL_POINTER;
+    if (args->batch < 1 || args->max_blocks < 1 || args->bt_stride_b < args->max_blocks)
+        return KVQ_ERR_SHAPE;
+    if (args->batch > INT32_MAX / 2) return KVQ_ERR_UNSUPPORTED;
+    kvq::AppendParams p = make_append_params(args, k_new, v_new, row, args->head_dim);
+    p.tokens = args->batch;
+    return hip_status(kvq::launch_append_f16(p, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int kvq_reshape_and_cache(const kvq_decode_args* args, const void* k_new, const void* v_new,
+                          int64_t new_stride_tok, int64_t new_stride_head,
+                          const int64_t* slot_mapping, int32_t num_tokens,
+                          kvq_stream_t stream) {
+    int st = check_append_args(args, k_new, v_new, new_stride_tok, new_stride_head);
+    if (st != KVQ_OK) return st;
+    if (!slot_mapping) return KVQ_ERR_NULL_POINTER;
+    if (num_tokens < 0) return KVQ_ERR_SHAPE;
+    if (num_tokens == 0) return KVQ_OK;
+    kvq::AppendParams p = make_append_params(args, k_new, v_new, new_stride_tok,
+                                             new_stride_head);
+    p.slot_mapping = slot_mapping;
+    p.tokens = num_tokens;
+    return hip_status(kvq::launch_append_f16(p, reinterpret_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

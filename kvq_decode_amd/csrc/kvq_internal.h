@@ -88,4 +88,24 @@ struct QuantParams {
 hipError_t launch_quantize_cache(const QuantParams& p, int kv_format, hipStream_t stream);
 hipError_t launch_quantize_append(const QuantParams& p, int kv_format, hipStream_t stream);
 
+// fp16 append (append.hip). Strides in elements. `tokens` new rows; row t goes to flat
+// slot slot_mapping[t] when slot_mapping is set, else to position seq_lens[t] - 1 of
+// sequence t through block_table.
+struct AppendParams {
+    const _Float16* k_new;
+    const _Float16* v_new;
+    int64_t n_stok, n_sh;
+    _Float16* k;
+    _Float16* v;
+    int64_t k_sblk, k_stok, k_sh;
+    int64_t v_sblk, v_stok, v_sh;
+    const int32_t* bt;
+    int64_t bt_sb;
+    const int32_t* seq_lens;
+    const int64_t* slot_mapping;
+    int32_t tokens, kv_heads, head_dim, block_size, max_blocks, num_blocks;
+};
+
+hipError_t launch_append_f16(const AppendParams& p, hipStream_t stream);
+
 }  // namespace kvq

@@ -43,6 +43,21 @@ class QuantizedKVCache(NamedTuple):
         return dict(kv_format=self.kv_format, k_scale=self.k_scale, k_zero=self.k_zero,
                     v_scale=self.v_scale, v_zero=self.v_zero, k_group=self.k_group)
 
+    @property
+    def k_sz(self) -> torch.Tensor:
+        """The interleaved K (scale, zero) storage [num_blocks, Hkv, D, 2]."""
+        return _pairs(self.k_scale, self.k_zero, "k")
+
+    @property
+    def v_sz(self) -> torch.Tensor:
+        """The interleaved V (scale, zero) storage [num_blocks, Hkv, block_size, 2]."""
+        return _pairs(self.v_scale, self.v_zero, "v")
+
+
+def _pairs(scale: torch.Tensor, zero: torch.Tensor, name: str) -> torch.Tensor:
+    check_scale_pairs(scale, zero, tuple(scale.shape), name)
+    return scale.as_strided(tuple(scale.shape) + (2,), tuple(scale.stride()) + (1,))
+
 
 def allocate_quantized_cache(num_blocks: int, block_size: int, kv_heads: int, head_dim: int,
                              kv_format: str, device, k_group: int = DEFAULT_K_GROUP
