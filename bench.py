@@ -3,13 +3,21 @@ decode path (split-KV stage 1 + merge) against the 8 TB/s HBM3E roofline.
 
     python bench.py [--steps K] [--warmup W] [--config C2] [--splits S]
     python bench.py --sweep            # split / workgroup sweep, table on stderr
+    python bench.py --layers 32        # whole-model decode step (32 layers, HIP graph)
 
 Workload ("C2"): Llama-3-8B GQA layer (32 q heads, 8 kv heads,
 head_dim 128), batch 8, every sequence 32768 tokens, block_size 16, q/K/V ~ N(0,1) fp16,
-block table = a random permutation of a 16384-block pool; split count from the heuristic
-(32 on 256 CUs). A step is one decode of the whole batch (stage 1 + stage 2), inputs
-resident in HBM. Algorithmic bytes = KV reads only (reference src/bpt/roofline.py:1-4,
-bench/bench_triton_fp16.py:58): B * ctx * Hkv * 2 * D * 2 bytes for fp16.
+block table = a random permutation of a 16384-block pool; split count and workgroup
+size from the library's plan (kvq_plan_decode: 4 splits x 2 waves on 256 CUs). A step is
+one decode of the whole batch (stage 1 + stage 2), inputs resident in HBM. Algorithmic
+bytes = KV reads only (reference src/bpt/roofline.py:1-4, bench/bench_triton_fp16.py:58):
+B * ctx * Hkv * 2 * D * 2 bytes for fp16.
+
+--layers N times a whole-model decode step instead: N layers, each with its own cache of
+the --config shape, decoded back to back - eagerly, and replayed from one captured HIP
+graph - and prints one JSON line with µs per step (one token per sequence) and the
+aggregate KV-read TB/s (reference src/bpt/roofline.py:42-63 models the same 32-layer
+step for Llama-3-8B).
 
 Prints progress on stderr and ONE JSON line on stdout.
 """
@@ -117,6 +125,15 @@ class Step:
         self.lse = torch.empty(B, HQ, self.splits, dtype=torch.float32, device="cuda")
         self.stream = torch.cuda.current_stream().cuda_stream
         self.B = B
+        # the argument block holds raw pointers: keep the tensors they point into alive
+        # (a freed block can be returned to the device, e.g. by the empty_cache() that
+        # starts a graph capture, and a launch would then read unmapped memory)
+        self.inputs = (q, k, v, bt, sl, dict(fmt or {}))
+
+    def use_current_stream(self):
+        """Launch on torch's current stream from now on (e.g. a graph-capture stream)."""
+        import torch
+        self.stream = torch.cuda.current_stream().cuda_stream
 
     def stage1(self):
         a = self.ctypes.byref(self.args)
@@ -390,6 +407,60 @@ def run_config(config, steps, warmup, splits=None, waves=0, pipeline=0, flushed=
     return res, (q, k, v, bt, sl)
 
 
+def run_layers(config, layers, steps, warmup):
+    """Whole-model decode step: `layers` independent caches of the config's shape, one
+    decode each, back to back; timed eagerly and as replays of one captured HIP graph."""
+    import torch
+    B, ctx, pool, fmt_name, desc = CONFIGS[config]
+    step_list, lens = [], None
+    for layer in range(layers):
+        q, k, v, bt, sl, fmt = make_inputs(B, ctx, pool, seed=layer, kv_format=fmt_name)
+        lens = lens or [int(x) for x in sl.tolist()]
+        splits, waves = default_plan(config, B, bt.shape[1])
+        step_list.append(Step(q, k, v, bt, sl, splits, waves, 0, fmt))
+        if layer == 0:
+            log(f"{config} x {layers} layers: {desc}; splits={step_list[0].splits} "
+                f"waves={waves}")
+    torch.cuda.synchronize()
+    nbytes = kv_bytes(lens, fmt_name) * layers
+
+    def model_step():
+        for st in step_list:
+            st()
+
+    eager_wall, eager_ev = time_steps(model_step, steps, warmup)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for st in step_list:
+            st.use_current_stream()
+        model_step()
+    for st in step_list:
+        st.use_current_stream()
+    torch.cuda.synchronize()
+    graph_wall, graph_ev = time_steps(graph.replay, steps, warmup)
+    log(f"  eager {eager_wall * 1e3:.1f} us/step (events {eager_ev * 1e3:.1f}); graph "
+        f"{graph_wall * 1e3:.1f} us/step (events {graph_ev * 1e3:.1f}); "
+        f"{nbytes / 1e9:.2f} GB KV per step")
+    tbs = nbytes / (graph_wall * 1e-3) / 1e12
+    return {
+        "metric": f"whole-model decode step, attention only ({layers} layers): KV-read TB/s "
+                  "and µs per step", "value": round(tbs, 4), "unit": "TB/s", "n_gpus": 1,
+        "steps": steps, "warmup": warmup, "ms_per_step": round(graph_wall, 5),
+        "us_per_step": round(graph_wall * 1e3, 2),
+        "us_per_step_eager": round(eager_wall * 1e3, 2),
+        "tokens_per_s": round(B / (graph_wall * 1e-3), 1),
+        "pct_of_hbm_peak": round(100 * tbs * 1e3 / PEAK_GBPS, 2),
+        "roofline_min_us": round(nbytes / (PEAK_GBPS * 1e9) * 1e6, 2),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": fmt_name,
+        "data": "synthetic: per-layer q, K, V ~ N(0,1) fp16 (seed = layer index)",
+        "config": {"workload": f"{desc}, {layers} layers", "layers": layers, "batch": B,
+                   "sum_seq_lens": sum(lens), "kv_bytes_per_step": nbytes,
+                   "num_splits": step_list[0].splits, "graph": True, "kv_format": fmt_name},
+    }
+
+
 def sweep(args):
     import torch
     B, ctx, pool, fmt_name, _ = CONFIGS[args.config]
@@ -439,6 +510,8 @@ def main():
                     help="only the copy of known size (run under rocprofv3 --pmc)")
     ap.add_argument("--profile-run", type=int, default=0, metavar="STEPS",
                     help="only STEPS untimed steps of --config (run under rocprofv3 --pmc)")
+    ap.add_argument("--layers", type=int, default=0,
+                    help="time a whole-model step of N layers of --config (HIP graph)")
     ap.add_argument("--traffic-summary", metavar="PMC_DIR",
                     help="write profiles/decode_split_<config>_traffic.txt from PMC_DIR/"
                          "{copy_fetch,copy_write,fetch,write}")
@@ -459,6 +532,10 @@ def main():
         return
     if args.sweep:
         sweep(args)
+        return
+    if args.layers:
+        print(json.dumps(run_layers(args.config, args.layers, args.steps, args.warmup)),
+              flush=True)
         return
     import torch
     names = list(CONFIGS) if args.suite else [args.config]
