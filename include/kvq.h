@@ -126,13 +126,14 @@ int kvq_choose_num_splits(int32_t batch, int32_t kv_heads, int32_t block_size,
  *              wave for fp16; quantized 256, or 64 when batch * kv_heads > cu_count, so that
  *              uneven sequence lengths still balance), capped at pow2_floor(chunks / 4);
  *              chunks = max_pages * block_size / 16
- *   waves = min(Wmax, per_pair) with Wmax = 2 (fp16) or 1 (quantized),
+ *   waves = min(2, per_pair) for fp16; clamp(per_pair / 8, 1, 4) for quantized,
  *   splits = per_pair / waves
  * fp16 streams fastest with about 2 waves per CU, each 2 chunks (16 KB) ahead, spread
  * over at least one workgroup per CU; more waves in flight lower the achieved bandwidth.
- * The quantized kernels run best with single-wave workgroups, about 4 per CU for uniform
- * lengths and small partitions for large ragged batches (all measured on MI355X for batch
- * 1..64 and 32k..128k contexts). Writes both outputs (splits before
+ * The quantized kernels run best with about 4 waves per CU, at most 8 splits per
+ * (sequence, kv head) and, for large ragged batches, several waves per workgroup on small
+ * partitions (all measured on MI355X for batch 1..64 and 32k..128k contexts). Writes
+ * both outputs (splits before
  * kvq_normalize_splits); returns KVQ_OK or an error. */
 int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t max_pages,
                     int32_t kv_format, int32_t cu_count, int32_t* splits_out,

@@ -357,8 +357,13 @@ int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t
     if (per_pair < balance) per_pair = balance;
     const int64_t cap = pow2_floor(chunks / 4);
     if (per_pair > cap) per_pair = cap;
-    const int64_t max_waves = quant ? 1 : 2;
-    const int64_t waves = per_pair < max_waves ? per_pair : max_waves;
+    // fp16: up to 2 waves per workgroup. Quantized: one wave per 8 units of per_pair, up
+    // to 4, so that large ragged batches get fewer, larger splits (less partial traffic)
+    int64_t waves = per_pair < 2 ? per_pair : 2;
+    if (quant) {
+        waves = per_pair / 8;
+        waves = waves < 1 ? 1 : (waves > 4 ? 4 : waves);
+    }
     *waves_out = int32_t(waves);
     *splits_out = int32_t(per_pair / waves);
     return KVQ_OK;
