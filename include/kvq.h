@@ -121,16 +121,17 @@ int kvq_choose_num_splits(int32_t batch, int32_t kv_heads, int32_t block_size,
 /* MI355X work plan used when the caller gives no split count; takes the place of the
  * heuristic above (triton_fp16.py:175-180) on this hardware. It sizes the decomposition
  * in waves, because a workgroup here holds several waves that combine through LDS:
- *   per_pair = pow2_floor(T * cu_count / (batch * kv_heads)), T = 2 waves per CU (fp16)
- *              or 4 (quantized), raised to pow2_floor(cdiv(chunks, C)) (C = 512 chunks per
+ *   per_pair = pow2_floor(T * cu_count / (batch * kv_heads)), T = 2 waves per CU (fp16),
+ *              4 (INT8, FP8) or 8 (INT4), raised to pow2_floor(cdiv(chunks, C)) (C = 512 chunks per
  *              wave for fp16; quantized 256, or 64 when batch * kv_heads > cu_count, so that
  *              uneven sequence lengths still balance), capped at pow2_floor(chunks / 4);
  *              chunks = max_pages * block_size / 16
- *   waves = min(2, per_pair) for fp16; clamp(per_pair / 8, 1, 4) for quantized,
+ *   waves = min(2, per_pair) for fp16; clamp(per_pair / 8, 1, Wq) for quantized (Wq = 4;
+ *           INT4 8),
  *   splits = per_pair / waves
  * fp16 streams fastest with about 2 waves per CU, each 2 chunks (16 KB) ahead, spread
  * over at least one workgroup per CU; more waves in flight lower the achieved bandwidth.
- * The quantized kernels run best with about 4 waves per CU, at most 8 splits per
+ * The quantized kernels run best with about 4 (INT4: 8) waves per CU, at most 8 splits per
  * (sequence, kv head) and, for large ragged batches, several waves per workgroup on small
  * partitions (all measured on MI355X for batch 1..64 and 32k..128k contexts). Writes
  * both outputs (splits before

@@ -347,7 +347,9 @@ int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t
     const bool quant = kv_format != KVQ_KV_F16;
     const int64_t chunks = int64_t(max_pages) * (block_size / 16);
     const int64_t pairs = int64_t(batch) * kv_heads;
-    const int64_t waves_per_cu = quant ? 4 : 2;
+    // INT4 moves half the bytes per token of INT8 / FP8 through the same per-chunk work,
+    // so it needs twice the waves in flight to keep HBM busy
+    const int64_t waves_per_cu = kv_format == KVQ_KV_INT4 ? 8 : quant ? 4 : 2;
     // quantized: 256-chunk partitions while (sequence, kv head) pairs alone do not fill
     // the CUs, 64-chunk partitions beyond (large batches, where ragged lengths need small
     // work items to balance)
@@ -358,11 +360,13 @@ int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t
     const int64_t cap = pow2_floor(chunks / 4);
     if (per_pair > cap) per_pair = cap;
     // fp16: up to 2 waves per workgroup. Quantized: one wave per 8 units of per_pair, up
-    // to 4, so that large ragged batches get fewer, larger splits (less partial traffic)
+    // to 4 (INT4: 8), so that long or many sequences get fewer, larger splits (less
+    // partial traffic)
     int64_t waves = per_pair < 2 ? per_pair : 2;
     if (quant) {
+        const int64_t wmax = kv_format == KVQ_KV_INT4 ? 8 : 4;
         waves = per_pair / 8;
-        waves = waves < 1 ? 1 : (waves > 4 ? 4 : waves);
+        waves = waves < 1 ? 1 : (waves > wmax ? wmax : waves);
     }
     *waves_out = int32_t(waves);
     *splits_out = int32_t(per_pair / waves);

@@ -74,6 +74,7 @@ template <>
 struct QFmt<KVQ_KV_INT8> {
     static constexpr float F = 16777216.f;  // 2^24
     static constexpr int KLOADS = 2, VBYTES = 8;
+    static constexpr bool VROWS = false;
     __device__ static int chan_base(int st, int g) { return 64 * (st >> 1) + 16 * g + 8 * (st & 1); }
     static constexpr bool permuted() { return false; }
     __device__ static h8 kop(const u4v* kr, int st) {
@@ -109,6 +110,7 @@ template <>
 struct QFmt<KVQ_KV_FP8_E4M3> {
     static constexpr float F = 1.f;
     static constexpr int KLOADS = 2, VBYTES = 8;
+    static constexpr bool VROWS = false;
     __device__ static int chan_base(int st, int g) { return 64 * (st >> 1) + 16 * g + 8 * (st & 1); }
     static constexpr bool permuted() { return false; }
     __device__ static h8 kop(const u4v* kr, int st) {
@@ -143,12 +145,14 @@ struct QFmt<KVQ_KV_FP8_E4M3> {
 
 // INT4: K rows of 64 bytes, lane (token, g) loads bytes [16g, +16) (channels [32g, +32));
 // k-step st uses dword st: halves in code order {0,4, 1,5, 2,6, 3,7} of channels 32g + 8st,
-// the odd codes at 2^-20 (w = 16). V: 4 bytes (8 codes) per token row per lane; tile t =
-// code t of the lane's 8, odd tiles at 2^-20.
+// the odd codes at 2^-20 (w = 16). V: the lane needs 4 bytes (8 codes) of each of its 4
+// token rows; the rows are loaded whole (16 lanes per 1 KB instruction) and regrouped
+// through LDS (vstage_i4). Tile t = code t of the lane's 8, odd tiles at 2^-20.
 template <>
 struct QFmt<KVQ_KV_INT4> {
     static constexpr float F = 16777216.f;  // 2^24
     static constexpr int KLOADS = 1, VBYTES = 4;
+    static constexpr bool VROWS = true;  // V loaded in whole rows, staged through LDS (vstage_i4)
     __device__ static int chan_base(int st, int g) { return 32 * g + 8 * st; }
     static constexpr bool permuted() { return true; }
     __device__ static h8 kop(const u4v* kr, int st) {
@@ -181,7 +185,8 @@ struct QFmt<KVQ_KV_INT4> {
 template <int FMT>
 struct ChunkQ {
     u4v k[QFmt<FMT>::KLOADS];
-    uint32_t v[4][QFmt<FMT>::VBYTES / 4];
+    uint32_t v[4][QFmt<FMT>::VBYTES / 4];  // V by token row (formats without VROWS)
+    u4v vr;                                // V whole rows: row l/4, bytes [16(l%4), +16)
     u4v vsz;
     u2 ksz;
 };
@@ -215,6 +220,7 @@ __device__ __forceinline__ QLaneOff lane_offsets(const DecodeParams& p, int i16,
 #pragma unroll
     for (int r = 0; r < 4; ++r)
         o.v[r] = (uint32_t)(min(4 * g + r, last) * (int)p.v_stok + Q::VBYTES * i16);
+    if constexpr (Q::VROWS) o.v[0] = (uint32_t)(min(lane >> 2, last) * (int)p.v_stok + 16 * (lane & 3));
     o.vs = 16 * g;
     o.ks = 8 * lane;
     return o;
@@ -270,6 +276,9 @@ __device__ __forceinline__ void load_chunk_q(const QBase& B, int c, const QLaneO
 #pragma unroll
     for (int j = 0; j < Q::KLOADS; ++j)
         ch.k[j] = __builtin_amdgcn_raw_buffer_load_b128(B.k, lo.k[j], ko, kNT);
+    if constexpr (Q::VROWS) {
+        ch.vr = __builtin_amdgcn_raw_buffer_load_b128(B.v, lo.v[0], vo, kNT);
+    } else {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         if constexpr (Q::VBYTES == 8) {
@@ -279,6 +288,7 @@ __device__ __forceinline__ void load_chunk_q(const QBase& B, int c, const QLaneO
         } else {
             ch.v[r][0] = __builtin_amdgcn_raw_buffer_load_b32(B.v, lo.v[r], vo, kNT);
         }
+    }
     }
     // V (scale, zero) pairs of tokens slot + 4g .. +3 (16 bytes; slots past the sequence
     // hold garbage and are masked by selects, never multiplied)
@@ -323,6 +333,35 @@ __device__ __forceinline__ void k_operand(const ChunkQ<FMT>& ch, char* kst, int 
         kstage_q(ch.k, kst, g, kr);
     } else {
         kr[0] = ch.k[0];
+    }
+}
+
+// INT4 V rows (16 rows of 64 bytes, lane l holding row l/4, dwords [4(l%4), +4)) to the
+// PV operand's grouping (lane (i16, g) needs dword i16 of rows 4g .. 4g + 3) through the
+// wave's LDS tile. Dword c of row R sits at 80 (R / 4) + 16 (R % 4) + c: the 16-byte row
+// writes and the 4-byte reads (rows 4g + r, column i16: 80g + 16r + i16) each hit distinct
+// banks, so neither conflicts.
+__device__ __forceinline__ void vstage_i4(u4v vr, char* kst, int i16, int g,
+                                          uint32_t (*v)[1]) {
+    const int lane = __lane_id();
+    const int row = lane >> 2;
+    uint32_t* t = (uint32_t*)kst;
+    *(u4v*)(t + 80 * (row >> 2) + 16 * (row & 3) + 4 * (lane & 3)) = vr;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r][0] = t[80 * g + 16 * r + i16];
+}
+
+// The chunk's V codes grouped by token row as vtiles takes them.
+template <int FMT>
+__device__ __forceinline__ void v_rows(const ChunkQ<FMT>& ch, char* kst, int i16, int g,
+                                       uint32_t (*v)[QFmt<FMT>::VBYTES / 4]) {
+    if constexpr (QFmt<FMT>::VROWS) {
+        vstage_i4(ch.vr, kst, i16, g, v);
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int j = 0; j < QFmt<FMT>::VBYTES / 4; ++j) v[r][j] = ch.v[r][j];
     }
 }
 
@@ -433,6 +472,9 @@ __device__ __forceinline__ void chunk_q(const ChunkQ<FMT>& ch, const h8* qhi, co
                                         float csl, float sl2f, int valid, int g, char* kst,
                                         SoftmaxState<128>& st, float& corr) {
     typedef QFmt<FMT> Q;
+    // V regrouped first (INT4: through LDS), so that its latency overlaps the QK product
+    uint32_t vrows[4][Q::VBYTES / 4];
+    v_rows<FMT>(ch, kst, __lane_id() & 15, g, vrows);
     u4v kr[Q::KLOADS];
     k_operand<FMT>(ch, kst, g, kr);
     float s2[4];
@@ -464,7 +506,7 @@ __device__ __forceinline__ void chunk_q(const ChunkQ<FMT>& ch, const h8* qhi, co
     h4 phi, plo;
     pv_weights<MASK>(pr, ch.vsz, valid, g, phi, plo, corr);
     uint32_t a01[8], a23[8];
-    Q::vtiles(ch.v, a01, a23);
+    Q::vtiles(vrows, a01, a23);
     if constexpr (SPLIT) {
         // column h takes p hi, column h + 8 p lo (the lanes of a pair hold the same p)
         const h4 pop = (__lane_id() & 8) ? plo : phi;
@@ -502,6 +544,10 @@ __device__ __forceinline__ void chunk_pair(const ChunkQ<FMT>& ca, const ChunkQ<F
                                            int valid_b, int g, int slot, bool lo_part,
                                            char* kst, SoftmaxState<128>& st, float& corr) {
     typedef QFmt<FMT> Q;
+    // V regrouped first (INT4: through LDS), so that its latency overlaps the QK products
+    uint32_t va[4][Q::VBYTES / 4], vb[4][Q::VBYTES / 4];
+    v_rows<FMT>(ca, kst, __lane_id() & 15, g, va);
+    v_rows<FMT>(cb, kst, __lane_id() & 15, g, vb);
     f4 sa = (f4)0.f, sb = (f4)0.f;
     {
         u4v kr[Q::KLOADS];
@@ -540,8 +586,8 @@ __device__ __forceinline__ void chunk_pair(const ChunkQ<FMT>& ca, const ChunkQ<F
     pbw[3] = slot ? pw[1] : 0u;
     const h8 pb = __builtin_bit_cast(h8, pbw);
     uint32_t a01[8], a23[8], b01[8], b23[8];
-    Q::vtiles(ca.v, a01, a23);
-    Q::vtiles(cb.v, b01, b23);
+    Q::vtiles(va, a01, a23);
+    Q::vtiles(vb, b01, b23);
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
         const u4v w = {a01[t], a23[t], b01[t], b23[t]};
@@ -688,7 +734,7 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
             for (int r = 0; r < 4; ++r) st.acc[t][r] += ror8(st.acc[t][r]);
     }
     tile_weights<FMT>(st);
-    if constexpr (Q::KLOADS == 2) __syncthreads();  // every wave is done with its K tile
+    __syncthreads();  // every wave is done with its LDS staging tile
     combine_store<D, W, FINAL>(p, st.acc, Q::F, rows_sum(corr), st.m, rows_sum(st.l), wave, i16,
                                g, kvh, split, b);
 }
@@ -823,12 +869,12 @@ __global__ __launch_bounds__(W * 64) void decode_q2_kernel(const DecodeParams p)
         st.m = M;
     }
     tile_weights<FMT>(st);
-    if constexpr (Q::KLOADS == 2) __syncthreads();  // every wave is done with its K tile
+    __syncthreads();  // every wave is done with its LDS staging tile
     combine_store<D, W, FINAL>(p, st.acc, Q::F, rows_sum(corr), st.m, rows_sum(st.l), wave, i16,
                                g, kvh, split, b);
 }
 
-// LDS: region 0 (the cross-wave combine, or the INT8 / FP8 K tiles), one 512-byte K-scale
+// LDS: region 0 (the cross-wave combine, or the waves' 2 KB staging tiles), one 512-byte K-scale
 // slot per wave, then q in k-operand order (4 KB)
 template <int W>
 static size_t q_shmem(const DecodeParams& p, int fmt) {

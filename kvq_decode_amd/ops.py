@@ -64,10 +64,11 @@ def plan_decode(batch: int, kv_heads: int, block_size: int, max_pages: int,
     split-KV decomposition the reference's heuristic aims at (triton_fp16.py:175-180:
     enough programs to fill the GPU, no tiny splits), counted in waves because one
     workgroup here holds several waves that combine through LDS. Computed by the library
-    (kvq_plan_decode): about 2 waves per CU for fp16 and 4 for quantized caches, at most
+    (kvq_plan_decode): about 2 waves per CU for fp16, 4 for INT8 / FP8 and 8 for INT4, at most
     512 (fp16) / 256 or, for batches whose (sequence, kv head) pairs outnumber the CUs, 64
     (quantized) 16-token chunks per wave; up to 2 waves per workgroup for fp16, and for
-    quantized caches one wave per 8 waves of the (sequence, kv head) pair, up to 4."""
+    quantized caches one wave per 8 waves of the (sequence, kv head) pair, up to 4 (INT4:
+    8)."""
     _require(kv_format in KV_FORMATS, f"kv_format must be one of {tuple(KV_FORMATS)}")
     s, w = ctypes.c_int32(), ctypes.c_int32()
     _lib.check("kvq_plan_decode",

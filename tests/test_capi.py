@@ -78,10 +78,13 @@ def test_plan_decode():
         (16, 2048, "fp16", (2, 2)),
         (1, 8192, "fp16", (32, 2)),     # 64 per pair
         (64, 2048, "fp16", (2, 2)),     # raised to 4 per pair: <= 512 chunks per wave
-        (16, 2048, "int4", (8, 1)),     # quantized: single-wave workgroups, 4 waves/CU
+        (16, 2048, "int4", (8, 2)),     # INT4: 8 waves per CU, 16 per pair
+        (16, 2048, "int8", (8, 1)),     # INT8 / FP8: 4 waves per CU, single-wave workgroups
         (64, 2048, "int8", (8, 4)),     # 512 pairs > 256 CUs: 64-chunk partitions, 4 waves
-        (1, 4096, "int4", (32, 4)),     # 128 per pair: 4 waves per workgroup
-        (8, 2048, "int4", (8, 2)),      # 16 per pair
+        (1, 4096, "int4", (32, 8)),     # 256 per pair: 8 waves per workgroup (INT4 cap)
+        (1, 4096, "int8", (32, 4)),     # 128 per pair: 4 waves per workgroup (INT8 cap)
+        (8, 2048, "int4", (8, 4)),      # 32 per pair
+        (8, 2048, "fp8_e4m3", (8, 2)),  # 16 per pair
         (64, 64, "fp16", (1, 1)),       # 1 per pair from 2 waves/CU
         (2, 3, "fp16", (1, 1)),         # at least 4 chunks per wave
     ]
