@@ -66,15 +66,19 @@ constexpr float kM0 = -1e30f;
 template <int FMT>
 struct QFmt;
 
+// Per format: KLOADS / VLOADS = 16-byte-per-lane K / V loads per 16-token chunk (whole
+// rows), VBYTES = bytes of each of its 4 token rows a lane needs for the PV operand, TILE =
+// bytes of the wave's LDS staging tiles (K rows for INT8 / FP8, then V rows).
+//
 // INT8 / FP8 share the byte layout: K rows of 128 bytes; after the LDS staging (kstage_q)
 // lane (token l%16, g) holds bytes [64j + 16g, +16) for j = 0, 1; k-step st = 2j + u uses
-// dwords 2u, 2u+1, i.e. channels 64*(st/2) + 16g + 8*(st%2) + e in order. V: 8 bytes per
-// token row per lane, tile t = byte t of the lane's 8.
+// dwords 2u, 2u+1, i.e. channels 64*(st/2) + 16g + 8*(st%2) + e in order. V: 8 bytes of
+// each token row per lane (regrouped from whole rows by vstage_i8), tile t = byte t of the
+// lane's 8.
 template <>
 struct QFmt<KVQ_KV_INT8> {
     static constexpr float F = 16777216.f;  // 2^24
-    static constexpr int KLOADS = 2, VBYTES = 8;
-    static constexpr bool VROWS = false;
+    static constexpr int KLOADS = 2, VBYTES = 8, VLOADS = 2, TILE = 4608;
     __device__ static int chan_base(int st, int g) { return 64 * (st >> 1) + 16 * g + 8 * (st & 1); }
     static constexpr bool permuted() { return false; }
     __device__ static h8 kop(const u4v* kr, int st) {
@@ -109,8 +113,7 @@ __device__ __forceinline__ uint32_t f8_hi(uint32_t x) {
 template <>
 struct QFmt<KVQ_KV_FP8_E4M3> {
     static constexpr float F = 1.f;
-    static constexpr int KLOADS = 2, VBYTES = 8;
-    static constexpr bool VROWS = false;
+    static constexpr int KLOADS = 2, VBYTES = 8, VLOADS = 2, TILE = 4608;
     __device__ static int chan_base(int st, int g) { return 64 * (st >> 1) + 16 * g + 8 * (st & 1); }
     static constexpr bool permuted() { return false; }
     __device__ static h8 kop(const u4v* kr, int st) {
@@ -151,8 +154,7 @@ struct QFmt<KVQ_KV_FP8_E4M3> {
 template <>
 struct QFmt<KVQ_KV_INT4> {
     static constexpr float F = 16777216.f;  // 2^24
-    static constexpr int KLOADS = 1, VBYTES = 4;
-    static constexpr bool VROWS = true;  // V loaded in whole rows, staged through LDS (vstage_i4)
+    static constexpr int KLOADS = 1, VBYTES = 4, VLOADS = 1, TILE = 2048;
     __device__ static int chan_base(int st, int g) { return 32 * g + 8 * st; }
     static constexpr bool permuted() { return true; }
     __device__ static h8 kop(const u4v* kr, int st) {
@@ -185,8 +187,7 @@ struct QFmt<KVQ_KV_INT4> {
 template <int FMT>
 struct ChunkQ {
     u4v k[QFmt<FMT>::KLOADS];
-    uint32_t v[4][QFmt<FMT>::VBYTES / 4];  // V by token row (formats without VROWS)
-    u4v vr;                                // V whole rows: row l/4, bytes [16(l%4), +16)
+    u4v vr[QFmt<FMT>::VLOADS];  // V whole rows (vstage_i4 / vstage_i8 give the layouts)
     u4v vsz;
     u2 ksz;
 };
@@ -198,10 +199,12 @@ struct ChunkQ {
 //   K, INT8 / FP8 (128-byte rows): load j row min(8j + l/8, last), bytes [16(l%8), +16) -
 //     each instruction covers 8 whole rows (every 128-byte line in one instruction); the
 //     rows reach the k-operand layout through the wave's LDS tile (kstage_q);
-//   V rows min(4g + r, last) bytes [VBYTES * (l%16), +VBYTES), the V (scale, zero) pairs
-//   of tokens 4g..4g+3 (16 bytes), and the K group's pairs of channels 2l, 2l+1 (8 bytes).
+//   V, the same whole-row pattern: INT4 row min(l/4, last) bytes [16(l%4), +16); INT8 /
+//     FP8 load j row min(8j + l/8, last) bytes [16(l%8), +16) (regrouped by vstage_*);
+//   the V (scale, zero) pairs of tokens 4g..4g+3 (16 bytes), and the K group's pairs of
+//   channels 2l, 2l+1 (8 bytes).
 struct QLaneOff {
-    uint32_t k[2], v[4], vs, ks;
+    uint32_t k[2], v[2], vs, ks;
 };
 
 template <int FMT>
@@ -217,10 +220,13 @@ __device__ __forceinline__ QLaneOff lane_offsets(const DecodeParams& p, int i16,
         for (int j = 0; j < 2; ++j)
             o.k[j] = (uint32_t)(min(8 * j + (lane >> 3), last) * (int)p.k_stok + 16 * (lane & 7));
     }
+    if constexpr (Q::VLOADS == 1) {  // 64-byte rows: 16 per instruction
+        o.v[0] = (uint32_t)(min(lane >> 2, last) * (int)p.v_stok + 16 * (lane & 3));
+    } else {  // 128-byte rows: 8 per instruction
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-        o.v[r] = (uint32_t)(min(4 * g + r, last) * (int)p.v_stok + Q::VBYTES * i16);
-    if constexpr (Q::VROWS) o.v[0] = (uint32_t)(min(lane >> 2, last) * (int)p.v_stok + 16 * (lane & 3));
+        for (int j = 0; j < 2; ++j)
+            o.v[j] = (uint32_t)(min(8 * j + (lane >> 3), last) * (int)p.v_stok + 16 * (lane & 7));
+    }
     o.vs = 16 * g;
     o.ks = 8 * lane;
     return o;
@@ -276,20 +282,9 @@ __device__ __forceinline__ void load_chunk_q(const QBase& B, int c, const QLaneO
 #pragma unroll
     for (int j = 0; j < Q::KLOADS; ++j)
         ch.k[j] = __builtin_amdgcn_raw_buffer_load_b128(B.k, lo.k[j], ko, kNT);
-    if constexpr (Q::VROWS) {
-        ch.vr = __builtin_amdgcn_raw_buffer_load_b128(B.v, lo.v[0], vo, kNT);
-    } else {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        if constexpr (Q::VBYTES == 8) {
-            const u2 x = __builtin_amdgcn_raw_buffer_load_b64(B.v, lo.v[r], vo, kNT);
-            ch.v[r][0] = x[0];
-            ch.v[r][Q::VBYTES / 4 - 1] = x[1];
-        } else {
-            ch.v[r][0] = __builtin_amdgcn_raw_buffer_load_b32(B.v, lo.v[r], vo, kNT);
-        }
-    }
-    }
+    for (int j = 0; j < Q::VLOADS; ++j)
+        ch.vr[j] = __builtin_amdgcn_raw_buffer_load_b128(B.v, lo.v[j], vo, kNT);
     // V (scale, zero) pairs of tokens slot + 4g .. +3 (16 bytes; slots past the sequence
     // hold garbage and are masked by selects, never multiplied)
     const uint32_t so = (uint32_t)phys * B.vs_blk + 4 * slot;
@@ -341,27 +336,47 @@ __device__ __forceinline__ void k_operand(const ChunkQ<FMT>& ch, char* kst, int 
 // wave's LDS tile. Dword c of row R sits at 80 (R / 4) + 16 (R % 4) + c: the 16-byte row
 // writes and the 4-byte reads (rows 4g + r, column i16: 80g + 16r + i16) each hit distinct
 // banks, so neither conflicts.
-__device__ __forceinline__ void vstage_i4(u4v vr, char* kst, int i16, int g,
+__device__ __forceinline__ void vstage_i4(const u4v* vr, char* vst, int i16, int g,
                                           uint32_t (*v)[1]) {
     const int lane = __lane_id();
     const int row = lane >> 2;
-    uint32_t* t = (uint32_t*)kst;
-    *(u4v*)(t + 80 * (row >> 2) + 16 * (row & 3) + 4 * (lane & 3)) = vr;
+    uint32_t* t = (uint32_t*)vst;
+    *(u4v*)(t + 80 * (row >> 2) + 16 * (row & 3) + 4 * (lane & 3)) = vr[0];
 #pragma unroll
     for (int r = 0; r < 4; ++r) v[r][0] = t[80 * g + 16 * r + i16];
 }
 
-// The chunk's V codes grouped by token row as vtiles takes them.
+// INT8 / FP8 V rows (16 rows of 128 bytes; load j: lane l holds row 8j + l/8, dwords
+// [4(l%8), +4)) to the PV grouping (lane (i16, g) needs dwords 2 i16, 2 i16 + 1 of rows
+// 4g .. 4g + 3) through the wave's 2.5 KB V tile. Dword c of row R sits at
+// 160 (R / 4) + 32 (R % 4) + c: the 8-byte reads of lanes with g and g + 1 fall in opposite
+// halves of 64 banks, the 16-byte writes of 8 lanes cover 32 distinct banks.
+__device__ __forceinline__ void vstage_i8(const u4v* vr, char* vst, int i16, int g,
+                                          uint32_t (*v)[2]) {
+    const int lane = __lane_id();
+    uint32_t* t = (uint32_t*)vst;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int row = 8 * j + (lane >> 3);
+        *(u4v*)(t + 160 * (row >> 2) + 32 * (row & 3) + 4 * (lane & 7)) = vr[j];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const u2 x = *(const u2*)(t + 160 * g + 32 * r + 2 * i16);
+        v[r][0] = x[0];
+        v[r][1] = x[1];
+    }
+}
+
+// The chunk's V codes grouped by token row as vtiles takes them. The V tile follows the
+// wave's 2 KB K tile for INT8 / FP8 and takes its place for INT4 (no K staging).
 template <int FMT>
 __device__ __forceinline__ void v_rows(const ChunkQ<FMT>& ch, char* kst, int i16, int g,
                                        uint32_t (*v)[QFmt<FMT>::VBYTES / 4]) {
-    if constexpr (QFmt<FMT>::VROWS) {
+    if constexpr (QFmt<FMT>::VLOADS == 1) {
         vstage_i4(ch.vr, kst, i16, g, v);
     } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-            for (int j = 0; j < QFmt<FMT>::VBYTES / 4; ++j) v[r][j] = ch.v[r][j];
+        vstage_i8(ch.vr, kst + 2048, i16, g, v);
     }
 }
 
@@ -647,7 +662,7 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
     // 2 KB K tiles.
     extern __shared__ float smem[];
     const int r0 = quant_lds_region0(W, G, FMT);
-    char* kst = (char*)smem + wave * 2048;
+    char* kst = (char*)smem + wave * Q::TILE;
     h8* qsh = (h8*)(smem + r0 + W * 128);
     if (wave == 0) stage_q<FMT>(p, b, kvh, i16, g, qsh);
     __syncthreads();
@@ -765,7 +780,7 @@ __global__ __launch_bounds__(W * 64) void decode_q2_kernel(const DecodeParams p)
 
     extern __shared__ float smem[];
     const int r0 = quant_lds_region0(W, G, FMT);
-    char* kst = (char*)smem + wave * 2048;
+    char* kst = (char*)smem + wave * Q::TILE;
     h8* qsh = (h8*)(smem + r0 + W * 128);
     if (wave == 0) stage_q<FMT>(p, b, kvh, i16, g, qsh);
     __syncthreads();

@@ -46,12 +46,12 @@ hipError_t launch_decode(const DecodeParams& p, int kv_format, int head_dim, boo
 
 // Floats of LDS region 0 of the quantized decode kernel (decode_q.hip) with `waves` waves
 // per workgroup: the cross-wave combine ([waves][group][128] accumulators + [waves][16] m
-// and l), or the waves' 2 KB staging tiles if larger (INT8 / FP8 K rows, INT4 V rows; the
-// tiles are used before the combine).
+// and l), or the waves' staging tiles if larger (INT8 / FP8: a 2 KB K tile and a 2.5 KB V
+// tile, 4608 bytes per wave; INT4: a V tile in 2 KB per wave; the tiles are used before
+// the combine).
 __host__ __device__ inline int quant_lds_region0(int waves, int group, int kv_format) {
-    (void)kv_format;
     const int combine = waves * group * 128 + 2 * waves * 16;
-    const int tiles = waves * 512;
+    const int tiles = waves * (kv_format == KVQ_KV_INT4 ? 512 : 1152);
     return combine > tiles ? combine : tiles;
 }
 
