@@ -283,11 +283,13 @@ void decode_f16_kernel(const DecodeParams p) {
                                split, b);
 }
 
-// Stage 2 (reference _merge_kernel, triton_fp16.py:147-163): one workgroup of 256 threads
-// per (q head, sequence) = 8 groups of 32 threads; a thread owns D/32 consecutive columns
-// and its group folds splits g, g+8, ... First the global max of lse (every thread scans
-// all splits: S floats, cache-resident), so the weighted sum needs no rescaling and its
-// loads are independent; then the 8 groups are summed through LDS.
+// Stage 2 (reference _merge_kernel, triton_fp16.py:147-163): out = sum_s w_s o_s / sum_s w_s
+// with w_s = exp(lse_s - max lse). One workgroup of 256 threads per (q head, sequence) = 8
+// groups of 32 threads; a thread owns D/32 consecutive columns and its group folds splits
+// g, g+8, ... with a running max (in log2 units), rescaling its sums when the max grows,
+// so every load of a split is independent of the others and of the max (one memory round
+// trip instead of a max pass before the sum). The 8 groups are then combined through LDS
+// against their common max. Empty splits (lse = -inf) get weight 0.
 template <int D>
 __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ o_part,
                                                     const float* __restrict__ lse,
@@ -297,35 +299,50 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ o_
     const int hq = blockIdx.x, b = blockIdx.y;
     const int t = threadIdx.x, lane32 = t & 31, grp = t >> 5;
     const int64_t row0 = ((int64_t)b * q_heads + hq) * S;
-    const float* L = lse + row0;
-    float M = -INFINITY;
-    for (int s = 0; s < S; ++s) M = fmaxf(M, L[s]);
-    float wsum = 0.f;
+    float m = -INFINITY, wsum = 0.f;
     float acc[PER];
 #pragma unroll
     for (int e = 0; e < PER; ++e) acc[e] = 0.f;
-    if (M > -INFINITY) {
 #pragma unroll 4
-        for (int s = grp; s < S; s += 8) {
-            const float w = fast_exp2((L[s] - M) * kLog2e);
-            const float* src = o_part + (row0 + s) * D + lane32 * PER;
-            wsum += w;
+    for (int s = grp; s < S; s += 8) {
+        const float l = lse[row0 + s] * kLog2e;
+        const float* src = o_part + (row0 + s) * D + lane32 * PER;
+        float o[PER];
 #pragma unroll
-            for (int e = 0; e < PER; ++e) acc[e] += w * src[e];
+        for (int e = 0; e < PER; ++e) o[e] = src[e];
+        if (l > m) {  // the running max grows: rescale what is summed so far
+            const float r = fast_exp2(m - l);  // 0 while nothing is summed (m = -inf)
+            wsum *= r;
+#pragma unroll
+            for (int e = 0; e < PER; ++e) acc[e] *= r;
+            m = l;
         }
+        const float w = l > -INFINITY ? fast_exp2(l - m) : 0.f;
+        wsum += w;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) acc[e] += w * o[e];
     }
     __shared__ float sm_acc[8][D];
-    __shared__ float sm_w[8];
+    __shared__ float sm_m[8], sm_w[8];
 #pragma unroll
     for (int e = 0; e < PER; ++e) sm_acc[grp][lane32 * PER + e] = acc[e];
-    if (lane32 == 0) sm_w[grp] = wsum;
+    if (lane32 == 0) {
+        sm_m[grp] = m;
+        sm_w[grp] = wsum;
+    }
     __syncthreads();
+    float M = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) M = fmaxf(M, sm_m[g]);
     for (int d = t; d < D; d += 256) {
         float o = 0.f, W = 0.f;
+        if (M > -INFINITY) {
 #pragma unroll
-        for (int g = 0; g < 8; ++g) {
-            o += sm_acc[g][d];
-            W += sm_w[g];
+            for (int g = 0; g < 8; ++g) {
+                const float r = sm_m[g] > -INFINITY ? fast_exp2(sm_m[g] - M) : 0.f;
+                o += r * sm_acc[g][d];
+                W += r * sm_w[g];
+            }
         }
         out[(int64_t)b * o_sb + (int64_t)hq * o_sh + d] = (_Float16)(W > 0.f ? o / W : 0.f);
     }
