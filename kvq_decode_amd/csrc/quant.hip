@@ -91,15 +91,19 @@ __device__ __forceinline__ void store_pair(uint8_t* row, int j, uint32_t c0, uin
     }
 }
 
-// K: per (kv head, group, sequence), thread j owns channels 2j, 2j+1 (D/2 threads).
-// `src_row(t)` returns the fp16 row of token t of the group; codes go to the token's page
-// slot, scale/zero to the group's first block.
+// K: per (kv head, group, sequence), 256 threads: thread (j, ts) owns channels 2j, 2j+1
+// (j < D/2) of the group's rows t0 + ts, t0 + ts + TS, ... (TS = 512 / D row slices).
+// Pass 1 reduces min / max over each slice, then across the slices through LDS; pass 2
+// encodes the slice's rows with the group's (scale, zero). Codes go to each token's page
+// slot, the pairs to the group's first block. Append: the group holding the newest token,
+// read from the fp16 residual except the new row itself (from k_new), which also joins
+// the residual for later appends.
 template <int FMT, bool APPEND>
-__global__ __launch_bounds__(128) void quant_k_kernel(const QuantParams p) {
+__global__ __launch_bounds__(256) void quant_k_kernel(const QuantParams p) {
     const int kvh = blockIdx.x, grp = blockIdx.y, b = blockIdx.z;
-    const int j = threadIdx.x;
     const int D = p.head_dim;
-    if (2 * j >= D) return;
+    const int TS = 512 / D;                // row slices
+    const int j = threadIdx.x % (D / 2), ts = threadIdx.x / (D / 2);
     const int n = seq_len_of(p, b);
     int t0 = grp * p.k_group, t1 = min(t0 + p.k_group, n);
     if (APPEND) {  // only the group holding the newest token, rows 0..(n-1) % k_group
@@ -107,10 +111,10 @@ __global__ __launch_bounds__(128) void quant_k_kernel(const QuantParams p) {
         t0 = ((n - 1) / p.k_group) * p.k_group;
         t1 = n;
     }
-    if (t0 >= t1) return;
+    if (t0 >= t1) return;  // uniform over the workgroup
     const int64_t resid = ((int64_t)b * p.kv_heads + kvh) * p.k_group * D;
-    if (APPEND) {  // the new token's K joins the fp16 residual of its group
-        const _Float16* kn = p.k_new + ((int64_t)b * p.kv_heads + kvh) * D + 2 * j;
+    const _Float16* kn = p.k_new + ((int64_t)b * p.kv_heads + kvh) * D + 2 * j;
+    if (APPEND && ts == 0) {  // the new token's K joins the fp16 residual of its group
         _Float16* dst = p.k_resid + resid + (int64_t)(t1 - 1 - t0) * D + 2 * j;
         dst[0] = kn[0];
         dst[1] = kn[1];
@@ -118,7 +122,7 @@ __global__ __launch_bounds__(128) void quant_k_kernel(const QuantParams p) {
     auto load = [&](int t, float& x0, float& x1) {
         const _Float16* src;
         if (APPEND) {
-            src = p.k_resid + resid + (int64_t)(t - t0) * D + 2 * j;
+            src = t == t1 - 1 ? kn : p.k_resid + resid + (int64_t)(t - t0) * D + 2 * j;
         } else {
             const int phys = phys_of(p, b, t / p.block_size);
             src = p.k_src + (int64_t)phys * p.s_sblk + (int64_t)(t % p.block_size) * p.s_stok +
@@ -128,7 +132,8 @@ __global__ __launch_bounds__(128) void quant_k_kernel(const QuantParams p) {
         x1 = (float)src[1];
     };
     float mn0 = INFINITY, mx0 = -INFINITY, mn1 = INFINITY, mx1 = -INFINITY;
-    for (int t = t0; t < t1; ++t) {
+#pragma unroll 8
+    for (int t = t0 + ts; t < t1; t += TS) {
         float x0, x1;
         load(t, x0, x1);
         mn0 = fminf(mn0, x0);
@@ -136,8 +141,32 @@ __global__ __launch_bounds__(128) void quant_k_kernel(const QuantParams p) {
         mn1 = fminf(mn1, x1);
         mx1 = fmaxf(mx1, x1);
     }
-    const ScaleZero q0 = make_params<FMT>(mn0, mx0), q1 = make_params<FMT>(mn1, mx1);
-    for (int t = t0; t < t1; ++t) {
+    __shared__ float4 part[256];       // per thread: (mn0, mx0, mn1, mx1)
+    __shared__ float4 params[128];     // per channel pair: (s0, z0, s1, z1)
+    part[threadIdx.x] = make_float4(mn0, mx0, mn1, mx1);
+    __syncthreads();
+    if (ts == 0) {
+        for (int k = 1; k < TS; ++k) {
+            const float4 o = part[k * (D / 2) + j];
+            mn0 = fminf(mn0, o.x);
+            mx0 = fmaxf(mx0, o.y);
+            mn1 = fminf(mn1, o.z);
+            mx1 = fmaxf(mx1, o.w);
+        }
+        const ScaleZero q0 = make_params<FMT>(mn0, mx0), q1 = make_params<FMT>(mn1, mx1);
+        params[j] = make_float4(q0.s, q0.z, q1.s, q1.z);
+        // (scale, zero) pairs of channels 2j, 2j + 1: one 8-byte store
+        const int lead = phys_of(p, b, t0 / p.block_size);
+        const int64_t sz = ((int64_t)lead * p.kv_heads + kvh) * D + 2 * j;
+        typedef _Float16 h4q __attribute__((ext_vector_type(4)));
+        const h4q pairs = {(_Float16)q0.s, (_Float16)q0.z, (_Float16)q1.s, (_Float16)q1.z};
+        *(h4q*)(p.k_scale + 2 * sz) = pairs;
+    }
+    __syncthreads();
+    const float4 pr = params[j];
+    const ScaleZero q0 = {pr.x, pr.y}, q1 = {pr.z, pr.w};
+#pragma unroll 8
+    for (int t = t0 + ts; t < t1; t += TS) {
         float x0, x1;
         load(t, x0, x1);
         const int phys = phys_of(p, b, t / p.block_size);
@@ -145,12 +174,6 @@ __global__ __launch_bounds__(128) void quant_k_kernel(const QuantParams p) {
                        (int64_t)(t % p.block_size) * p.k_stok + (int64_t)kvh * p.k_sh;
         store_pair<FMT>(row, j, encode<FMT>(x0, q0), encode<FMT>(x1, q1));
     }
-    // (scale, zero) pairs of channels 2j, 2j + 1: one 8-byte store
-    const int lead = phys_of(p, b, t0 / p.block_size);
-    const int64_t sz = ((int64_t)lead * p.kv_heads + kvh) * D + 2 * j;
-    typedef _Float16 h4q __attribute__((ext_vector_type(4)));
-    const h4q pairs = {(_Float16)q0.s, (_Float16)q0.z, (_Float16)q1.s, (_Float16)q1.z};
-    *(h4q*)(p.k_scale + 2 * sz) = pairs;
 }
 
 // V: one token row (D channels of one kv head) per 16 lanes, each lane D/16 channels.
@@ -200,7 +223,7 @@ template <int FMT, bool APPEND>
 hipError_t launch_fmt(const QuantParams& p, hipStream_t stream) {
     const int groups = APPEND ? 1 : p.max_groups;
     hipLaunchKernelGGL((quant_k_kernel<FMT, APPEND>), dim3(p.kv_heads, groups, p.batch),
-                       dim3(p.head_dim / 2), 0, stream, p);
+                       dim3(256), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int tok_wgs = APPEND ? 1 : (p.max_blocks * p.block_size + 15) / 16;
