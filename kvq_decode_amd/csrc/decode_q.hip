@@ -658,8 +658,8 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
     const QBase base = q_base(p, kvh);
 
     // LDS: [region 0][K-scale slots, 512 B per wave][q, 4 KB] (launch_q). Region 0 holds
-    // the cross-wave combine after the chunk loop and, before it, the INT8 / FP8 waves'
-    // 2 KB K tiles.
+    // the cross-wave combine after the chunk loop and, before it, the waves' staging tiles
+    // (Q::TILE bytes each: INT8 / FP8 K and V rows, INT4 V rows).
     extern __shared__ float smem[];
     const int r0 = quant_lds_region0(W, G, FMT);
     char* kst = (char*)smem + wave * Q::TILE;
@@ -917,6 +917,8 @@ static hipError_t launch_q2(const DecodeParams& p, hipStream_t stream) {
 // one MFMA chain, any ring depth. 9 to 16 heads: two chains, ring depth 4.
 template <int FMT, bool FINAL, int W>
 static hipError_t launch_q_g(const DecodeParams& p, int ring, hipStream_t stream) {
+    // pair kernel: ring 4 -> 8 chunks in flight, else 4 (a pair computes while P - 2 load);
+    // single-chunk kernel: the ring depth as given (two chains above 8 heads: 4)
     if (p.group <= 4 && p.k_group_chunks >= 2)
         return ring == 4 ? launch_q2<FMT, W, FINAL, 8>(p, stream)
                          : launch_q2<FMT, W, FINAL, 4>(p, stream);

@@ -58,6 +58,7 @@ def choose_num_splits(batch: int, kv_heads: int, block_size: int, max_pages: int
     return _lib.check("kvq_choose_num_splits", s)
 
 
+@functools.lru_cache(maxsize=4096)  # a pure function of its arguments; saves a C call per op
 def plan_decode(batch: int, kv_heads: int, block_size: int, max_pages: int,
                 cu_count: int, kv_format: str = "fp16") -> Tuple[int, int]:
     """(num_splits, waves_per_group) for the MI355X kernels when num_splits is None: the
@@ -83,6 +84,7 @@ def auto_splits(batch: int, kv_heads: int, block_size: int, max_pages: int,
     return plan_decode(batch, kv_heads, block_size, max_pages, cu_count, kv_format)[0]
 
 
+@functools.lru_cache(maxsize=4096)
 def normalize_splits(num_splits: int, max_pages: int) -> Tuple[int, int]:
     """(splits, pages_per_split) after the reference's clamp/re-derivation
     (triton_fp16.py:211-217)."""
