@@ -1,5 +1,5 @@
 """Decode-step benchmark on one MI355X: achieved KV-read bandwidth of the paged-KV GQA
-decode path (split-KV stage 1 + merge) against the 8 TB/s HBM3E roofline.
+decode path (stage 1 + merge) against the 8 TB/s HBM3E roofline.
 
     python bench.py [--steps K] [--warmup W] [--config C2] [--splits S]
     python bench.py --sweep            # split / workgroup sweep, table on stderr
@@ -7,9 +7,9 @@ decode path (split-KV stage 1 + merge) against the 8 TB/s HBM3E roofline.
 
 Workload ("C2"): Llama-3-8B GQA layer (32 q heads, 8 kv heads,
 head_dim 128), batch 8, every sequence 32768 tokens, block_size 16, q/K/V ~ N(0,1) fp16,
-block table = a random permutation of a 16384-block pool; split count and workgroup
-size from the library's plan (kvq_plan_decode: 4 splits x 2 waves on 256 CUs). A step is
-one decode of the whole batch (stage 1 + stage 2), inputs resident in HBM. Algorithmic
+block table = a random permutation of a 16384-block pool; partition from the library's
+plan (kvq_plan_units: 32 work units of 2 waves per kv head on 256 CUs). A step is one
+decode of the whole batch (stage 1 + stage 2), inputs resident in HBM. Algorithmic
 bytes = KV reads only (reference src/bpt/roofline.py:1-4, bench/bench_triton_fp16.py:58):
 B * ctx * Hkv * 2 * D * 2 bytes for fp16.
 
@@ -105,9 +105,10 @@ def kv_bytes(lens, kv_format):
 
 class Step:
     """One decode step through the C ABI with prebuilt arguments and workspace, so the
-    timed loop issues exactly the library's launches (split + merge, or single pass)."""
+    timed loop issues exactly the library's launches (work units + merge, split + merge,
+    or single pass). units > 0 selects the work-unit partition."""
 
-    def __init__(self, q, k, v, bt, sl, splits, waves=0, pipeline=0, fmt=None):
+    def __init__(self, q, k, v, bt, sl, splits, waves=0, pipeline=0, fmt=None, units=0):
         import ctypes
 
         import torch
@@ -118,11 +119,16 @@ class Step:
         self.check = _lib.check
         B = q.shape[0]
         self.out = torch.empty_like(q)
-        self.splits, self.pps = ops.normalize_splits(splits, bt.shape[1])
+        self.units = units
+        self.splits, self.pps = (0, 0) if units else ops.normalize_splits(splits, bt.shape[1])
         self.args = ops.build_args(q, k, v, bt, sl, self.out, 1.0 / math.sqrt(D),
                                    waves_per_group=waves, pipeline=pipeline, **(fmt or {}))
-        self.o_part = torch.empty(B, HQ, self.splits, D, dtype=torch.float32, device="cuda")
-        self.lse = torch.empty(B, HQ, self.splits, dtype=torch.float32, device="cuda")
+        if units:
+            o_shape, l_shape = ops.units_workspace_shapes(B, HQ, D, units)
+        else:
+            o_shape, l_shape = ops.workspace_shapes(B, HQ, D, self.splits)
+        self.o_part = torch.empty(o_shape, dtype=torch.float32, device="cuda")
+        self.lse = torch.empty(l_shape, dtype=torch.float32, device="cuda")
         self.stream = torch.cuda.current_stream().cuda_stream
         self.B = B
         # the argument block holds raw pointers: keep the tensors they point into alive
@@ -137,7 +143,11 @@ class Step:
 
     def stage1(self):
         a = self.ctypes.byref(self.args)
-        if self.splits == 1:
+        if self.units:
+            self.check("kvq_decode_units_split",
+                       self.L.kvq_decode_units_split(a, self.units, self.o_part.data_ptr(),
+                                                     self.lse.data_ptr(), self.stream))
+        elif self.splits == 1:
             self.check("kvq_decode_single", self.L.kvq_decode_single(a, self.stream))
         else:
             self.check("kvq_decode_split",
@@ -145,7 +155,12 @@ class Step:
                                                self.lse.data_ptr(), self.stream))
 
     def stage2(self):
-        if self.splits > 1:
+        if self.units:
+            self.check("kvq_decode_units_merge",
+                       self.L.kvq_decode_units_merge(self.ctypes.byref(self.args), self.units,
+                                                     self.o_part.data_ptr(), self.lse.data_ptr(),
+                                                     self.stream))
+        elif self.splits > 1:
             self.check("kvq_decode_merge",
                        self.L.kvq_decode_merge(self.o_part.data_ptr(), self.lse.data_ptr(),
                                                self.out.data_ptr(), self.out.stride(0),
@@ -230,11 +245,16 @@ def cpu_baseline(q, k, v, bt, sl):
             "s_per_step": sec}
 
 
-def read_traffic(workload, splits):
+def plan_text(step):
+    """The partition of a Step, as recorded in the traffic summaries."""
+    return f"units {step.units}" if step.units else f"splits {step.splits}"
+
+
+def read_traffic(workload, plan):
     """HBM bytes per stage-1 launch measured by rocprofv3 --pmc, if a summary for this
-    workload and split count is committed under profiles/, else None. The file holds
-    `key = value` lines; `splits` must match and `hbm_bytes_per_launch` is returned."""
-    path = os.path.join(REPO, "profiles", f"decode_split_{workload}_traffic.txt")
+    workload and partition (plan_text) is committed under profiles/, else None. The file
+    holds `key = value` lines; `plan` must match and `hbm_bytes_per_launch` is returned."""
+    path = os.path.join(REPO, "profiles", f"decode_{workload}_traffic.txt")
     if not os.path.exists(path):
         return None
     vals = {}
@@ -244,7 +264,7 @@ def read_traffic(workload, splits):
                 key, val = line.split("=", 1)
                 vals[key.strip()] = val.strip()
     try:
-        if int(vals.get("splits", -1)) != splits:
+        if vals.get("plan") != plan:
             return None
         return float(vals["hbm_bytes_per_launch"])
     except (KeyError, ValueError):
@@ -272,12 +292,12 @@ def profile_run(config, steps):
     import torch
     B, ctx, pool, fmt_name, _ = CONFIGS[config]
     q, k, v, bt, sl, fmt = make_inputs(B, ctx, pool, kv_format=fmt_name)
-    splits, waves = default_plan(config, B, bt.shape[1])
-    step = Step(q, k, v, bt, sl, splits, waves, 0, fmt)
+    splits, waves, units = default_plan(config, B, bt.shape[1])
+    step = Step(q, k, v, bt, sl, splits, waves, 0, fmt, units)
     for _ in range(steps):
         step()
     torch.cuda.synchronize()
-    log(f"profile run: {config} splits={step.splits} waves={waves} x {steps} steps")
+    log(f"profile run: {config} {plan_text(step)} waves={waves} x {steps} steps")
 
 
 def _pmc_means(csv_dir, name_has):
@@ -296,33 +316,35 @@ def _pmc_means(csv_dir, name_has):
     return sum(vals.values()) / len(vals), len(vals)
 
 
-def stage1_kernel(fmt_name, group=HQ // HKV):
-    """Name of the stage-1 kernel for a format: decode_f16_kernel, or for quantized
-    caches decode_q2_kernel (1 to 4 q heads per kv head) / decode_q_kernel."""
+def stage1_kernel(fmt_name, units=False, group=HQ // HKV):
+    """Name of the stage-1 kernel for a format and partition: decode_f16_units_kernel /
+    decode_q_units_kernel (work units), else decode_f16_kernel, or for quantized caches
+    decode_q2_kernel (1 to 4 q heads per kv head) / decode_q_kernel."""
+    if units:
+        return "decode_f16_units_kernel" if fmt_name == "fp16" else "decode_q_units_kernel"
     if fmt_name == "fp16":
         return "decode_f16_kernel"
     return "decode_q2_kernel" if group <= 4 else "decode_q_kernel"
 
 
 def traffic_summary(config, pmc_dir):
-    """Writes profiles/decode_split_<config>_traffic.txt from four rocprofv3 --pmc runs
-    under pmc_dir: copy_fetch/, copy_write/ (calibrate_copy) and fetch/, write/
-    (profile_run). Counter values are scaled by the copy's known bytes per counter unit."""
+    """Writes profiles/decode_<config>_traffic.txt from four rocprofv3 --pmc runs under
+    pmc_dir: copy_fetch/, copy_write/ (calibrate_copy) and fetch/, write/ (profile_run).
+    Counter values are scaled by the copy's known bytes per counter unit."""
     B, ctx, pool, fmt_name, desc = CONFIGS[config]
-    kernel = stage1_kernel(fmt_name)
+    lens = seq_lengths(B, ctx)
+    max_pages = max(-(-x // BS) for x in lens)
+    splits, waves, units = default_plan(config, B, max_pages, cu_count=256)
+    from kvq_decode_amd import ops
+    plan = f"units {units}" if units else f"splits {ops.normalize_splits(splits, max_pages)[0]}"
+    kernel = stage1_kernel(fmt_name, units)
     cf, _ = _pmc_means(os.path.join(pmc_dir, "copy_fetch"), "copy")
     cw, _ = _pmc_means(os.path.join(pmc_dir, "copy_write"), "copy")
     kf, n = _pmc_means(os.path.join(pmc_dir, "fetch"), kernel)
     kw, _ = _pmc_means(os.path.join(pmc_dir, "write"), kernel)
     copy_bytes = 4 * COPY_ELEMS
     rf, wf = copy_bytes / cf, copy_bytes / cw
-    lens = seq_lengths(B, ctx)
     algo = kv_bytes(lens, fmt_name)
-    from kvq_decode_amd import ops
-    max_pages = max(-(-x // BS) for x in lens)
-    splits, waves = (1, 0) if config == "C1" else ops.plan_decode(B, HKV, BS, max_pages, 256,
-                                                                   fmt_name)
-    splits = ops.normalize_splits(splits, max_pages)[0]
     rd, wr = kf * rf, kw * wf
     lines = [
         f"# HBM traffic of one stage-1 launch ({kernel}), {desc}",
@@ -339,7 +361,7 @@ def traffic_summary(config, pmc_dir):
         f"{config} --profile-run 10",
         f"#   python3 bench.py --config {config} --traffic-summary D",
         f"config = {config}",
-        f"splits = {splits}",
+        f"plan = {plan}",
         f"waves_per_group = {waves}",
         f"dispatches = {n}",
         f"fetch_size_per_dispatch = {kf:.1f}",
@@ -354,33 +376,42 @@ def traffic_summary(config, pmc_dir):
         f"algorithmic_bytes_per_launch = {algo}",
         f"traffic_over_algorithmic = {(rd + wr) / algo:.4f}",
     ]
-    path = os.path.join(REPO, "profiles", f"decode_split_{config}_traffic.txt")
+    path = os.path.join(REPO, "profiles", f"decode_{config}_traffic.txt")
     with open(path, "w") as f:
         f.write("\n".join(lines) + "\n")
     log("\n".join(lines))
     log(f"wrote {path}")
 
 
-def default_plan(config, B, max_pages):
-    """(splits, waves) the op would use with num_splits=None (C1: no split, configs[0])."""
+def default_plan(config, B, max_pages, cu_count=None):
+    """(splits, waves, units) the op would use with num_splits=None: the work-unit plan
+    (units > 0) where the library prefers it, else the split plan (C1: no split,
+    configs[0])."""
     from kvq_decode_amd import _sm_count
-    from kvq_decode_amd.ops import plan_decode
+    from kvq_decode_amd.ops import plan_decode, plan_units
     if config == "C1":
-        return 1, 0
-    return plan_decode(B, HKV, BS, max_pages, _sm_count(0), CONFIGS[config][3])
+        return 1, 0, 0
+    cus = cu_count or _sm_count(0)
+    fmt_name = CONFIGS[config][3]
+    units, waves = plan_units(B, HKV, BS, max_pages, cus, fmt_name)
+    if units:
+        return 0, waves, units
+    return (*plan_decode(B, HKV, BS, max_pages, cus, fmt_name), 0)
 
 
-def run_config(config, steps, warmup, splits=None, waves=0, pipeline=0, flushed=True):
-    """Measure one configuration; returns the result fields (no CPU baseline)."""
+def run_config(config, steps, warmup, splits=None, waves=0, pipeline=0, flushed=True,
+               units=0):
+    """Measure one configuration; returns the result fields (no CPU baseline). With
+    neither `splits` nor `units` given, the op's default plan."""
     B, ctx, pool, fmt_name, desc = CONFIGS[config]
     q, k, v, bt, sl, fmt = make_inputs(B, ctx, pool, kv_format=fmt_name)
     lens = [int(x) for x in sl.tolist()]
-    if splits is None:
-        splits, planned = default_plan(config, B, bt.shape[1])
+    if splits is None and not units:
+        splits, planned, units = default_plan(config, B, bt.shape[1])
         waves = waves or planned
-    step = Step(q, k, v, bt, sl, splits, waves, pipeline, fmt)
+    step = Step(q, k, v, bt, sl, splits, waves, pipeline, fmt, units)
     nbytes = kv_bytes(lens, fmt_name)
-    log(f"{config}: {desc}; splits={step.splits} pages/split={step.pps} KV bytes/step={nbytes}")
+    log(f"{config}: {desc}; {plan_text(step)} pages/split={step.pps} KV bytes/step={nbytes}")
     wall_ms, ev_ms = time_steps(step, steps, warmup)
     stage1_ms = time_stage1(step, max(20, min(steps, 100)))
     flushed_ms = time_flushed(step, 30) if flushed else None
@@ -388,7 +419,7 @@ def run_config(config, steps, warmup, splits=None, waves=0, pipeline=0, flushed=
         f"{stage1_ms * 1e3:.1f} us" + (f", flushed median {flushed_ms * 1e3:.1f} us" if flushed else ""))
     tbs = nbytes / (wall_ms * 1e-3) / 1e12
     achieved = nbytes / (stage1_ms * 1e-3) / 1e9
-    kernel = stage1_kernel(fmt_name)
+    kernel = stage1_kernel(fmt_name, step.units)
     res = {
         "value": round(tbs, 4), "ms_per_step": round(wall_ms, 5),
         "us_per_step": round(wall_ms * 1e3, 2),
@@ -396,12 +427,14 @@ def run_config(config, steps, warmup, splits=None, waves=0, pipeline=0, flushed=
         "us_per_step_flushed_median": round(flushed_ms * 1e3, 2) if flushed else None,
         "config": {"workload": desc, "batch": B, "seq_len": ctx if ctx else "U[1024,32768]",
                    "sum_seq_lens": sum(lens), "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
-                   "block_size": BS, "pool_blocks": k.shape[0], "num_splits": step.splits,
+                   "block_size": BS, "pool_blocks": k.shape[0],
+                   "partition": "work units" if step.units else "split-KV",
+                   "units_per_kv_head": step.units, "num_splits": step.splits,
                    "pages_per_split": step.pps, "waves_per_group": waves,
                    "kv_bytes_per_step": nbytes, "kv_format": fmt_name},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
-                     "traffic": read_traffic(config, step.splits),
+                     "traffic": read_traffic(config, plan_text(step)),
                      "kernel": f"{kernel} (stage 1)", "kernel_us": round(stage1_ms * 1e3, 2)},
     }
     return res, (q, k, v, bt, sl)
@@ -416,10 +449,10 @@ def run_layers(config, layers, steps, warmup):
     for layer in range(layers):
         q, k, v, bt, sl, fmt = make_inputs(B, ctx, pool, seed=layer, kv_format=fmt_name)
         lens = lens or [int(x) for x in sl.tolist()]
-        splits, waves = default_plan(config, B, bt.shape[1])
-        step_list.append(Step(q, k, v, bt, sl, splits, waves, 0, fmt))
+        splits, waves, units = default_plan(config, B, bt.shape[1])
+        step_list.append(Step(q, k, v, bt, sl, splits, waves, 0, fmt, units))
         if layer == 0:
-            log(f"{config} x {layers} layers: {desc}; splits={step_list[0].splits} "
+            log(f"{config} x {layers} layers: {desc}; {plan_text(step_list[0])} "
                 f"waves={waves}")
     torch.cuda.synchronize()
     nbytes = kv_bytes(lens, fmt_name) * layers
@@ -457,7 +490,8 @@ def run_layers(config, layers, steps, warmup):
         "data": "synthetic: per-layer q, K, V ~ N(0,1) fp16 (seed = layer index)",
         "config": {"workload": f"{desc}, {layers} layers", "layers": layers, "batch": B,
                    "sum_seq_lens": sum(lens), "kv_bytes_per_step": nbytes,
-                   "num_splits": step_list[0].splits, "graph": True, "kv_format": fmt_name},
+                   "partition": plan_text(step_list[0]), "graph": True,
+                   "kv_format": fmt_name},
     }
 
 
@@ -495,7 +529,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="C2", choices=sorted(CONFIGS))
-    ap.add_argument("--splits", type=int, default=None, help="default: the op's heuristic")
+    ap.add_argument("--splits", type=int, default=None, help="default: the op's plan")
+    ap.add_argument("--units", type=int, default=0,
+                    help="work units per kv head (default: the op's plan)")
     ap.add_argument("--waves", type=int, default=0)
     ap.add_argument("--pipeline", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -513,7 +549,7 @@ def main():
     ap.add_argument("--layers", type=int, default=0,
                     help="time a whole-model step of N layers of --config (HIP graph)")
     ap.add_argument("--traffic-summary", metavar="PMC_DIR",
-                    help="write profiles/decode_split_<config>_traffic.txt from PMC_DIR/"
+                    help="write profiles/decode_<config>_traffic.txt from PMC_DIR/"
                          "{copy_fetch,copy_write,fetch,write}")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -541,7 +577,7 @@ def main():
     names = list(CONFIGS) if args.suite else [args.config]
     for name in names:
         res, inputs = run_config(name, args.steps, args.warmup, args.splits, args.waves,
-                                 args.pipeline)
+                                 args.pipeline, units=args.units)
         result = {"metric": METRIC, "value": res.pop("value"), "unit": "TB/s", "n_gpus": 1,
                   "steps": args.steps, "warmup": args.warmup, **res,
                   "higher_is_better": True, "scaling": "weak", "vs_baseline": None,

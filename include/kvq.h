@@ -140,6 +140,19 @@ int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t
                     int32_t kv_format, int32_t cu_count, int32_t* splits_out,
                     int32_t* waves_out);
 
+/* Work-unit plan, the library's default for batches of 2 to 256 sequences (no reference
+ * counterpart; it takes the place of the split heuristic, triton_fp16.py:175-180, where
+ * that would split). When kvq_plan_decode gives splits >= 2 and 2 <= batch <= 256:
+ *   units = T * cu_count / (waves * kv_heads) (at least 1), with T waves per CU and
+ *           `waves` per unit workgroup: fp16 T = 2, waves = 2; INT8 / FP8 T = 4,
+ *           waves = 4; INT4 T = 8, waves = 2,
+ * for kvq_decode_units; otherwise units = waves = 0 (use kvq_plan_decode's split plan).
+ * Units balance ragged batches (a static split count sizes every sequence's splits by
+ * the longest one); on uniform batches the two plans run within about 1% of each other
+ * on MI355X. Returns KVQ_OK or an error. */
+int kvq_plan_units(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t max_pages,
+                   int32_t kv_format, int32_t cu_count, int32_t* units_out, int32_t* waves_out);
+
 /* Split normalization, triton_fp16.py:211-217: clamps num_splits to [1, max_pages], then
  * pages_per_split = cdiv(max_pages, S) and S = cdiv(max_pages, pages_per_split).
  * Writes both; returns KVQ_OK or an error. */
@@ -173,6 +186,25 @@ int kvq_decode_single(const kvq_decode_args* args, kvq_stream_t stream);
  * when S == 1). */
 int kvq_paged_decode(const kvq_decode_args* args, int32_t num_splits, float* o_part,
                      float* lse, kvq_stream_t stream);
+
+/* Work-unit decode (no reference counterpart: another partition of the same two stages,
+ * triton_fp16.py:83-163, for ragged and large batches; every kv_format, batch at most 256).
+ * Per kv head, the 16-token chunks of all sequences, concatenated in batch order
+ * (sequence b has cdiv(seq_lens[b], 16) chunks, N in total), are cut into
+ * NU = min(units, N) equal ranges; one workgroup of args->waves_per_group waves (0 = 2;
+ * 1, 2 or 4) per (kv head, range) runs the part of each sequence its range overlaps, its
+ * waves sharing each part, so the work per workgroup does not depend on how the lengths
+ * are spread. Partial row of (range u, sequence b) = u + b. Workspace:
+ *   o_part fp32 [q_heads, units + batch, head_dim], lse fp32 [q_heads, units + batch].
+ * kvq_decode_units runs stage 1 (kvq_decode_units_split) and stage 2
+ * (kvq_decode_units_merge: each sequence's partial rows into args->out; an empty sequence
+ * gets a zero row). The output equals kvq_paged_decode's to rounding. */
+int kvq_decode_units(const kvq_decode_args* args, int32_t units, float* o_part, float* lse,
+                     kvq_stream_t stream);
+int kvq_decode_units_split(const kvq_decode_args* args, int32_t units, float* o_part,
+                           float* lse, kvq_stream_t stream);
+int kvq_decode_units_merge(const kvq_decode_args* args, int32_t units, const float* o_part,
+                           const float* lse, kvq_stream_t stream);
 
 /* Bulk KIVI quantization of fp16 paged caches (no reference counterpart: the reference's
  * quantized KV is "not started", README.md:16; its byte model is roofline.py:6-9).

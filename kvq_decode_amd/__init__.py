@@ -12,6 +12,9 @@ from kvq_decode_amd.ops import (  # noqa: F401
     choose_num_splits,
     normalize_splits,
     paged_decode_attention,
+    plan_decode,
+    plan_units,
+    units_workspace_shapes,
     workspace_shapes,
 )
 from kvq_decode_amd._lib import KvqError, version  # noqa: F401
@@ -22,6 +25,9 @@ __all__ = [
     "choose_num_splits",
     "normalize_splits",
     "workspace_shapes",
+    "units_workspace_shapes",
+    "plan_decode",
+    "plan_units",
     "TARGET_PROGRAMS_PER_SM",
     "MIN_TOKENS_PER_SPLIT",
     "KvqArgumentError",

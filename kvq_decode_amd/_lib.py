@@ -34,6 +34,10 @@ EXPORTED_SYMBOLS = (
     "kvq_decode_merge",
     "kvq_decode_single",
     "kvq_paged_decode",
+    "kvq_decode_units",
+    "kvq_decode_units_split",
+    "kvq_decode_units_merge",
+    "kvq_plan_units",
     "kvq_quantize_cache",
     "kvq_quantize_append",
     "kvq_append_kv",
@@ -94,6 +98,8 @@ def lib():
         L.kvq_choose_num_splits.argtypes = [_i32] * 7
         L.kvq_plan_decode.restype = ctypes.c_int
         L.kvq_plan_decode.argtypes = [_i32] * 6 + [ctypes.POINTER(_i32)] * 2
+        L.kvq_plan_units.restype = ctypes.c_int
+        L.kvq_plan_units.argtypes = [_i32] * 6 + [ctypes.POINTER(_i32)] * 2
         L.kvq_normalize_splits.restype = ctypes.c_int
         L.kvq_normalize_splits.argtypes = [_i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)]
         args_p = ctypes.POINTER(DecodeArgs)
@@ -105,6 +111,12 @@ def lib():
         L.kvq_decode_single.argtypes = [args_p, _vp]
         L.kvq_paged_decode.restype = ctypes.c_int
         L.kvq_paged_decode.argtypes = [args_p, _i32, _vp, _vp, _vp]
+        L.kvq_decode_units.restype = ctypes.c_int
+        L.kvq_decode_units.argtypes = [args_p, _i32, _vp, _vp, _vp]
+        L.kvq_decode_units_split.restype = ctypes.c_int
+        L.kvq_decode_units_split.argtypes = [args_p, _i32, _vp, _vp, _vp]
+        L.kvq_decode_units_merge.restype = ctypes.c_int
+        L.kvq_decode_units_merge.argtypes = [args_p, _i32, _vp, _vp, _vp]
         L.kvq_quantize_cache.restype = ctypes.c_int
         L.kvq_quantize_cache.argtypes = [args_p, _vp, _vp, _i64, _i64, _i64, _vp]
         L.kvq_quantize_append.restype = ctypes.c_int

@@ -301,6 +301,28 @@ kvq::AppendParams make_append_params(const kvq_decode_args* a, const void* k_new
     return p;
 }
 
+// Checks of the work-unit entry points; fills the launch parameters. The units kernels
+// read every seq_len of the batch in one workgroup (batch <= kUnitMaxBatch).
+int units_params(const kvq_decode_args* args, int32_t units, float* o_part, float* lse,
+                 kvq::DecodeParams* p, int* waves, int* pipe) {
+    int st = check_decode_args(args, true);
+    if (st != KVQ_OK) return st;
+    if (!o_part || !lse) return KVQ_ERR_NULL_POINTER;
+    if (args->batch > kvq::kUnitMaxBatch) return KVQ_ERR_UNSUPPORTED;
+    if (units < 1 || int64_t(units) * args->kv_heads > INT32_MAX ||
+        int64_t(units) + args->batch > INT32_MAX)
+        return KVQ_ERR_SPLITS;
+    *waves = args->waves_per_group == 0 ? 2 : args->waves_per_group;
+    if (*waves != 1 && *waves != 2 && *waves != 4) return KVQ_ERR_UNSUPPORTED;
+    *pipe = pick_pipeline(args);
+    if (*pipe == 0 || lds_bytes(args, *waves) > kLdsBudget) return KVQ_ERR_UNSUPPORTED;
+    *p = make_params(args);
+    p->o_part = o_part;
+    p->lse = lse;
+    p->units = units;
+    return KVQ_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -370,6 +392,29 @@ int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t
     }
     *waves_out = int32_t(waves);
     *splits_out = int32_t(per_pair / waves);
+    return KVQ_OK;
+}
+
+int kvq_plan_units(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t max_pages,
+                   int32_t kv_format, int32_t cu_count, int32_t* units_out, int32_t* waves_out) {
+    if (!units_out || !waves_out) return KVQ_ERR_NULL_POINTER;
+    int32_t splits = 0, split_waves = 0;
+    const int st = kvq_plan_decode(batch, kv_heads, block_size, max_pages, kv_format, cu_count,
+                                   &splits, &split_waves);
+    if (st != KVQ_OK) return st;
+    *units_out = 0;
+    *waves_out = 0;
+    // A single sequence cannot be ragged, and a plan without splits has no merge to share
+    if (batch < 2 || batch > kvq::kUnitMaxBatch || splits < 2) return KVQ_OK;
+    // Waves per CU and per unit workgroup, measured on MI355X: fp16 2 in workgroups of 2;
+    // INT8 / FP8 4 in workgroups of 4; INT4 (half the bytes of a chunk for about the
+    // same per-chunk work) 8 in workgroups of 2
+    const bool int4 = kv_format == KVQ_KV_INT4;
+    const int64_t waves_per_cu = kv_format == KVQ_KV_F16 ? 2 : int4 ? 8 : 4;
+    const int64_t waves = kv_format == KVQ_KV_F16 || int4 ? 2 : 4;
+    const int64_t units = waves_per_cu * cu_count / (waves * int64_t(kv_heads));
+    *units_out = int32_t(units < 1 ? 1 : units);
+    *waves_out = int32_t(waves);
     return KVQ_OK;
 }
 
@@ -449,6 +494,34 @@ int kvq_paged_decode(const kvq_decode_args* args, int32_t num_splits, float* o_p
     if (st != KVQ_OK) return st;
     return kvq_decode_merge(o_part, lse, args->out, args->o_stride_b, args->o_stride_h,
                             args->batch, args->q_heads, args->head_dim, s, stream);
+}
+
+int kvq_decode_units_split(const kvq_decode_args* args, int32_t units, float* o_part,
+                           float* lse, kvq_stream_t stream) {
+    kvq::DecodeParams p;
+    int waves = 0, pipe = 0;
+    const int st = units_params(args, units, o_part, lse, &p, &waves, &pipe);
+    if (st != KVQ_OK) return st;
+    return hip_status(kvq::launch_decode_units(p, args->kv_format, args->head_dim, waves, pipe,
+                                               reinterpret_cast<hipStream_t>(stream)));
+}
+
+int kvq_decode_units_merge(const kvq_decode_args* args, int32_t units, const float* o_part,
+                           const float* lse, kvq_stream_t stream) {
+    kvq::DecodeParams p;
+    int waves = 0, pipe = 0;
+    const int st = units_params(args, units, const_cast<float*>(o_part), const_cast<float*>(lse),
+                                &p, &waves, &pipe);
+    if (st != KVQ_OK) return st;
+    return hip_status(kvq::launch_merge_units(p, args->head_dim,
+                                              reinterpret_cast<hipStream_t>(stream)));
+}
+
+int kvq_decode_units(const kvq_decode_args* args, int32_t units, float* o_part, float* lse,
+                     kvq_stream_t stream) {
+    const int st = kvq_decode_units_split(args, units, o_part, lse, stream);
+    if (st != KVQ_OK) return st;
+    return kvq_decode_units_merge(args, units, o_part, lse, stream);
 }
 
 int kvq_quantize_cache(const kvq_decode_args* args, const void* k_src, const void* v_src,

@@ -201,22 +201,22 @@ __device__ __forceinline__ void chunk_f16(const ChunkF16<D>& ch, const h8* qop, 
 // (chunks past the wave's last fully valid chunk re-read that chunk and are not used), so
 // the compiler's vmcnt waits count exactly the loads in flight behind the awaited chunk
 // and never drain the ring. The sequence's partial last chunk is handled once after it.
+//
+// f16_range runs one wave's chunk range [w_lo, w_hi) of sequence b (of length seq_len)
+// for kv head kvh and stores the workgroup's result (partial rows part_base + h *
+// part_stride, or the output row for FINAL).
 template <int D, int W, bool FINAL, int P>
-__global__ __launch_bounds__(W * 64)
-void decode_f16_kernel(const DecodeParams p) {
+__device__ __forceinline__ void f16_range(const DecodeParams& p, int kvh, int b, int seq_len,
+                                          int w_lo, int w_hi, int wave, int64_t part_base,
+                                          int64_t part_stride) {
     constexpr int NST = D / 32;
     constexpr int DV = D / 16;
 
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const WgCoord wc = wg_coord(p, FINAL ? 1 : p.num_splits);
-    if (!wc.live) return;
-    const int kvh = wc.kvh, split = wc.split, b = wc.b;
     const int i16 = lane & 15, g = lane >> 4;
     const int G = p.group;
     const bool head_ok = i16 < G;
-    const WaveRange wr = wave_range<W>(p, b, split, wave);
-    const int seq_len = wr.seq_len, w_lo = wr.w_lo, w_hi = wr.w_hi;
+    const int c_full = seq_len >> 4;  // chunks below this index are fully valid
 
     // Q^T operand: lane (head i16, g) holds Q[head][32*k + 8*g + 0..7]; padded heads = 0.
     h8 qop[NST];
@@ -242,7 +242,7 @@ void decode_f16_kernel(const DecodeParams p) {
     extern __shared__ float smem[];
     char* kst = (char*)smem + wave * 32 * D;
 
-    const int r_hi = min(w_hi, wr.c_full);
+    const int r_hi = min(w_hi, c_full);
     if (w_lo < r_hi) {
         const F16LaneOff<D> lo = f16_lane_offsets<D>(p, i16, g, 15);
         const int last = r_hi - 1;
@@ -279,26 +279,41 @@ void decode_f16_kernel(const DecodeParams p) {
     }
 
     __syncthreads();  // every wave is done with its staging tile
-    combine_store<D, W, FINAL>(p, st.acc, 1.f, 0.f, st.m, rows_sum(st.l), wave, i16, g, kvh,
-                               split, b);
+    combine_store<D, W, FINAL>(p, st.acc, 1.f, 0.f, st.m, rows_sum(st.l), wave, i16, g, kvh, b,
+                               part_base, part_stride);
 }
 
-// Stage 2 (reference _merge_kernel, triton_fp16.py:147-163): out = sum_s w_s o_s / sum_s w_s
-// with w_s = exp(lse_s - max lse). One workgroup of 256 threads per (q head, sequence) = 8
-// groups of 32 threads; a thread owns D/32 consecutive columns and its group folds splits
-// g, g+8, ... with a running max (in log2 units), rescaling its sums when the max grows,
-// so every load of a split is independent of the others and of the max (one memory round
-// trip instead of a max pass before the sum). The 8 groups are then combined through LDS
-// against their common max. Empty splits (lse = -inf) get weight 0.
+// Split-KV stage 1 / single pass: workgroup = (kv head, split, sequence), W waves.
+template <int D, int W, bool FINAL, int P>
+__global__ __launch_bounds__(W * 64)
+void decode_f16_kernel(const DecodeParams p) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const WgCoord wc = wg_coord(p, FINAL ? 1 : p.num_splits);
+    if (!wc.live) return;
+    const WaveRange wr = wave_range<W>(p, wc.b, wc.split, wave);
+    f16_range<D, W, FINAL, P>(p, wc.kvh, wc.b, wr.seq_len, wr.w_lo, wr.w_hi, wave,
+                              split_part_base(p, wc.b, wc.split), p.num_splits);
+}
+
+// Work units (decode_common.h UnitSpace): workgroup = (kv head, unit), W waves; the unit
+// runs one segment per sequence its chunk range overlaps, its waves sharing each segment.
+template <int D, int W, int P>
+__global__ __launch_bounds__(W * 64)
+void decode_f16_units_kernel(const DecodeParams p) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    for_unit_segments<W>(p, [&](int kvh, int b, int seq_len, int w_lo, int w_hi, int64_t base,
+                                int64_t stride) {
+        f16_range<D, W, false, P>(p, kvh, b, seq_len, w_lo, w_hi, wave, base, stride);
+    });
+}
+
+// Merges the S partial rows row0 .. row0 + S - 1 into the fp16 output row `out`.
 template <int D>
-__global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ o_part,
-                                                    const float* __restrict__ lse,
-                                                    _Float16* __restrict__ out, int64_t o_sb,
-                                                    int64_t o_sh, int q_heads, int S) {
+__device__ __forceinline__ void merge_rows(const float* __restrict__ o_part,
+                                           const float* __restrict__ lse, int64_t row0, int S,
+                                           _Float16* __restrict__ out) {
     constexpr int PER = D / 32;  // columns per thread (1..8)
-    const int hq = blockIdx.x, b = blockIdx.y;
     const int t = threadIdx.x, lane32 = t & 31, grp = t >> 5;
-    const int64_t row0 = ((int64_t)b * q_heads + hq) * S;
     float m = -INFINITY, wsum = 0.f;
     float acc[PER];
 #pragma unroll
@@ -344,8 +359,57 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ o_
                 W += r * sm_w[g];
             }
         }
-        out[(int64_t)b * o_sb + (int64_t)hq * o_sh + d] = (_Float16)(W > 0.f ? o / W : 0.f);
+        out[d] = (_Float16)(W > 0.f ? o / W : 0.f);
     }
+}
+
+// Stage 2 (reference _merge_kernel, triton_fp16.py:147-163): out = sum_s w_s o_s / sum_s w_s
+// with w_s = exp(lse_s - max lse). One workgroup of 256 threads per (q head, sequence) = 8
+// groups of 32 threads; a thread owns D/32 consecutive columns and its group folds splits
+// g, g+8, ... with a running max (in log2 units), rescaling its sums when the max grows,
+// so every load of a split is independent of the others and of the max (one memory round
+// trip instead of a max pass before the sum). The 8 groups are then combined through LDS
+// against their common max. Empty splits (lse = -inf) get weight 0.
+template <int D>
+__global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ o_part,
+                                                    const float* __restrict__ lse,
+                                                    _Float16* __restrict__ out, int64_t o_sb,
+                                                    int64_t o_sh, int q_heads, int S) {
+    const int hq = blockIdx.x, b = blockIdx.y;
+    merge_rows<D>(o_part, lse, ((int64_t)b * q_heads + hq) * S, S,
+                  out + (int64_t)b * o_sb + (int64_t)hq * o_sh);
+}
+
+// Stage 2 of the work units (decode_common.h UnitSpace): sequence b's partials of q head hq
+// are rows hq * (units + B) + u + b for its units u = first .. last, where first / last
+// hold its first / last chunk. Workgroup = (q head, sequence), 256 threads; the prefix P_b
+// and the total N come from one block reduction over seq_lens (B <= 256).
+template <int D>
+__global__ __launch_bounds__(256) void merge_units_kernel(const DecodeParams p) {
+    const int hq = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+    const int cap = p.max_blocks * p.block_size;
+    const int n_b = cdiv(min(max(p.seq_lens[b], 0), cap), 16);
+    int n_t = 0;
+    if (t < p.batch) n_t = cdiv(min(max(p.seq_lens[t], 0), cap), 16);
+    const int tot = wave_sum(n_t), pre = wave_sum(t < b ? n_t : 0);
+    __shared__ int red[2][4];
+    if ((t & 63) == 0) {
+        red[0][t >> 6] = tot;
+        red[1][t >> 6] = pre;
+    }
+    __syncthreads();
+    UnitSpace us;
+    us.N = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+    us.NU = min(p.units, us.N);
+    const int P = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    _Float16* out = (_Float16*)p.out + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh;
+    if (n_b == 0) {  // an empty sequence has no partials: a zero row
+        for (int d = t; d < D; d += 256) out[d] = (_Float16)0.f;
+        return;
+    }
+    const int first = unit_of(us, P), last = unit_of(us, (int64_t)P + n_b - 1);
+    merge_rows<D>(p.o_part, p.lse, (int64_t)hq * (p.units + p.batch) + first + b,
+                  last - first + 1, out);
 }
 
 template <int D, int W, bool FINAL, int P>
@@ -389,6 +453,70 @@ static hipError_t launch_f16_d(const DecodeParams& p, bool final_out, int waves,
                                hipStream_t stream) {
     return final_out ? launch_f16_p<D, true>(p, waves, ring, stream)
                      : launch_f16_p<D, false>(p, waves, ring, stream);
+}
+
+template <int D, int W>
+static hipError_t launch_units_w(const DecodeParams& p, int ring, hipStream_t stream) {
+    const dim3 grid((unsigned)(p.kv_heads * p.units));
+    const size_t combine = sizeof(float) * (W * p.group * D + 2 * W * 16);
+    const size_t stage = (size_t)W * 32 * D;
+    const size_t shmem = combine > stage ? combine : stage;
+    switch (ring) {
+        case 1:
+            hipLaunchKernelGGL((decode_f16_units_kernel<D, W, 1>), grid, dim3(W * 64), shmem,
+                               stream, p);
+            break;
+        case 2:
+            hipLaunchKernelGGL((decode_f16_units_kernel<D, W, 2>), grid, dim3(W * 64), shmem,
+                               stream, p);
+            break;
+        case 4:
+            if constexpr (D <= 128) {
+                hipLaunchKernelGGL((decode_f16_units_kernel<D, W, 4>), grid, dim3(W * 64), shmem,
+                                   stream, p);
+                break;
+            }
+            return hipErrorInvalidValue;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_units_d(const DecodeParams& p, int waves, int ring,
+                                 hipStream_t stream) {
+    switch (waves) {
+        case 1: return launch_units_w<D, 1>(p, ring, stream);
+        case 2: return launch_units_w<D, 2>(p, ring, stream);
+        case 4: return launch_units_w<D, 4>(p, ring, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_decode_units(const DecodeParams& p, int kv_format, int head_dim, int waves,
+                               int ring, hipStream_t stream) {
+    if (kv_format != KVQ_KV_F16)
+        return head_dim == 128 ? launch_decode_q_units(p, kv_format, waves, ring, stream)
+                               : hipErrorInvalidValue;
+    switch (head_dim) {
+        case 32: return launch_units_d<32>(p, waves, ring, stream);
+        case 64: return launch_units_d<64>(p, waves, ring, stream);
+        case 128: return launch_units_d<128>(p, waves, ring, stream);
+        case 256: return launch_units_d<256>(p, waves, ring, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_merge_units(const DecodeParams& p, int head_dim, hipStream_t stream) {
+    const dim3 grid(p.q_heads, p.batch);
+    switch (head_dim) {
+        case 32: hipLaunchKernelGGL(merge_units_kernel<32>, grid, dim3(256), 0, stream, p); break;
+        case 64: hipLaunchKernelGGL(merge_units_kernel<64>, grid, dim3(256), 0, stream, p); break;
+        case 128: hipLaunchKernelGGL(merge_units_kernel<128>, grid, dim3(256), 0, stream, p); break;
+        case 256: hipLaunchKernelGGL(merge_units_kernel<256>, grid, dim3(256), 0, stream, p); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_decode(const DecodeParams& p, int kv_format, int head_dim, bool final_out,

@@ -148,12 +148,14 @@ struct SoftmaxState {
 // m and its column sum l. LDS: [W][G][D] accumulators then [W][16] m and l.
 // FINAL writes o / l in fp16 to p.out (single pass); otherwise the normalized partial to
 // o_part and its natural-log LSE to lse (stage 1, reference triton_fp16.py:138-143),
-// with o = 0, lse = -inf for an empty split.
+// with o = 0, lse = -inf for an empty split. The partial of q head h goes to row
+// part_base + h * part_stride of [rows][D] o_part / [rows] lse (split-KV: part_base =
+// b * q_heads * num_splits + split, part_stride = num_splits; units: see UnitSpace).
 template <int D, int W, bool FINAL>
 __device__ __forceinline__ void combine_store(const DecodeParams& p, const f4* acc,
                                               float acc_scale, float corr, float m, float l,
-                                              int wave, int i16, int g, int kvh, int split,
-                                              int b) {
+                                              int wave, int i16, int g, int kvh, int b,
+                                              int64_t part_base, int64_t part_stride) {
     constexpr int DV = D / 16;
     const int G = p.group;
     extern __shared__ float smem[];
@@ -194,10 +196,126 @@ __device__ __forceinline__ void combine_store(const DecodeParams& p, const f4* a
             _Float16* out = (_Float16*)p.out + (int64_t)b * p.o_sb + (int64_t)(hq0 + hh) * p.o_sh;
             out[d] = (_Float16)o;
         } else {
-            const int64_t row = ((int64_t)b * p.q_heads + hq0 + hh) * p.num_splits + split;
+            const int64_t row = part_base + (int64_t)(hq0 + hh) * part_stride;
             p.o_part[row * D + d] = o;
             if (d == 0) p.lse[row] = L > 0.f ? (M + __builtin_amdgcn_logf(L)) * kLn2 : -INFINITY;
         }
+    }
+}
+
+// Partial rows of split `split` of sequence b in the split-KV layout [B][Hq][S][D].
+__device__ __forceinline__ int64_t split_part_base(const DecodeParams& p, int b, int split) {
+    return (int64_t)b * p.q_heads * p.num_splits + split;
+}
+
+// Work units (DecodeParams::units > 0). The 16-token chunks of one kv head, flattened
+// over the batch, are cut into NU equal ranges: sequence b holds chunks [P_b, P_b + n_b)
+// (n_b = cdiv(len_b, 16), P_b = n_0 + ... + n_(b-1), N = P_B) and unit u covers
+// [floor(u N / NU), floor((u + 1) N / NU)), NU = min(units, N), so no unit is empty. A
+// unit's workgroup takes the sequences its range overlaps, one segment each, whatever the
+// lengths are: ragged batches balance as well as uniform ones. The partial of segment
+// (u, b) is row u + b of its q head: a sequence's segments lie in consecutive units, so
+// its rows are consecutive, and rows of different sequences never collide (a later
+// sequence's first unit is at least the earlier one's last). Per q head there are at most
+// NU + B - 1 rows; o_part is [Hq][units + B][D] and lse [Hq][units + B]. B is at most
+// kUnitMaxBatch (checked on the host).
+struct UnitSpace {
+    int N, NU;
+};
+
+// First chunk of unit u, and the unit holding chunk x (the largest u with lo(u) <= x).
+__device__ __forceinline__ int unit_lo(UnitSpace us, int u) {
+    return (int)((int64_t)u * us.N / us.NU);
+}
+__device__ __forceinline__ int unit_of(UnitSpace us, int64_t x) {
+    return (int)(((x + 1) * us.NU + us.N - 1) / us.N - 1);
+}
+
+__device__ __forceinline__ int wave_sum(int x) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+}
+
+// LDS of the work-unit driver: the chunk prefix P_0 .. P_B and the clamped lengths. Its
+// size is a multiple of 16 bytes, so the dynamic LDS after it stays aligned for the
+// 128-bit accesses of the staging tiles.
+struct __attribute__((aligned(16))) UnitLds {
+    int pref[kUnitMaxBatch + 4];
+    int len[kUnitMaxBatch];
+};
+
+// Runs fn(kvh, b, seq_len, w_lo, w_hi, part_base, part_stride) for each segment of this
+// workgroup's unit (workgroup = (kv head, unit), W waves), in batch order, with a
+// barrier between segments (they reuse the LDS of the range functions). [w_lo, w_hi) is
+// the calling wave's contiguous share of the segment's chunks.
+//
+// Workgroup order: plain (kv head fastest), or with xcd_group and units a multiple of
+// kXcds, grouped so that the kv heads of one unit share an XCD (workgroup i runs on XCD
+// i % kXcds) and with it the L2 lines of the V scales, which interleave kv heads.
+template <int W, typename Fn>
+__device__ __forceinline__ void for_unit_segments(const DecodeParams& p, Fn&& fn) {
+    __shared__ UnitLds s;
+    int kvh, u;
+    if (p.xcd_group && p.units % kXcds == 0) {
+        const int q = blockIdx.x / kXcds;
+        kvh = q % p.kv_heads;
+        u = (q / p.kv_heads) * kXcds + blockIdx.x % kXcds;
+    } else {
+        kvh = blockIdx.x % p.kv_heads;
+        u = blockIdx.x / p.kv_heads;
+    }
+    const int t = threadIdx.x, B = p.batch;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    if (t < 64) {  // lane t: sequences 4t .. 4t + 3
+        const int cap = p.max_blocks * p.block_size;
+        int n[4], local = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int b = 4 * t + e;
+            const int len = b < B ? min(max(p.seq_lens[b], 0), cap) : 0;
+            if (b < B) s.len[b] = len;
+            n[e] = cdiv(len, 16);
+            local += n[e];
+        }
+        int incl = local;  // inclusive scan over the wave
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o);
+            if (t >= o) incl += y;
+        }
+        int run = incl - local;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (4 * t + e < B) s.pref[4 * t + e] = run;
+            run += n[e];
+        }
+        if (t == 63) s.pref[B] = incl;
+    }
+    __syncthreads();
+    UnitSpace us;
+    us.N = __builtin_amdgcn_readfirstlane(s.pref[B]);
+    us.NU = min(p.units, us.N);
+    if (u >= us.NU) return;
+    const int lo = unit_lo(us, u), hi = unit_lo(us, u + 1);
+    // the sequence holding chunk lo: the largest b with P_b <= lo (P_B = N > lo)
+    int b = 0, top = B;
+    while (top - b > 1) {
+        const int mid = (b + top) >> 1;
+        if (__builtin_amdgcn_readfirstlane(s.pref[mid]) <= lo) b = mid;
+        else top = mid;
+    }
+    for (; b < B; ++b) {
+        const int p0 = __builtin_amdgcn_readfirstlane(s.pref[b]);
+        if (p0 >= hi) break;
+        const int p1 = __builtin_amdgcn_readfirstlane(s.pref[b + 1]);
+        const int c_lo = max(lo, p0) - p0, c_hi = min(hi, p1) - p0;
+        if (c_lo >= c_hi) continue;  // an empty sequence
+        const int per = cdiv(c_hi - c_lo, W);
+        const int w_lo = min(c_lo + wave * per, c_hi), w_hi = min(w_lo + per, c_hi);
+        fn(kvh, b, __builtin_amdgcn_readfirstlane(s.len[b]), w_lo, w_hi, (int64_t)u + b,
+           (int64_t)p.units + B);
+        __syncthreads();
     }
 }
 

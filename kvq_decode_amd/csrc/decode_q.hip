@@ -641,19 +641,20 @@ __device__ __forceinline__ void stage_q(const DecodeParams& p, int b, int kvh, i
 // P-deep register ring: chunk c + P is loaded while chunk c computes, the block-table
 // entries of chunks c + 2P .. c + 3P - 1 meanwhile. Every chunk carries its own K group's
 // scales, so any group size works with any P. 5 to 16 q heads per kv head.
+//
+// q_range runs one wave's chunk range [w_lo, w_hi) of sequence b (of length seq_len) for
+// kv head kvh and stores the workgroup's result (partial rows part_base + h * part_stride,
+// or the output row for FINAL).
 template <int FMT, int W, bool FINAL, int P, bool SPLIT>
-__global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) {
+__device__ __forceinline__ void q_range(const DecodeParams& p, int kvh, int b, int seq_len,
+                                        int w_lo, int w_hi, int wave, int64_t part_base,
+                                        int64_t part_stride) {
     typedef QFmt<FMT> Q;
     constexpr int D = 128, DV = 8;
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const WgCoord wc = wg_coord(p, FINAL ? 1 : p.num_splits);
-    if (!wc.live) return;
-    const int kvh = wc.kvh, split = wc.split, b = wc.b;
     const int i16 = lane & 15, g = lane >> 4;
     const int G = p.group;
-    const WaveRange wr = wave_range<W>(p, b, split, wave);
-    const int seq_len = wr.seq_len, w_lo = wr.w_lo, w_hi = wr.w_hi;
+    const int c_full = seq_len >> 4;  // chunks below this index are fully valid
     const int kgs = p.k_group_shift;  // log2 of 16-token chunks per K group
     const QBase base = q_base(p, kvh);
 
@@ -698,7 +699,7 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
     // last chunk (at most one per sequence) is handled once after it. Every load in the
     // ring is issued on every path (chunks past r_hi - 1 re-read chunk r_hi - 1 and are
     // never used), so each wait counts exactly the loads still in flight behind it.
-    const int r_hi = min(w_hi, wr.c_full);
+    const int r_hi = min(w_hi, c_full);
     const int gmask = (1 << kgs) - 1;
     if (w_lo < r_hi) {
         const QLaneOff lo = lane_offsets<FMT>(p, i16, g, 15);
@@ -751,7 +752,18 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
     tile_weights<FMT>(st);
     __syncthreads();  // every wave is done with its LDS staging tile
     combine_store<D, W, FINAL>(p, st.acc, Q::F, rows_sum(corr), st.m, rows_sum(st.l), wave, i16,
-                               g, kvh, split, b);
+                               g, kvh, b, part_base, part_stride);
+}
+
+// Split-KV stage 1 / single pass: workgroup = (kv head, split, sequence), W waves.
+template <int FMT, int W, bool FINAL, int P, bool SPLIT>
+__global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const WgCoord wc = wg_coord(p, FINAL ? 1 : p.num_splits);
+    if (!wc.live) return;
+    const WaveRange wr = wave_range<W>(p, wc.b, wc.split, wave);
+    q_range<FMT, W, FINAL, P, SPLIT>(p, wc.kvh, wc.b, wr.seq_len, wr.w_lo, wr.w_hi, wave,
+                                     split_part_base(p, wc.b, wc.split), p.num_splits);
 }
 
 // Chunk pairs, 1 to 4 q heads per kv head, K groups of at least 2 chunks. Pairs are
@@ -760,21 +772,18 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
 // run as single-chunk steps. P-deep ring over the pairs (P = 4 or 8 chunks: while a pair
 // computes, P - 2 chunks are in flight); the ring depth never changes the arithmetic.
 template <int FMT, int W, bool FINAL, int P>
-__global__ __launch_bounds__(W * 64) void decode_q2_kernel(const DecodeParams p) {
+__device__ __forceinline__ void q2_range(const DecodeParams& p, int kvh, int b, int seq_len,
+                                         int w_lo, int w_hi, int wave, int64_t part_base,
+                                         int64_t part_stride) {
     static_assert(P == 4 || P == 8, "a pair computes while P - 2 chunks are in flight");
     typedef QFmt<FMT> Q;
     constexpr int D = 128, DV = 8;
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const WgCoord wc = wg_coord(p, FINAL ? 1 : p.num_splits);
-    if (!wc.live) return;
-    const int kvh = wc.kvh, split = wc.split, b = wc.b;
     const int i16 = lane & 15, g = lane >> 4;
     const int G = p.group;
     const int slot = (i16 >> 2) & 1;   // the column's chunk of the pair
     const bool lo_part = i16 >= 8;     // the column holds the lo parts
-    const WaveRange wr = wave_range<W>(p, b, split, wave);
-    const int seq_len = wr.seq_len, w_lo = wr.w_lo, w_hi = wr.w_hi;
+    const int c_full = seq_len >> 4;
     const int kgs = p.k_group_shift;
     const QBase base = q_base(p, kvh);
 
@@ -813,7 +822,7 @@ __global__ __launch_bounds__(W * 64) void decode_q2_kernel(const DecodeParams p)
         chunk_pair<FMT, true>(ch, ch, qv, csl, sl2f, valid, 0, g, slot, lo_part, kst, st, corr);
     };
 
-    const int r_hi = min(w_hi, wr.c_full);  // fully valid chunks [w_lo, r_hi)
+    const int r_hi = min(w_hi, c_full);  // fully valid chunks [w_lo, r_hi)
     int c_first = w_lo;
     if ((w_lo & 1) && w_lo < r_hi) {
         single(w_lo, 16);
@@ -886,7 +895,33 @@ __global__ __launch_bounds__(W * 64) void decode_q2_kernel(const DecodeParams p)
     tile_weights<FMT>(st);
     __syncthreads();  // every wave is done with its LDS staging tile
     combine_store<D, W, FINAL>(p, st.acc, Q::F, rows_sum(corr), st.m, rows_sum(st.l), wave, i16,
-                               g, kvh, split, b);
+                               g, kvh, b, part_base, part_stride);
+}
+
+template <int FMT, int W, bool FINAL, int P>
+__global__ __launch_bounds__(W * 64) void decode_q2_kernel(const DecodeParams p) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const WgCoord wc = wg_coord(p, FINAL ? 1 : p.num_splits);
+    if (!wc.live) return;
+    const WaveRange wr = wave_range<W>(p, wc.b, wc.split, wave);
+    q2_range<FMT, W, FINAL, P>(p, wc.kvh, wc.b, wr.seq_len, wr.w_lo, wr.w_hi, wave,
+                               split_part_base(p, wc.b, wc.split), p.num_splits);
+}
+
+// Work units (decode_common.h UnitSpace): workgroup = (kv head, unit), W waves running
+// one segment per sequence the unit's chunk range overlaps, each wave a contiguous share
+// of it; PAIRS selects the chunk-pair kernel.
+template <int FMT, int W, int P, bool PAIRS, bool SPLIT>
+__global__ __launch_bounds__(W * 64) void decode_q_units_kernel(const DecodeParams p) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    for_unit_segments<W>(p, [&](int kvh, int b, int seq_len, int w_lo, int w_hi, int64_t base,
+                                int64_t stride) {
+        if constexpr (PAIRS)
+            q2_range<FMT, W, false, P>(p, kvh, b, seq_len, w_lo, w_hi, wave, base, stride);
+        else
+            q_range<FMT, W, false, P, SPLIT>(p, kvh, b, seq_len, w_lo, w_hi, wave, base,
+                                             stride);
+    });
 }
 
 // LDS: region 0 (the cross-wave combine, or the waves' 2 KB staging tiles), one 512-byte K-scale
@@ -939,6 +974,50 @@ static hipError_t launch_q_w(const DecodeParams& p, int waves, int ring, hipStre
         case 2: return launch_q_g<FMT, FINAL, 2>(p, ring, stream);
         case 4: return launch_q_g<FMT, FINAL, 4>(p, ring, stream);
         case 8: return launch_q_g<FMT, FINAL, 8>(p, ring, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// Work units: the kernel variant launch_q_g picks, for W-wave workgroups.
+template <int FMT, int W, int P, bool PAIRS, bool SPLIT>
+static hipError_t launch_qu(const DecodeParams& p, hipStream_t stream) {
+    hipLaunchKernelGGL((decode_q_units_kernel<FMT, W, P, PAIRS, SPLIT>),
+                       dim3((unsigned)(p.kv_heads * p.units)), dim3(W * 64), q_shmem<W>(p, FMT),
+                       stream, p);
+    return hipGetLastError();
+}
+
+template <int FMT, int W>
+static hipError_t launch_q_units_w(const DecodeParams& p, int ring, hipStream_t stream) {
+    if (p.group <= 4 && p.k_group_chunks >= 2)
+        return ring == 4 ? launch_qu<FMT, W, 8, true, false>(p, stream)
+                         : launch_qu<FMT, W, 4, true, false>(p, stream);
+    if (p.group > 8) return launch_qu<FMT, W, 4, false, false>(p, stream);
+    switch (ring) {
+        case 1: return launch_qu<FMT, W, 1, false, true>(p, stream);
+        case 2: return launch_qu<FMT, W, 2, false, true>(p, stream);
+        case 4: return launch_qu<FMT, W, 4, false, true>(p, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <int FMT>
+static hipError_t launch_q_units(const DecodeParams& p, int waves, int ring,
+                                 hipStream_t stream) {
+    switch (waves) {
+        case 1: return launch_q_units_w<FMT, 1>(p, ring, stream);
+        case 2: return launch_q_units_w<FMT, 2>(p, ring, stream);
+        case 4: return launch_q_units_w<FMT, 4>(p, ring, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_decode_q_units(const DecodeParams& p, int kv_format, int waves, int ring,
+                                 hipStream_t stream) {
+    switch (kv_format) {
+        case KVQ_KV_INT8: return launch_q_units<KVQ_KV_INT8>(p, waves, ring, stream);
+        case KVQ_KV_FP8_E4M3: return launch_q_units<KVQ_KV_FP8_E4M3>(p, waves, ring, stream);
+        case KVQ_KV_INT4: return launch_q_units<KVQ_KV_INT4>(p, waves, ring, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -37,6 +37,7 @@ struct DecodeParams {
     int32_t num_splits, pages_per_split;
     float scale_log2;        // softmax scale * log2(e)
     int32_t xcd_group;       // workgroup order (decode_common.h wg_coord): 0 plain, 1 grouped
+    int32_t units;           // work units per kv head (decode_common.h UnitSpace); 0 = splits
 };
 
 // Launches the decode kernel for the format/head_dim in `fmt`/`head_dim`. `final_out`
@@ -55,10 +56,22 @@ __host__ __device__ inline int quant_lds_region0(int waves, int group, int kv_fo
     return combine > tiles ? combine : tiles;
 }
 
+// Stage 1 of the work units for the quantized formats (decode_q.hip); head_dim 128.
+hipError_t launch_decode_q_units(const DecodeParams& p, int kv_format, int waves, int ring,
+                                 hipStream_t stream);
+
 // Quantized formats (decode_q.hip); head_dim 128 only.
 // `ring` = chunks of loads in flight per wave: 1, 2 or 4.
 hipError_t launch_decode_q(const DecodeParams& p, int kv_format, int head_dim, bool final_out,
                            int waves_per_group, int ring, hipStream_t stream);
+
+// Work units (decode_common.h UnitSpace): stage 1 over p.units units per kv head of
+// `waves`-wave workgroups, and the merge of each sequence's partial rows into p.out.
+// Batch at most kUnitMaxBatch; quantized formats head_dim 128.
+constexpr int kUnitMaxBatch = 256;
+hipError_t launch_decode_units(const DecodeParams& p, int kv_format, int head_dim, int waves,
+                               int ring, hipStream_t stream);
+hipError_t launch_merge_units(const DecodeParams& p, int head_dim, hipStream_t stream);
 
 hipError_t launch_merge(const float* o_part, const float* lse, void* out, int64_t o_sb,
                         int64_t o_sh, int batch, int q_heads, int head_dim, int num_splits,

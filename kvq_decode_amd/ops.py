@@ -95,9 +95,31 @@ def normalize_splits(num_splits: int, max_pages: int) -> Tuple[int, int]:
     return s.value, pps.value
 
 
+@functools.lru_cache(maxsize=4096)
+def plan_units(batch: int, kv_heads: int, block_size: int, max_pages: int,
+               cu_count: int, kv_format: str = "fp16") -> Tuple[int, int]:
+    """(units, waves_per_group) of the work-unit partition when the library prefers it
+    for num_splits=None, else (0, 0) (kvq_plan_units): batches of 2 to 256 sequences
+    whose split plan (`plan_decode`) has 2 or more splits get 2 waves per CU in 2-wave
+    unit workgroups (fp16), 4 in 4-wave workgroups (INT8, FP8) or 8 in 2-wave workgroups
+    (INT4), which keeps ragged batches balanced."""
+    _require(kv_format in KV_FORMATS, f"kv_format must be one of {tuple(KV_FORMATS)}")
+    u, w = ctypes.c_int32(), ctypes.c_int32()
+    _lib.check("kvq_plan_units",
+               _lib.lib().kvq_plan_units(batch, kv_heads, block_size, max_pages,
+                                         KV_FORMATS[kv_format], cu_count, ctypes.byref(u),
+                                         ctypes.byref(w)))
+    return u.value, w.value
+
+
 def workspace_shapes(batch: int, q_heads: int, head_dim: int, splits: int):
     """Shapes of the split-KV workspace (o_part, lse) for `splits` splits."""
     return (batch, q_heads, splits, head_dim), (batch, q_heads, splits)
+
+
+def units_workspace_shapes(batch: int, q_heads: int, head_dim: int, units: int):
+    """Shapes of the work-unit workspace (o_part, lse) for `units` units per kv head."""
+    return (q_heads, units + batch, head_dim), (q_heads, units + batch)
 
 
 def check_scale_pairs(scale: torch.Tensor, zero: torch.Tensor, shape, name: str) -> None:
@@ -180,6 +202,7 @@ def paged_decode_attention(
     check_seq_lens: bool = False,
     waves_per_group: int = 0,
     pipeline: int = 0,
+    units: int = 0,
 ) -> torch.Tensor:
     """GQA decode attention over a paged KV cache (reference triton_fp16.py:183-247).
 
@@ -188,9 +211,13 @@ def paged_decode_attention(
     int32 (every entry >= 1). num_splits: None = heuristic, 1 = single pass, n = split
     each sequence n ways. Returns [B, Hq, D] fp16 (written into `out` when given).
     `workspace` = (o_part, lse) float32 buffers of at least the shapes
-    `workspace_shapes(B, Hq, D, S)` for the normalized split count S. With
-    num_splits=None the split count and workgroup size come from `plan_decode`
-    (`choose_num_splits` keeps the reference's formula for callers that want it)."""
+    `workspace_shapes(B, Hq, D, S)` for the normalized split count S (work units:
+    `units_workspace_shapes(B, Hq, D, units)`). With num_splits=None the partition comes
+    from `plan_units` (work units, batches of 2 to 256 that the split plan would split)
+    or else `plan_decode` (`choose_num_splits` keeps the reference's formula for callers
+    that want it). `units` > 0 (B <= 256) asks for the work-unit partition: per kv head,
+    all sequences' 16-token chunks in batch order cut into `units` equal ranges
+    (`kvq_decode_units`)."""
     _require(kv_format in KV_FORMATS, f"unknown kv_format {kv_format!r}")
     B, Hq, D = q.shape
     _, block_size, Hkv, Dc = k_cache.shape
@@ -236,6 +263,29 @@ def paged_decode_attention(
                  "out must be float16 [B, Hq, D] with a contiguous last dim")
 
     max_pages = block_table.shape[1]
+    if num_splits is None and units == 0:
+        units, planned_waves = plan_units(B, Hkv, block_size, max_pages,
+                                          _sm_count(dev.index or 0), kv_format)
+        if units > 0 and waves_per_group == 0:
+            waves_per_group = planned_waves
+    if units > 0:
+        args = build_args(q, k_cache, v_cache, block_table, seq_lens, out, scale, kv_format,
+                          k_scale, k_zero, v_scale, v_zero, k_group, waves_per_group, pipeline)
+        if workspace is None:
+            o_shape, l_shape = units_workspace_shapes(B, Hq, D, units)
+            o_part = torch.empty(o_shape, dtype=torch.float32, device=dev)
+            lse = torch.empty(l_shape, dtype=torch.float32, device=dev)
+        else:
+            o_part, lse = workspace
+            _require(o_part.dtype == lse.dtype == torch.float32 and o_part.is_contiguous()
+                     and lse.is_contiguous() and o_part.device == dev and lse.device == dev,
+                     "workspace must be contiguous float32 on the op's device")
+            _require(o_part.numel() >= Hq * (units + B) * D and lse.numel() >= Hq * (units + B),
+                     f"workspace too small for {units} units")
+        _lib.check("kvq_decode_units",
+                   _lib.lib().kvq_decode_units(ctypes.byref(args), units, o_part.data_ptr(),
+                                               lse.data_ptr(), _stream(dev)))
+        return out
     if num_splits is None:
         splits, planned_waves = plan_decode(B, Hkv, block_size, max_pages,
                                             _sm_count(dev.index or 0), kv_format)

@@ -103,6 +103,35 @@ def test_plan_decode():
         _lib.KVQ_ERR_NULL_POINTER
 
 
+def test_plan_units():
+    """The work-unit plan is chosen for batches of 2 to 256 whose split plan splits:
+    2 waves per CU in 2-wave unit workgroups (fp16), 4 in 4-wave workgroups (INT8, FP8),
+    8 in 2-wave workgroups (INT4); else (0, 0)."""
+    from kvq_decode_amd.ops import plan_units
+    cases = [  # batch, max_pages, format -> (units, waves)
+        (8, 2048, "fp16", (32, 2)),     # C2: 32 units x 8 kv heads x 2 waves = 2 per CU
+        (16, 2048, "fp16", (32, 2)),
+        (64, 2048, "int4", (128, 2)),   # C5: 8 waves per CU
+        (16, 2048, "int8", (32, 4)),    # C4: 4 waves per CU
+        (16, 2048, "fp8_e4m3", (32, 4)),
+        (1, 8192, "fp16", (0, 0)),      # one sequence: the split plan
+        (64, 64, "fp16", (0, 0)),       # the split plan runs a single pass
+        (257, 2048, "fp16", (0, 0)),    # beyond one workgroup's prefix table
+    ]
+    for batch, pages, fmt, want in cases:
+        assert plan_units(batch, 8, 16, pages, 256, fmt) == want, (batch, pages, fmt)
+    assert plan_units(8, 32, 16, 2048, 256, "fp16") == (8, 2)   # MHA: 32 kv heads
+    assert plan_units(8, 1, 16, 2048, 256, "fp16") == (256, 2)  # MQA
+    L = _lib.lib()
+    u, w = ctypes.c_int32(), ctypes.c_int32()
+    assert L.kvq_plan_units(0, 8, 16, 64, 0, 256, ctypes.byref(u), ctypes.byref(w)) == \
+        _lib.KVQ_ERR_SHAPE
+    assert L.kvq_plan_units(2, 8, 16, 64, 7, 256, ctypes.byref(u), ctypes.byref(w)) == \
+        _lib.KVQ_ERR_FORMAT
+    assert L.kvq_plan_units(2, 8, 16, 64, 0, 256, None, ctypes.byref(w)) == \
+        _lib.KVQ_ERR_NULL_POINTER
+
+
 def test_normalize_splits():
     L = _lib.lib()
     s, pps = ctypes.c_int32(), ctypes.c_int32()
@@ -237,6 +266,24 @@ def test_split_rejects_bad_split_geometry():
     assert L.kvq_decode_split(ctypes.byref(a), 4, 8, op, lse, None) == _lib.KVQ_ERR_SPLITS  # 32 < 64 pages
     assert L.kvq_decode_split(ctypes.byref(a), 4, 16, 0, lse, None) == _lib.KVQ_ERR_NULL_POINTER
     assert L.kvq_decode_split(None, 4, 16, op, lse, None) == _lib.KVQ_ERR_NULL_POINTER
+
+
+def test_units_reject():
+    L = _lib.lib()
+    a = good_args()
+    op, lse = 1 << 41, 1 << 42
+    for fn in (L.kvq_decode_units, L.kvq_decode_units_split, L.kvq_decode_units_merge):
+        assert fn(ctypes.byref(a), 0, op, lse, None) == _lib.KVQ_ERR_SPLITS
+        assert fn(ctypes.byref(a), 8, 0, lse, None) == _lib.KVQ_ERR_NULL_POINTER
+        assert fn(None, 8, op, lse, None) == _lib.KVQ_ERR_NULL_POINTER
+    a.batch = 257  # one workgroup reads every seq_len of the batch
+    assert L.kvq_decode_units(ctypes.byref(a), 8, op, lse, None) == _lib.KVQ_ERR_UNSUPPORTED
+    a.batch = 2
+    a.waves_per_group = 8  # unit workgroups: 1, 2 or 4 waves
+    assert L.kvq_decode_units(ctypes.byref(a), 8, op, lse, None) == _lib.KVQ_ERR_UNSUPPORTED
+    a.waves_per_group = 0
+    a.kv_format = 3  # quantized without scale tensors
+    assert L.kvq_decode_units(ctypes.byref(a), 8, op, lse, None) == _lib.KVQ_ERR_FORMAT
 
 
 def test_merge_and_quantize_reject():

@@ -1,0 +1,182 @@
+"""Work-unit decode (kvq_decode_units) vs the numpy oracle. Needs a GPU.
+
+The work-unit path computes the same attention as the split-KV path over a different
+partition (per kv head, the concatenated chunks of the batch cut into equal ranges), so it
+is held to the same bar: |out - ref| <= 2e-3 + 1e-2 * |ref| elementwise and max-abs < 2e-3
+against the oracle's float32 output (reference tests/test_triton_fp16.py:42).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle.attention import paged_decode_attention_ref
+from test_decode_gpu import check_close, make, to_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+# units 1 = one wave per kv head runs the whole batch; 3 and 7 cut sequences at odd
+# chunk boundaries; 1000 exceeds the chunk count (NU = N, one chunk per unit)
+@pytest.mark.parametrize("units", [1, 3, 7, 64, 1000])
+@pytest.mark.parametrize("Hq,Hkv,D", [(32, 8, 128), (4, 4, 64), (8, 1, 64)])
+@pytest.mark.parametrize("block_size", [16, 32])
+@pytest.mark.parametrize("lens", [[1], [37], [100, 33, 1, 64], [4096, 1000, 17, 2049]])
+def test_units_match_reference(Hq, Hkv, D, block_size, lens, units):
+    from kvq_decode_amd import paged_decode_attention
+    q, kc, vc, bt, sl = make(Hq, Hkv, D, block_size, lens)
+    ref = paged_decode_attention_ref(q, kc, vc, bt, sl, out_dtype=np.float32)
+    out = paged_decode_attention(*to_gpu(q, kc, vc, bt, sl), units=units)
+    torch.cuda.synchronize()
+    check_close(out, ref, f"units={units} Hq={Hq} Hkv={Hkv} D={D} bs={block_size} lens={lens}")
+
+
+@pytest.mark.parametrize("D", [32, 256])
+@pytest.mark.parametrize("pipeline", [1, 2, 4])
+def test_units_head_dims_and_ring_depths(D, pipeline):
+    from kvq_decode_amd import paged_decode_attention
+    if D == 256 and pipeline == 4:
+        pytest.skip("ring depth 4 is not built for head_dim 256")
+    q, kc, vc, bt, sl = make(8, 2, D, 16, [700, 3, 129, 2000, 16], seed=3)
+    ref = paged_decode_attention_ref(q, kc, vc, bt, sl, out_dtype=np.float32)
+    out = paged_decode_attention(*to_gpu(q, kc, vc, bt, sl), units=13, pipeline=pipeline)
+    torch.cuda.synchronize()
+    check_close(out, ref, f"units=13 D={D} pipeline={pipeline}")
+
+
+def test_units_full_batch_ragged():
+    """256 sequences (the work-unit limit) of lengths 1 .. 600, fewer units than sequences
+    and more."""
+    from kvq_decode_amd import paged_decode_attention
+    rng = np.random.default_rng(7)
+    lens = [int(x) for x in rng.integers(1, 600, 256)]
+    q, kc, vc, bt, sl = make(8, 2, 64, 16, lens, seed=7)
+    ref = paged_decode_attention_ref(q, kc, vc, bt, sl, out_dtype=np.float32)
+    args = to_gpu(q, kc, vc, bt, sl)
+    for units in (40, 300, 5000):
+        out = paged_decode_attention(*args, units=units)
+        torch.cuda.synchronize()
+        check_close(out, ref, f"B=256 units={units}")
+
+
+def test_units_empty_sequences_give_zero_rows():
+    """seq_lens 0 (which the split path's callers must not pass) yields a zero row here;
+    the other sequences are unaffected."""
+    from kvq_decode_amd import paged_decode_attention
+    q, kc, vc, bt, sl = make(8, 2, 64, 16, [300, 40, 500, 17], seed=5)
+    ref = paged_decode_attention_ref(q, kc, vc, bt, sl, out_dtype=np.float32)
+    sl0 = sl.copy()
+    sl0[1] = 0
+    sl0[3] = 0
+    out = paged_decode_attention(*to_gpu(q, kc, vc, bt, sl0), units=9)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out[1]) == 0 and torch.count_nonzero(out[3]) == 0
+    check_close(out[[0, 2]], ref[[0, 2]], "units with empty sequences")
+
+
+def test_units_deterministic_and_agree_with_splits():
+    from kvq_decode_amd import paged_decode_attention
+    args = to_gpu(*make(32, 8, 128, 16, [4096, 1000, 17, 2049]))
+    a = paged_decode_attention(*args, units=50)
+    b = paged_decode_attention(*args, units=50)
+    assert torch.equal(a, b)
+    s = paged_decode_attention(*args, num_splits=8)
+    assert (a.float() - s.float()).abs().max().item() < 2e-3
+
+
+def test_units_workspace_and_limits():
+    from kvq_decode_amd import paged_decode_attention
+    q, kc, vc, bt, sl = to_gpu(*make(8, 2, 64, 16, [100, 200], seed=1))
+    units = 6
+    ws = (torch.empty((8, units + 2, 64), dtype=torch.float32, device="cuda"),
+          torch.empty((8, units + 2), dtype=torch.float32, device="cuda"))
+    a = paged_decode_attention(q, kc, vc, bt, sl, units=units, workspace=ws)
+    b = paged_decode_attention(q, kc, vc, bt, sl, units=units)
+    assert torch.equal(a, b)
+    from kvq_decode_amd._lib import KvqError
+    from kvq_decode_amd.ops import KvqArgumentError
+    with pytest.raises(KvqArgumentError):
+        paged_decode_attention(q, kc, vc, bt, sl, units=units,
+                               workspace=(ws[0][:, :units].contiguous(), ws[1]))
+    # more sequences than one workgroup's prefix table holds
+    q2, kc2, vc2, bt2, sl2 = to_gpu(*make(2, 1, 32, 16, [5] * 257, seed=2))
+    with pytest.raises(KvqError):
+        paged_decode_attention(q2, kc2, vc2, bt2, sl2, units=8)
+
+
+QFORMATS = ["int8", "fp8_e4m3", "int4"]
+
+
+def _quant_case(fmt, lens, Hq=32, Hkv=8, bs=16, seed=1, k_group=128):
+    """(gpu args, decode kwargs, float32 reference over the dequantized cache)."""
+    from oracle import kivi
+    from kvq_decode_amd.quant import quantize_paged_cache
+    import test_quant_gpu as tq
+    q, kc, vc, bt, sl = tq.make(lens, bs, Hq=Hq, Hkv=Hkv, seed=seed)
+    qc = quantize_paged_cache(tq.gpu(kc), tq.gpu(vc), tq.gpu(bt), tq.gpu(sl), fmt,
+                              k_group=k_group)
+    host = {n: getattr(qc, n).cpu().numpy() for n in
+            ("k_codes", "v_codes", "k_scale", "k_zero", "v_scale", "v_zero")}
+    kd, vd = kivi.dequantize_paged_cache(host, bt, sl, fmt, group=k_group)
+    ref = paged_decode_attention_ref(q.astype(np.float32), kd, vd, bt, sl, out_dtype=np.float32)
+    args = (tq.gpu(q), qc.k_codes, qc.v_codes, tq.gpu(bt), tq.gpu(sl))
+    return args, qc.decode_kwargs(), ref
+
+
+# units 3 and 7 cut sequences at odd chunks (the chunk-pair kernel's single-chunk edges
+# and K groups split between units); 1000 gives one chunk per unit
+@pytest.mark.parametrize("units", [1, 3, 7, 64, 1000])
+@pytest.mark.parametrize("fmt", QFORMATS)
+def test_units_quantized(fmt, units):
+    from kvq_decode_amd import paged_decode_attention
+    args, kw, ref = _quant_case(fmt, [1, 37, 300, 2049, 129])
+    out = paged_decode_attention(*args, units=units, **kw)
+    torch.cuda.synchronize()
+    check_close(out, ref, f"{fmt} units={units}")
+
+
+@pytest.mark.parametrize("fmt", QFORMATS)
+def test_units_quantized_groups_rings_and_k_groups(fmt):
+    """Head groups of every quantized kernel variant (pairs: 1-4 heads; one chain: 5-8;
+    two chains: 9-16), ring depths 1, 2, 4 and K groups of 1 and 16 chunks."""
+    from kvq_decode_amd import paged_decode_attention
+    for Hq, Hkv in ((8, 8), (6, 2), (10, 2), (32, 2)):
+        args, kw, ref = _quant_case(fmt, [700, 3, 129], Hq=Hq, Hkv=Hkv, seed=2)
+        for ring in (1, 2, 4):
+            out = paged_decode_attention(*args, units=11, pipeline=ring, **kw)
+            torch.cuda.synchronize()
+            check_close(out, ref, f"{fmt} Hq={Hq} Hkv={Hkv} ring={ring} units=11")
+    for k_group in (16, 256):
+        args, kw, ref = _quant_case(fmt, [5, 300, 1000], seed=6, k_group=k_group)
+        out = paged_decode_attention(*args, units=9, **kw)
+        torch.cuda.synchronize()
+        check_close(out, ref, f"{fmt} k_group={k_group} units=9")
+
+
+def test_units_c5_shape_int4():
+    """The C5 shape (INT4, 64 sequences of U[1024, 32768] tokens) at a tenth of the
+    lengths, with the unit count the work plan would use, against the oracle on every
+    sequence."""
+    from kvq_decode_amd import paged_decode_attention
+    lens = (np.random.default_rng(0).integers(1024, 32769, 64) // 10).tolist()
+    args, kw, ref = _quant_case("int4", lens, seed=3)
+    out = paged_decode_attention(*args, units=256, **kw)
+    torch.cuda.synchronize()
+    check_close(out, ref, "int4 C5/10 units=256")
+
+
+@pytest.mark.parametrize("waves", [2, 4])
+@pytest.mark.parametrize("fmt", ["fp16"] + QFORMATS)
+def test_units_multi_wave_workgroups(fmt, waves):
+    """W waves per unit share each segment (contiguous shares, combined through LDS)."""
+    from kvq_decode_amd import paged_decode_attention
+    lens = [1, 37, 300, 2049, 129, 5000]
+    if fmt == "fp16":
+        q, kc, vc, bt, sl = make(32, 8, 128, 16, lens, seed=8)
+        ref = paged_decode_attention_ref(q, kc, vc, bt, sl, out_dtype=np.float32)
+        args, kw = to_gpu(q, kc, vc, bt, sl), {}
+    else:
+        args, kw, ref = _quant_case(fmt, lens, seed=8)
+    for units in (1, 5, 40):
+        out = paged_decode_attention(*args, units=units, waves_per_group=waves, **kw)
+        torch.cuda.synchronize()
+        check_close(out, ref, f"{fmt} units={units} W={waves}")
