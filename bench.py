@@ -40,8 +40,10 @@ HQ, HKV, D, BS = 32, 8, 128, 16
 # U[1024, 32768]; pool None = sum of the sequences' pages.
 CONFIGS = {
     "C1": (1, 4096, 256, "fp16", "C1: fp16 KV, batch 1, seq_len 4096, no split"),
-    "C2": (8, 32768, 16384, "fp16", "C2: fp16 KV, batch 8, seq_len 32768, split-KV + merge"),
-    "C3": (1, 131072, 8192, "fp16", "C3: fp16 KV, batch 1, seq_len 131072, split-KV + merge"),
+    "C2": (8, 32768, 16384, "fp16", "C2: fp16 KV, batch 8, seq_len 32768 (reference: split-KV "
+           "+ merge)"),
+    "C3": (1, 131072, 8192, "fp16", "C3: fp16 KV, batch 1, seq_len 131072 (reference: split-KV "
+           "+ merge)"),
     "B1_64K": (1, 65536, 4096, "fp16", "fp16 KV, batch 1, seq_len 65536 (north-star 50% point)"),
     "C4_INT8": (16, 32768, 32768, "int8", "C4: INT8 KIVI KV, batch 16, seq_len 32768"),
     "C4_FP8": (16, 32768, 32768, "fp8_e4m3", "C4: FP8-e4m3 KIVI KV, batch 16, seq_len 32768"),
