@@ -211,8 +211,10 @@ int kvq_decode_units_merge(const kvq_decode_args* args, int32_t units, const flo
  * For each sequence b and kv head, writes codes for the seq_lens[b] valid token slots of
  * both caches, K scales/zeros per channel per k_group tokens (stored in the group's first
  * block) and V scales/zeros per token. Slots past a sequence's length are not written.
- * k_src/v_src: fp16 caches with the strides in args (args->k_cache / v_cache are the
- * destination code caches, args->kv_format the target format). */
+ * k_src/v_src: fp16 caches with the given element strides (args->k_cache / v_cache are
+ * the destination code caches, args->kv_format the target format); 16-byte aligned, with
+ * strides that are multiples of 8 elements (KVQ_ERR_ALIGNMENT otherwise): each lane
+ * reads 8 channels of a row at once. */
 int kvq_quantize_cache(const kvq_decode_args* args, const void* k_src, const void* v_src,
                        int64_t src_stride_blk, int64_t src_stride_tok,
                        int64_t src_stride_head, kvq_stream_t stream);
@@ -223,7 +225,8 @@ int kvq_quantize_cache(const kvq_decode_args* args, const void* k_src, const voi
  * to the fp16 residual k_resid [batch, kv_heads, k_group, head_dim] at row p % k_group,
  * and the group containing p is (re)quantized from the residual rows 0..p%k_group, so
  * the cache always equals kvq_quantize_cache of all tokens so far.
- * args->seq_lens must already count the new token. */
+ * args->seq_lens must already count the new token. k_new, v_new and k_resid are
+ * contiguous and 16-byte aligned (KVQ_ERR_ALIGNMENT otherwise). */
 int kvq_quantize_append(const kvq_decode_args* args, const void* k_new, const void* v_new,
                         void* k_resid, kvq_stream_t stream);
 

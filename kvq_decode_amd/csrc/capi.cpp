@@ -209,6 +209,7 @@ int check_quant_args(const kvq_decode_args* a) {
     if (a->kv_format < KVQ_KV_INT8 || a->kv_format > KVQ_KV_INT4) return KVQ_ERR_FORMAT;
     if (!a->k_scale || !a->k_zero || !a->v_scale || !a->v_zero) return KVQ_ERR_FORMAT;
     if (!scale_pairs(a)) return KVQ_ERR_FORMAT;
+    if (!aligned16(a->k_scale) || !aligned16(a->v_scale)) return KVQ_ERR_ALIGNMENT;
     if (a->batch < 1 || a->kv_heads < 1 || a->max_blocks < 1 || a->num_blocks < 1)
         return KVQ_ERR_SHAPE;
     if (!is_pow2(a->block_size) || a->block_size < 16) return KVQ_ERR_SHAPE;
@@ -248,6 +249,7 @@ kvq::QuantParams make_quant_params(const kvq_decode_args* a) {
     p.max_blocks = a->max_blocks;
     p.num_blocks = a->num_blocks;
     p.k_group = a->k_group;
+    p.bs_shift = ilog2(a->block_size);
     p.max_groups = cdiv(int64_t(a->max_blocks) * a->block_size, a->k_group);
     return p;
 }
@@ -531,6 +533,10 @@ int kvq_quantize_cache(const kvq_decode_args* args, const void* k_src, const voi
     if (st != KVQ_OK) return st;
     if (!k_src || !v_src) return KVQ_ERR_NULL_POINTER;
     if (src_stride_blk < 0 || src_stride_tok < 0 || src_stride_head < 0) return KVQ_ERR_SHAPE;
+    // the quantizers read 8 channels (16 bytes) per lane
+    if (!aligned16(k_src) || !aligned16(v_src) || src_stride_blk % 8 || src_stride_tok % 8 ||
+        src_stride_head % 8)
+        return KVQ_ERR_ALIGNMENT;
     kvq::QuantParams p = make_quant_params(args);
     p.k_src = static_cast<const _Float16*>(k_src);
     p.v_src = static_cast<const _Float16*>(v_src);
@@ -546,6 +552,7 @@ int kvq_quantize_append(const kvq_decode_args* args, const void* k_new, const vo
     int st = check_quant_args(args);
     if (st != KVQ_OK) return st;
     if (!k_new || !v_new || !k_resid) return KVQ_ERR_NULL_POINTER;
+    if (!aligned16(k_new) || !aligned16(v_new) || !aligned16(k_resid)) return KVQ_ERR_ALIGNMENT;
     kvq::QuantParams p = make_quant_params(args);
     p.k_new = static_cast<const _Float16*>(k_new);
     p.v_new = static_cast<const _Float16*>(v_new);

@@ -97,6 +97,7 @@ struct QuantParams {
     const _Float16* v_new;
     _Float16* k_resid;       // append only: [batch, kv_heads, k_group, head_dim]
     int32_t batch, kv_heads, head_dim, block_size, max_blocks, num_blocks, k_group;
+    int32_t bs_shift;        // log2(block_size) (a power of two)
     int32_t max_groups;      // cdiv(max_blocks * block_size, k_group)
 };
 

@@ -81,29 +81,51 @@ __device__ __forceinline__ int seq_len_of(const QuantParams& p, int b) {
     return clampi(p.seq_lens[b], 0, p.max_blocks * p.block_size);
 }
 
-// Codes of two adjacent channels (2j, 2j+1) of one token row.
+typedef _Float16 h8q __attribute__((ext_vector_type(8)));
+typedef _Float16 h4q __attribute__((ext_vector_type(4)));
+typedef _Float16 h2q __attribute__((ext_vector_type(2)));
+
+// A lane's 8 channels of one row, converted to float.
+__device__ __forceinline__ void to_float8(h8q v, float* x) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = (float)v[e];
+}
+
+// Codes of 8 consecutive channels 8c .. 8c + 7 of one token row, in one store: INT4 4
+// bytes (low nibble = even channel), INT8 / FP8 8 bytes. The row's code offset 8c (INT4:
+// 4c) is 4-byte (8-byte) aligned because code rows are 16-byte aligned.
 template <int FMT>
-__device__ __forceinline__ void store_pair(uint8_t* row, int j, uint32_t c0, uint32_t c1) {
+__device__ __forceinline__ void store8(uint8_t* row, int c, const uint32_t* code) {
     if (FMT == KVQ_KV_INT4) {
-        row[j] = (uint8_t)(c0 | (c1 << 4));
+        uint32_t w = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) w |= code[e] << (4 * e);
+        *(uint32_t*)(row + 4 * c) = w;
     } else {
-        *(uint16_t*)(row + 2 * j) = (uint16_t)(c0 | (c1 << 8));
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            lo |= code[e] << (8 * e);
+            hi |= code[4 + e] << (8 * e);
+        }
+        typedef uint32_t u2q __attribute__((ext_vector_type(2)));
+        *(u2q*)(row + 8 * c) = u2q{lo, hi};
     }
 }
 
-// K: per (kv head, group, sequence), 256 threads: thread (j, ts) owns channels 2j, 2j+1
-// (j < D/2) of the group's rows t0 + ts, t0 + ts + TS, ... (TS = 512 / D row slices).
-// Pass 1 reduces min / max over each slice, then across the slices through LDS; pass 2
-// encodes the slice's rows with the group's (scale, zero). Codes go to each token's page
-// slot, the pairs to the group's first block. Append: the group holding the newest token,
-// read from the fp16 residual except the new row itself (from k_new), which also joins
-// the residual for later appends.
-template <int FMT, bool APPEND>
+// K: workgroup = (kv head, group, sequence), 256 threads. Lane (c, slice) owns channels
+// 8c .. 8c + 7 (16-byte loads; D/8 lanes per row) of the group's rows t0 + slice,
+// t0 + slice + RS, ... (RS = 2048 / D row slices). Pass 1 reduces min / max over each
+// slice and then across the slices through LDS, keeping the slice's first 8 rows in
+// registers; pass 2 encodes them (re-reading rows past the 8th) with the group's (scale,
+// zero). Codes go to each token's page slot, the pairs to the group's first block.
+// Append: the group holding the newest token, read from the fp16 residual except the new
+// row itself (from k_new), which also joins the residual for later appends.
+template <int FMT, int D, bool APPEND>
 __global__ __launch_bounds__(256) void quant_k_kernel(const QuantParams p) {
+    constexpr int LPR = D / 8, RS = 256 / LPR, CACHE = 8;
     const int kvh = blockIdx.x, grp = blockIdx.y, b = blockIdx.z;
-    const int D = p.head_dim;
-    const int TS = 512 / D;                // row slices
-    const int j = threadIdx.x % (D / 2), ts = threadIdx.x / (D / 2);
+    const int c = threadIdx.x % LPR, rs = threadIdx.x / LPR;
     const int n = seq_len_of(p, b);
     int t0 = grp * p.k_group, t1 = min(t0 + p.k_group, n);
     if (APPEND) {  // only the group holding the newest token, rows 0..(n-1) % k_group
@@ -112,131 +134,185 @@ __global__ __launch_bounds__(256) void quant_k_kernel(const QuantParams p) {
         t1 = n;
     }
     if (t0 >= t1) return;  // uniform over the workgroup
-    const int64_t resid = ((int64_t)b * p.kv_heads + kvh) * p.k_group * D;
-    const _Float16* kn = p.k_new + ((int64_t)b * p.kv_heads + kvh) * D + 2 * j;
-    if (APPEND && ts == 0) {  // the new token's K joins the fp16 residual of its group
-        _Float16* dst = p.k_resid + resid + (int64_t)(t1 - 1 - t0) * D + 2 * j;
-        dst[0] = kn[0];
-        dst[1] = kn[1];
-    }
-    auto load = [&](int t, float& x0, float& x1) {
+    const int64_t resid = ((int64_t)b * p.kv_heads + kvh) * p.k_group * D + 8 * c;
+    const _Float16* kn = p.k_new + ((int64_t)b * p.kv_heads + kvh) * D + 8 * c;
+    if (APPEND && rs == 0)  // the new token's K joins the fp16 residual of its group
+        *(h8q*)(p.k_resid + resid + (int64_t)(t1 - 1 - t0) * D) = *(const h8q*)kn;
+    auto load = [&](int t) -> h8q {
         const _Float16* src;
         if (APPEND) {
-            src = t == t1 - 1 ? kn : p.k_resid + resid + (int64_t)(t - t0) * D + 2 * j;
+            src = t == t1 - 1 ? kn : p.k_resid + resid + (int64_t)(t - t0) * D;
         } else {
-            const int phys = phys_of(p, b, t / p.block_size);
-            src = p.k_src + (int64_t)phys * p.s_sblk + (int64_t)(t % p.block_size) * p.s_stok +
-                  (int64_t)kvh * p.s_sh + 2 * j;
+            const int phys = phys_of(p, b, t >> p.bs_shift);
+            src = p.k_src + (int64_t)phys * p.s_sblk + (int64_t)(t & (p.block_size - 1)) * p.s_stok +
+                  (int64_t)kvh * p.s_sh + 8 * c;
         }
-        x0 = (float)src[0];
-        x1 = (float)src[1];
+        return *(const h8q*)src;
     };
-    float mn0 = INFINITY, mx0 = -INFINITY, mn1 = INFINITY, mx1 = -INFINITY;
-#pragma unroll 8
-    for (int t = t0 + ts; t < t1; t += TS) {
-        float x0, x1;
-        load(t, x0, x1);
-        mn0 = fminf(mn0, x0);
-        mx0 = fmaxf(mx0, x0);
-        mn1 = fminf(mn1, x1);
-        mx1 = fmaxf(mx1, x1);
+    float mn[8], mx[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        mn[e] = INFINITY;
+        mx[e] = -INFINITY;
     }
-    __shared__ float4 part[256];       // per thread: (mn0, mx0, mn1, mx1)
-    __shared__ float4 params[128];     // per channel pair: (s0, z0, s1, z1)
-    part[threadIdx.x] = make_float4(mn0, mx0, mn1, mx1);
-    __syncthreads();
-    if (ts == 0) {
-        for (int k = 1; k < TS; ++k) {
-            const float4 o = part[k * (D / 2) + j];
-            mn0 = fminf(mn0, o.x);
-            mx0 = fmaxf(mx0, o.y);
-            mn1 = fminf(mn1, o.z);
-            mx1 = fmaxf(mx1, o.w);
+    auto reduce = [&](h8q v) {
+        float x[8];
+        to_float8(v, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            mn[e] = fminf(mn[e], x[e]);
+            mx[e] = fmaxf(mx[e], x[e]);
         }
-        const ScaleZero q0 = make_params<FMT>(mn0, mx0), q1 = make_params<FMT>(mn1, mx1);
-        params[j] = make_float4(q0.s, q0.z, q1.s, q1.z);
-        // (scale, zero) pairs of channels 2j, 2j + 1: one 8-byte store
-        const int lead = phys_of(p, b, t0 / p.block_size);
-        const int64_t sz = ((int64_t)lead * p.kv_heads + kvh) * D + 2 * j;
-        typedef _Float16 h4q __attribute__((ext_vector_type(4)));
-        const h4q pairs = {(_Float16)q0.s, (_Float16)q0.z, (_Float16)q1.s, (_Float16)q1.z};
-        *(h4q*)(p.k_scale + 2 * sz) = pairs;
+    };
+    h8q cache[CACHE];
+#pragma unroll
+    for (int i = 0; i < CACHE; ++i) {
+        const int t = t0 + rs + i * RS;
+        if (t < t1) {
+            cache[i] = load(t);
+            reduce(cache[i]);
+        }
+    }
+    for (int t = t0 + rs + CACHE * RS; t < t1; t += RS) reduce(load(t));
+
+    __shared__ float4 part[256][4];  // per thread: min 0-3, min 4-7, max 0-3, max 4-7
+    __shared__ float2 params[D];     // per channel: (scale, zero)
+    part[threadIdx.x][0] = make_float4(mn[0], mn[1], mn[2], mn[3]);
+    part[threadIdx.x][1] = make_float4(mn[4], mn[5], mn[6], mn[7]);
+    part[threadIdx.x][2] = make_float4(mx[0], mx[1], mx[2], mx[3]);
+    part[threadIdx.x][3] = make_float4(mx[4], mx[5], mx[6], mx[7]);
+    __syncthreads();
+    if (rs == 0) {
+        for (int k = 1; k < RS; ++k) {
+            const float4* o = part[k * LPR + c];
+            const float om[8] = {o[0].x, o[0].y, o[0].z, o[0].w, o[1].x, o[1].y, o[1].z, o[1].w};
+            const float oM[8] = {o[2].x, o[2].y, o[2].z, o[2].w, o[3].x, o[3].y, o[3].z, o[3].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                mn[e] = fminf(mn[e], om[e]);
+                mx[e] = fmaxf(mx[e], oM[e]);
+            }
+        }
+        // (scale, zero) pairs of channels 8c .. 8c + 7: two 16-byte stores
+        const int lead = phys_of(p, b, t0 >> p.bs_shift);
+        const int64_t sz = ((int64_t)lead * p.kv_heads + kvh) * D + 8 * c;
+        h8q pairs[2];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const ScaleZero q = make_params<FMT>(mn[e], mx[e]);
+            params[8 * c + e] = make_float2(q.s, q.z);
+            pairs[e / 4][2 * (e % 4)] = (_Float16)q.s;
+            pairs[e / 4][2 * (e % 4) + 1] = (_Float16)q.z;
+        }
+        *(h8q*)(p.k_scale + 2 * sz) = pairs[0];
+        *(h8q*)(p.k_scale + 2 * sz + 8) = pairs[1];
     }
     __syncthreads();
-    const float4 pr = params[j];
-    const ScaleZero q0 = {pr.x, pr.y}, q1 = {pr.z, pr.w};
-#pragma unroll 8
-    for (int t = t0 + ts; t < t1; t += TS) {
-        float x0, x1;
-        load(t, x0, x1);
-        const int phys = phys_of(p, b, t / p.block_size);
-        uint8_t* row = p.k_codes + (int64_t)phys * p.k_sblk +
-                       (int64_t)(t % p.block_size) * p.k_stok + (int64_t)kvh * p.k_sh;
-        store_pair<FMT>(row, j, encode<FMT>(x0, q0), encode<FMT>(x1, q1));
+    ScaleZero q[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float2 pr = params[8 * c + e];
+        q[e] = ScaleZero{pr.x, pr.y};
+    }
+    auto emit = [&](int t, h8q v) {
+        float x[8];
+        to_float8(v, x);
+        uint32_t code[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) code[e] = encode<FMT>(x[e], q[e]);
+        const int phys = phys_of(p, b, t >> p.bs_shift);
+        store8<FMT>(p.k_codes + (int64_t)phys * p.k_sblk + (int64_t)(t & (p.block_size - 1)) * p.k_stok +
+                        (int64_t)kvh * p.k_sh,
+                    c, code);
+    };
+#pragma unroll
+    for (int i = 0; i < CACHE; ++i) {
+        const int t = t0 + rs + i * RS;
+        if (t < t1) emit(t, cache[i]);
+    }
+    for (int t = t0 + rs + CACHE * RS; t < t1; t += RS) emit(t, load(t));
+}
+
+// V: one token row (D channels of one kv head) per D/8 lanes, each lane 8 channels (one
+// 16-byte load, one 4- or 8-byte code store). Bulk: workgroup = kVRows token rows of one
+// (kv head, sequence), 256 threads; append: the newest token, D/8 threads.
+constexpr int kVRows = 64;
+
+template <int FMT, int D, bool APPEND>
+__global__ __launch_bounds__(256) void quant_v_kernel(const QuantParams p) {
+    constexpr int LPR = D / 8, RPP = 256 / LPR;  // lanes per row, rows per pass
+    constexpr int PASSES = APPEND ? 1 : kVRows / RPP;
+    const int kvh = blockIdx.x, b = blockIdx.z;
+    const int c = threadIdx.x % LPR;
+    const int n = seq_len_of(p, b);
+    // every pass's row is loaded first, so the workgroup waits on memory once
+    int tok[PASSES], phys[PASSES];
+    h8q row[PASSES];
+#pragma unroll
+    for (int i = 0; i < PASSES; ++i) {
+        tok[i] = APPEND ? n - 1 : blockIdx.y * kVRows + i * RPP + threadIdx.x / LPR;
+        if (tok[i] < 0 || tok[i] >= n) continue;  // whole rows (LPR-lane groups) skip together
+        phys[i] = phys_of(p, b, tok[i] >> p.bs_shift);
+        const _Float16* src =
+            APPEND ? p.v_new + ((int64_t)b * p.kv_heads + kvh) * D + 8 * c
+                   : p.v_src + (int64_t)phys[i] * p.s_sblk + (int64_t)(tok[i] & (p.block_size - 1)) * p.s_stok +
+                         (int64_t)kvh * p.s_sh + 8 * c;
+        row[i] = *(const h8q*)src;
+    }
+#pragma unroll
+    for (int i = 0; i < PASSES; ++i) {
+        if (tok[i] < 0 || tok[i] >= n) continue;
+        const int slot = tok[i] & (p.block_size - 1);
+        float x[8];
+        to_float8(row[i], x);
+        float mn = x[0], mx = x[0];
+#pragma unroll
+        for (int e = 1; e < 8; ++e) {
+            mn = fminf(mn, x[e]);
+            mx = fmaxf(mx, x[e]);
+        }
+        // min / max over the row's LPR lanes (aligned lane groups of one wave)
+#pragma unroll
+        for (int o = 1; o < LPR; o <<= 1) {
+            mn = fminf(mn, __shfl_xor(mn, o, LPR));
+            mx = fmaxf(mx, __shfl_xor(mx, o, LPR));
+        }
+        const ScaleZero q = make_params<FMT>(mn, mx);
+        uint32_t code[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) code[e] = encode<FMT>(x[e], q);
+        store8<FMT>(p.v_codes + (int64_t)phys[i] * p.v_sblk + (int64_t)slot * p.v_stok +
+                        (int64_t)kvh * p.v_sh,
+                    c, code);
+        if (c == 0) {
+            const int64_t sz = ((int64_t)phys[i] * p.kv_heads + kvh) * p.block_size + slot;
+            *(h2q*)(p.v_scale + 2 * sz) = h2q{(_Float16)q.s, (_Float16)q.z};
+        }
     }
 }
 
-// V: one token row (D channels of one kv head) per 16 lanes, each lane D/16 channels.
-// Bulk: workgroup = 16 token rows of one (kv head, sequence); append: the newest token.
 template <int FMT, int D, bool APPEND>
-__global__ __launch_bounds__(256) void quant_v_kernel(const QuantParams p) {
-    constexpr int PER = D / 16;
-    const int kvh = blockIdx.x, b = blockIdx.z;
-    const int lane16 = threadIdx.x & 15;
-    const int n = seq_len_of(p, b);
-    int t = blockIdx.y * 16 + (threadIdx.x >> 4);
-    if (APPEND) t = threadIdx.x < 16 ? n - 1 : -1;
-    if (t < 0 || t >= n) return;
-    const int phys = phys_of(p, b, t / p.block_size);
-    const int slot = t % p.block_size;
-    const _Float16* src =
-        APPEND ? p.v_new + ((int64_t)b * p.kv_heads + kvh) * D
-               : p.v_src + (int64_t)phys * p.s_sblk + (int64_t)slot * p.s_stok + (int64_t)kvh * p.s_sh;
-    float x[PER];
-    float mn = INFINITY, mx = -INFINITY;
-#pragma unroll
-    for (int e = 0; e < PER; ++e) {
-        x[e] = (float)src[lane16 * PER + e];
-        mn = fminf(mn, x[e]);
-        mx = fmaxf(mx, x[e]);
-    }
-    // min / max over the row's 16 lanes (lanes of a row are contiguous within the wave)
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-        mn = fminf(mn, __shfl_xor(mn, o, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, o, 16));
-    }
-    const ScaleZero q = make_params<FMT>(mn, mx);
-    uint8_t* row = p.v_codes + (int64_t)phys * p.v_sblk + (int64_t)slot * p.v_stok +
-                   (int64_t)kvh * p.v_sh;
-#pragma unroll
-    for (int e = 0; e < PER; e += 2)
-        store_pair<FMT>(row, (lane16 * PER + e) / 2, encode<FMT>(x[e], q), encode<FMT>(x[e + 1], q));
-    if (lane16 == 0) {
-        const int64_t sz = ((int64_t)phys * p.kv_heads + kvh) * p.block_size + slot;
-        typedef _Float16 h2q __attribute__((ext_vector_type(2)));
-        *(h2q*)(p.v_scale + 2 * sz) = h2q{(_Float16)q.s, (_Float16)q.z};
-    }
+hipError_t launch_fmt_d(const QuantParams& p, hipStream_t stream) {
+    const int groups = APPEND ? 1 : p.max_groups;
+    hipLaunchKernelGGL((quant_k_kernel<FMT, D, APPEND>), dim3(p.kv_heads, groups, p.batch),
+                       dim3(256), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int tiles = APPEND ? 1 : (p.max_blocks * p.block_size + kVRows - 1) / kVRows;
+    hipLaunchKernelGGL((quant_v_kernel<FMT, D, APPEND>), dim3(p.kv_heads, tiles, p.batch),
+                       dim3(APPEND ? D / 8 : 256), 0, stream, p);
+    return hipGetLastError();
 }
 
 template <int FMT, bool APPEND>
 hipError_t launch_fmt(const QuantParams& p, hipStream_t stream) {
-    const int groups = APPEND ? 1 : p.max_groups;
-    hipLaunchKernelGGL((quant_k_kernel<FMT, APPEND>), dim3(p.kv_heads, groups, p.batch),
-                       dim3(256), 0, stream, p);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const int tok_wgs = APPEND ? 1 : (p.max_blocks * p.block_size + 15) / 16;
-    const dim3 vgrid(p.kv_heads, tok_wgs, p.batch);
-    const dim3 vblock(APPEND ? 16 : 256);
     switch (p.head_dim) {
-        case 32: hipLaunchKernelGGL((quant_v_kernel<FMT, 32, APPEND>), vgrid, vblock, 0, stream, p); break;
-        case 64: hipLaunchKernelGGL((quant_v_kernel<FMT, 64, APPEND>), vgrid, vblock, 0, stream, p); break;
-        case 128: hipLaunchKernelGGL((quant_v_kernel<FMT, 128, APPEND>), vgrid, vblock, 0, stream, p); break;
-        case 256: hipLaunchKernelGGL((quant_v_kernel<FMT, 256, APPEND>), vgrid, vblock, 0, stream, p); break;
+        case 32: return launch_fmt_d<FMT, 32, APPEND>(p, stream);
+        case 64: return launch_fmt_d<FMT, 64, APPEND>(p, stream);
+        case 128: return launch_fmt_d<FMT, 128, APPEND>(p, stream);
+        case 256: return launch_fmt_d<FMT, 256, APPEND>(p, stream);
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 template <bool APPEND>

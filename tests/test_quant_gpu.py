@@ -86,6 +86,95 @@ def test_bulk_quantizer_bit_exact(fmt, bs):
         assert np.array_equal(g, w), name
 
 
+@pytest.mark.parametrize("D", [32, 64, 256])
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_bulk_quantizer_other_head_dims(fmt, D):
+    """The quantizers take head_dim 32-256 (lanes of 8 channels: 4 to 32 lanes per row),
+    bit-exact with the spec, including K groups longer than the rows a lane keeps in
+    registers (k_group 256)."""
+    from kvq_decode_amd.quant import quantize_paged_cache
+    q, kc, vc, bt, sl = make([1, 37, 300, 700], 16, Hq=4, Hkv=2, D=D, seed=9)
+    for k_group in (128, 256):
+        want = kivi.quantize_paged_cache(kc, vc, bt, sl, fmt, group=k_group)
+        got = quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt, k_group=k_group)
+        torch.cuda.synchronize()
+        slots = valid_slots(bt, sl, 16)
+        for name in ("k_codes", "v_codes"):
+            g = getattr(got, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
+            w = want[name][slots[:, 0], slots[:, 1]]
+            assert np.array_equal(g, w), f"{name} D={D} k_group={k_group}"
+        lead = lead_blocks(bt, sl, 16, k_group)
+        for name in ("k_scale", "k_zero"):
+            g = getattr(got, name).cpu().numpy()[lead].view(np.uint16)
+            assert np.array_equal(g, want[name][lead].view(np.uint16)), name
+        for name in ("v_scale", "v_zero"):
+            g = getattr(got, name).cpu().numpy()[slots[:, 0], :, slots[:, 1]].view(np.uint16)
+            w = want[name][slots[:, 0], :, slots[:, 1]].view(np.uint16)
+            assert np.array_equal(g, w), name
+
+
+def _tie_rows(rng, n, width, fmt):
+    """n rows of `width` fp16 values whose first two entries are the row's min and max,
+    chosen so that scale and zero come out exact (INT: z = -1.5, s = 2^-6; FP8: z = 0,
+    s = 2^-6), and whose other entries sit on rounding boundaries of the quantized
+    value: half-integer codes (INT) or midpoints between e4m3 values (FP8), half of them
+    moved by one fp16 ulp."""
+    s0 = 2.0 ** -6
+    if fmt == "fp8_e4m3":
+        lo, hi = -448 * s0, 448 * s0
+        e = rng.integers(-6, 8, (n, width))
+        k = rng.integers(0, 8, (n, width))
+        mid = (8 + k + 0.5) * 2.0 ** (e - 3)
+        sub = rng.random((n, width)) < 0.2  # subnormal midpoints (k + 1/2) 2^-9
+        mid = np.where(sub, (k + 0.5) / 512.0, mid)
+        x = np.where(rng.random((n, width)) < 0.5, -mid, mid) * s0
+    else:
+        R = 15 if fmt == "int4" else 255
+        lo, hi = -1.5, -1.5 + R * s0
+        x = lo + (rng.integers(0, R, (n, width)) + 0.5) * s0
+    x = x.astype(np.float16)
+    nudge = rng.integers(-1, 2, (n, width)).astype(np.int16)
+    x = (x.view(np.int16) + np.where(rng.random((n, width)) < 0.5, nudge, 0)).view(np.float16)
+    x[:, 0], x[:, 1] = lo, hi
+    return x
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_quantizer_rounding_ties(fmt):
+    """Values on and one ulp off the codes' rounding boundaries (ties to even), per K
+    channel group and per V row: bit-exact with the spec."""
+    from kvq_decode_amd.quant import quantize_paged_cache
+    rng = np.random.default_rng(12)
+    lens, bs, Hkv, D = [300, 129, 45], 16, 2, 128
+    B, S = len(lens), max(lens)
+    # K: per channel, every 128-token group holds its min and max in its first two tokens
+    k = np.empty((B, S, Hkv, D), np.float16)
+    for b in range(B):
+        for h in range(Hkv):
+            for g0 in range(0, S, 128):
+                n = min(128, S - g0)
+                k[b, g0:g0 + n, h, :] = _tie_rows(rng, D, n, fmt).T
+    v = _tie_rows(rng, B * S * Hkv, D, fmt).reshape(B, S, Hkv, D)
+    sl = np.array(lens, np.int32)
+    kc, vc, bt = build_paged_cache(k, v, sl, bs, rng)
+    want = kivi.quantize_paged_cache(kc, vc, bt, sl, fmt)
+    got = quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt)
+    torch.cuda.synchronize()
+    slots = valid_slots(bt, sl, bs)
+    for name in ("k_codes", "v_codes"):
+        g = getattr(got, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
+        w = want[name][slots[:, 0], slots[:, 1]]
+        assert np.array_equal(g, w), f"{name}: {np.sum(g != w)} of {g.size} bytes differ"
+    lead = lead_blocks(bt, sl, bs)
+    for name in ("k_scale", "k_zero"):
+        g = getattr(got, name).cpu().numpy()[lead].view(np.uint16)
+        assert np.array_equal(g, want[name][lead].view(np.uint16)), name
+    for name in ("v_scale", "v_zero"):
+        g = getattr(got, name).cpu().numpy()[slots[:, 0], :, slots[:, 1]].view(np.uint16)
+        w = want[name][slots[:, 0], :, slots[:, 1]].view(np.uint16)
+        assert np.array_equal(g, w), name
+
+
 @pytest.mark.parametrize("num_splits", [1, 3, None])
 @pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("bs", [16, 32])
