@@ -141,15 +141,16 @@ int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t
                     int32_t* waves_out);
 
 /* Work-unit plan, the library's default for batches of 2 to 256 sequences (no reference
- * counterpart; it takes the place of the split heuristic, triton_fp16.py:175-180, where
- * that would split). When kvq_plan_decode gives splits >= 2 and 2 <= batch <= 256:
+ * counterpart; it takes the place of the split heuristic, triton_fp16.py:175-180). For
+ * 2 <= batch <= 256 when kvq_plan_decode gives splits >= 2 or the longest context
+ * (max_pages * block_size) is at least 4096 tokens:
  *   units = T * cu_count / (waves * kv_heads) (at least 1), with T waves per CU and
  *           `waves` per unit workgroup: fp16 T = 2, waves = 2; INT8 / FP8 T = 4,
  *           waves = 4; INT4 T = 8, waves = 2,
  * for kvq_decode_units; otherwise units = waves = 0 (use kvq_plan_decode's split plan).
  * Units balance ragged batches (a static split count sizes every sequence's splits by
- * the longest one); on uniform batches the two plans run within about 1% of each other
- * on MI355X. Returns KVQ_OK or an error. */
+ * the longest one); on uniform batches the two plans run within a few percent of each
+ * other on MI355X. Returns KVQ_OK or an error. */
 int kvq_plan_units(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t max_pages,
                    int32_t kv_format, int32_t cu_count, int32_t* units_out, int32_t* waves_out);
 

@@ -104,7 +104,8 @@ def test_plan_decode():
 
 
 def test_plan_units():
-    """The work-unit plan is chosen for batches of 2 to 256 whose split plan splits:
+    """The work-unit plan is chosen for batches of 2 to 256 whose split plan splits or
+    whose longest context is at least 4096 tokens:
     2 waves per CU in 2-wave unit workgroups (fp16), 4 in 4-wave workgroups (INT8, FP8),
     8 in 2-wave workgroups (INT4); else (0, 0)."""
     from kvq_decode_amd.ops import plan_units
@@ -115,7 +116,9 @@ def test_plan_units():
         (16, 2048, "int8", (32, 4)),    # C4: 4 waves per CU
         (16, 2048, "fp8_e4m3", (32, 4)),
         (1, 8192, "fp16", (0, 0)),      # one sequence: the split plan
-        (64, 64, "fp16", (0, 0)),       # the split plan runs a single pass
+        (64, 64, "fp16", (0, 0)),       # a single pass over 1024-token contexts
+        (64, 256, "fp16", (32, 2)),     # a single pass in the split plan, 4096 tokens
+        (64, 255, "fp16", (0, 0)),
         (257, 2048, "fp16", (0, 0)),    # beyond one workgroup's prefix table
     ]
     for batch, pages, fmt, want in cases:
