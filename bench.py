@@ -50,6 +50,8 @@ CONFIGS = {
     "B16_FP16": (16, 32768, 32768, "fp16", "fp16 KV, batch 16, seq_len 32768 (INT4 comparison)"),
     "B16_INT4": (16, 32768, 32768, "int4", "INT4 KIVI KV, batch 16, seq_len 32768 (>=3x target)"),
     "C5": (64, None, None, "int4", "C5: INT4 KIVI KV, batch 64, seq_lens U[1024, 32768]"),
+    "R_FP16": (64, None, None, "fp16", "fp16 KV, batch 64, seq_lens U[1024, 32768] (C5's "
+               "lengths; ragged batch)"),
 }
 
 

@@ -180,3 +180,22 @@ def test_units_multi_wave_workgroups(fmt, waves):
         out = paged_decode_attention(*args, units=units, waves_per_group=waves, **kw)
         torch.cuda.synchronize()
         check_close(out, ref, f"{fmt} units={units} W={waves}")
+
+
+@pytest.mark.parametrize("bs", [32, 64])
+@pytest.mark.parametrize("fmt", ["fp16"] + QFORMATS)
+def test_units_larger_pages(fmt, bs):
+    """Pages of 2 and 4 chunks: units that start and end inside a page, K groups of 128
+    tokens spanning 4 and 2 pages."""
+    from kvq_decode_amd import paged_decode_attention
+    lens = [5, 1000, 64, 2500, 129, 33]
+    if fmt == "fp16":
+        q, kc, vc, bt, sl = make(32, 8, 128, bs, lens, seed=13)
+        ref = paged_decode_attention_ref(q, kc, vc, bt, sl, out_dtype=np.float32)
+        args, kw = to_gpu(q, kc, vc, bt, sl), {}
+    else:
+        args, kw, ref = _quant_case(fmt, lens, bs=bs, seed=13)
+    for units in (7, 32, 128):
+        out = paged_decode_attention(*args, units=units, **kw)
+        torch.cuda.synchronize()
+        check_close(out, ref, f"{fmt} bs={bs} units={units}")
