@@ -8,7 +8,8 @@
 //       c = s == 0 ? 0 : clamp(rint((x - z) / s), 0, R)
 //   fp8 e4m3fn, E = 448: z = fp16((max + min) * 0.5), s = fp16((max - min) / (2E)),
 //       c = s == 0 ? 0x00 : e4m3fn_rne(clamp((x - z) / s, -E, E))
-// rint rounds half to even; division is IEEE (correctly rounded); no contraction.
+// rint rounds half to even; division is IEEE (correctly rounded, computed as in
+// quotient()); no contraction.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -47,6 +48,7 @@ __device__ __forceinline__ uint32_t e4m3fn_rne(float t) {
 
 struct ScaleZero {
     float s, z;  // fp16 values held in fp32
+    float r;     // RN(1 / s), 0 when s == 0
 };
 
 template <int FMT>
@@ -61,13 +63,25 @@ __device__ __forceinline__ ScaleZero make_params(float mn, float mx) {
         r.s = (float)(_Float16)__fdiv_rn(mx - mn, R);
         r.z = (float)(_Float16)mn;
     }
+    r.r = r.s == 0.f ? 0.f : __fdiv_rn(1.f, r.s);
     return r;
+}
+
+// RN(d / s) for d = fl(x - z) of fp16 x, z (0 or |d| >= 2^-24) and a positive fp16 s, from
+// the correctly rounded reciprocal r: q = RN(d r), the exact remainder d - s q by fma, and
+// one fma correction (Markstein's theorem; its exceptions need a divisor significand of 24
+// ones, and s has 11 significant bits). Checked bit-identical to IEEE division on every
+// finite fp16 s against random and near-multiple d.
+__device__ __forceinline__ float quotient(float d, ScaleZero p) {
+    const float q = d * p.r;
+    const float rem = __builtin_fmaf(-q, p.s, d);
+    return __builtin_fmaf(rem, p.r, q);
 }
 
 template <int FMT>
 __device__ __forceinline__ uint32_t encode(float x, ScaleZero p) {
     if (p.s == 0.f) return 0u;
-    const float t = __fdiv_rn(x - p.z, p.s);
+    const float t = quotient(x - p.z, p);
     if (FMT == KVQ_KV_FP8_E4M3) return e4m3fn_rne(fminf(fmaxf(t, -kFp8Max), kFp8Max));
     const float R = FMT == KVQ_KV_INT4 ? 15.f : 255.f;
     return (uint32_t)__builtin_rintf(fminf(fmaxf(t, 0.f), R));
@@ -138,12 +152,12 @@ __global__ __launch_bounds__(256) void quant_k_kernel(const QuantParams p) {
     const _Float16* kn = p.k_new + ((int64_t)b * p.kv_heads + kvh) * D + 8 * c;
     if (APPEND && rs == 0)  // the new token's K joins the fp16 residual of its group
         *(h8q*)(p.k_resid + resid + (int64_t)(t1 - 1 - t0) * D) = *(const h8q*)kn;
-    auto load = [&](int t) -> h8q {
+    // row t of the group, from the page `phys` holding it (bulk) or the residual (append)
+    auto load = [&](int t, int phys) -> h8q {
         const _Float16* src;
         if (APPEND) {
             src = t == t1 - 1 ? kn : p.k_resid + resid + (int64_t)(t - t0) * D;
         } else {
-            const int phys = phys_of(p, b, t >> p.bs_shift);
             src = p.k_src + (int64_t)phys * p.s_sblk + (int64_t)(t & (p.block_size - 1)) * p.s_stok +
                   (int64_t)kvh * p.s_sh + 8 * c;
         }
@@ -165,15 +179,19 @@ __global__ __launch_bounds__(256) void quant_k_kernel(const QuantParams p) {
         }
     };
     h8q cache[CACHE];
+    int cphys[CACHE];  // the cached rows' pages, for the code stores of pass 2
 #pragma unroll
     for (int i = 0; i < CACHE; ++i) {
         const int t = t0 + rs + i * RS;
         if (t < t1) {
-            cache[i] = load(t);
+            cphys[i] = phys_of(p, b, t >> p.bs_shift);
+            cache[i] = load(t, cphys[i]);
             reduce(cache[i]);
         }
     }
-    for (int t = t0 + rs + CACHE * RS; t < t1; t += RS) reduce(load(t));
+    for (int t = t0 + rs + CACHE * RS; t < t1; t += RS) {
+        reduce(load(t, phys_of(p, b, t >> p.bs_shift)));
+    }
 
     __shared__ float4 part[256][4];  // per thread: min 0-3, min 4-7, max 0-3, max 4-7
     __shared__ float2 params[D];     // per channel: (scale, zero)
@@ -212,15 +230,14 @@ __global__ __launch_bounds__(256) void quant_k_kernel(const QuantParams p) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const float2 pr = params[8 * c + e];
-        q[e] = ScaleZero{pr.x, pr.y};
+        q[e] = ScaleZero{pr.x, pr.y, pr.x == 0.f ? 0.f : __fdiv_rn(1.f, pr.x)};
     }
-    auto emit = [&](int t, h8q v) {
+    auto emit = [&](int t, int phys, h8q v) {
         float x[8];
         to_float8(v, x);
         uint32_t code[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) code[e] = encode<FMT>(x[e], q[e]);
-        const int phys = phys_of(p, b, t >> p.bs_shift);
         store8<FMT>(p.k_codes + (int64_t)phys * p.k_sblk + (int64_t)(t & (p.block_size - 1)) * p.k_stok +
                         (int64_t)kvh * p.k_sh,
                     c, code);
@@ -228,9 +245,12 @@ __global__ __launch_bounds__(256) void quant_k_kernel(const QuantParams p) {
 #pragma unroll
     for (int i = 0; i < CACHE; ++i) {
         const int t = t0 + rs + i * RS;
-        if (t < t1) emit(t, cache[i]);
+        if (t < t1) emit(t, cphys[i], cache[i]);
     }
-    for (int t = t0 + rs + CACHE * RS; t < t1; t += RS) emit(t, load(t));
+    for (int t = t0 + rs + CACHE * RS; t < t1; t += RS) {
+        const int phys = phys_of(p, b, t >> p.bs_shift);
+        emit(t, phys, load(t, phys));
+    }
 }
 
 // V: one token row (D channels of one kv head) per D/8 lanes, each lane 8 channels (one
