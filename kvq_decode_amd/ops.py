@@ -220,6 +220,8 @@ def paged_decode_attention(
     all sequences' 16-token chunks in batch order cut into `units` equal ranges
     (`kvq_decode_units`)."""
     _require(kv_format in KV_FORMATS, f"unknown kv_format {kv_format!r}")
+    _require(units >= 0, "units must be >= 0")
+    _require(units == 0 or num_splits is None, "give num_splits or units, not both")
     B, Hq, D = q.shape
     _, block_size, Hkv, Dc = k_cache.shape
     quant = kv_format != "fp16"

@@ -324,5 +324,7 @@ def test_python_op_argument_errors_and_no_cpu_fallback():
         paged_decode_attention(q, kc, kc, bt.long(), sl)
     with pytest.raises(KvqArgumentError):
         paged_decode_attention(q[:, :30], kc, kc, bt, sl)
+    with pytest.raises(KvqArgumentError, match="not both"):
+        paged_decode_attention(q, kc, kc, bt, sl, num_splits=2, units=8)
     with pytest.raises(KvqArgumentError, match="GPU only"):
         paged_decode_attention(q, kc, kc, bt, sl)
