@@ -72,6 +72,15 @@ typedef enum kvq_kv_format {
     KVQ_KV_INT4 = 3
 } kvq_kv_format;
 
+/* Version of the on-device quantized cache format above: code layout and nibble order,
+ * the interleaved (scale, zero) pairs, the K group's pairs in the group's first block, the
+ * quantization formulas (kvq_quantize_cache) and their rounding. A cache written under
+ * one version is read correctly only by libraries reporting the same version. */
+#define KVQ_CACHE_FORMAT_VERSION 1
+
+/* KVQ_CACHE_FORMAT_VERSION of the loaded library (no reference counterpart). */
+int kvq_cache_format_version(void);
+
 /* Everything that describes one decode call's inputs and output. Mirrors the arguments of
  * paged_decode_attention_triton (triton_fp16.py:183-191) and the strides its launches pass
  * (triton_fp16.py:221-230, 237-247). */

@@ -26,6 +26,7 @@ KV_FORMATS = {"fp16": 0, "int8": 1, "fp8_e4m3": 2, "int4": 3}
 # Every symbol include/kvq.h declares; tests check the library exports all of them.
 EXPORTED_SYMBOLS = (
     "kvq_version",
+    "kvq_cache_format_version",
     "kvq_status_string",
     "kvq_choose_num_splits",
     "kvq_plan_decode",
@@ -92,6 +93,8 @@ def lib():
         L = ctypes.CDLL(LIB_PATH)
         L.kvq_version.restype = ctypes.c_char_p
         L.kvq_version.argtypes = []
+        L.kvq_cache_format_version.restype = ctypes.c_int
+        L.kvq_cache_format_version.argtypes = []
         L.kvq_status_string.restype = ctypes.c_char_p
         L.kvq_status_string.argtypes = [ctypes.c_int]
         L.kvq_choose_num_splits.restype = ctypes.c_int

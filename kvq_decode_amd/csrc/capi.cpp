@@ -331,6 +331,8 @@ extern "C" {
 
 const char* kvq_version(void) { return "kvq 0.1.0 gfx950"; }
 
+int kvq_cache_format_version(void) { return KVQ_CACHE_FORMAT_VERSION; }
+
 const char* kvq_status_string(int status) {
     switch (status) {
         case KVQ_OK: return "ok";

@@ -28,6 +28,17 @@ from kvq_decode_amd.ops import DEFAULT_K_GROUP, KvqArgumentError, _require, chec
 QUANT_FORMATS = ("int8", "fp8_e4m3", "int4")
 
 
+# The on-device format these caches follow (include/kvq.h KVQ_CACHE_FORMAT_VERSION); a
+# cache kept across processes should be stored with it and read back only by a library
+# reporting the same value (cache_format_version()).
+CACHE_FORMAT_VERSION = 1
+
+
+def cache_format_version() -> int:
+    """The quantized cache format version of the loaded libkvq.so."""
+    return int(_lib.lib().kvq_cache_format_version())
+
+
 class QuantizedKVCache(NamedTuple):
     k_codes: torch.Tensor
     v_codes: torch.Tensor

@@ -57,6 +57,14 @@ def test_version_and_status_strings():
     assert L.kvq_status_string(-3) == b"unsupported configuration"
 
 
+def test_cache_format_version():
+    """The header's format version, the library's and the Python package's agree."""
+    from kvq_decode_amd.quant import CACHE_FORMAT_VERSION, cache_format_version
+    header = open(os.path.join(os.path.dirname(__file__), "..", "include", "kvq.h")).read()
+    m = re.search(r"#define KVQ_CACHE_FORMAT_VERSION (\d+)", header)
+    assert m and int(m.group(1)) == cache_format_version() == CACHE_FORMAT_VERSION
+
+
 def test_choose_num_splits_known_answers():
     """The reference's own recorded auto split counts (results/*.json, A100 108 SMs and
     T4 40 SMs, block_size 32) from its heuristic (triton_fp16.py:175-180)."""
