@@ -113,6 +113,43 @@ def test_bulk_quantizer_other_head_dims(fmt, D):
             assert np.array_equal(g, w), name
 
 
+@pytest.mark.parametrize("D", [32, 64, 256])
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_append_equals_bulk_other_head_dims(fmt, D):
+    """Quantize-on-append at head_dim 32-256 (4 to 32 lanes per row): a few appended
+    tokens, crossing a 128-token K group, leave the bulk quantization of all tokens."""
+    from kvq_decode_amd.quant import init_k_residual, quantize_append, quantize_paged_cache
+    bs, Hkv = 16, 2
+    n0, n1 = [126, 40, 1], [130, 42, 3]
+    q, kc, vc, bt, sl1 = make(n1, bs, Hq=4, Hkv=Hkv, D=D, seed=21)
+    kc_g, vc_g, bt_g = gpu(kc), gpu(vc), gpu(bt)
+    sl0 = torch.tensor(n0, dtype=torch.int32, device="cuda")
+    qc = quantize_paged_cache(kc_g, vc_g, bt_g, sl0, fmt)
+    resid = init_k_residual(kc_g, bt_g, sl0)
+    cur = list(n0)
+    while cur != n1:
+        cur = [min(c + 1, e) for c, e in zip(cur, n1)]
+        k_new = torch.stack([kc_g[bt_g[b, (t - 1) // bs], (t - 1) % bs] for b, t in enumerate(cur)])
+        v_new = torch.stack([vc_g[bt_g[b, (t - 1) // bs], (t - 1) % bs] for b, t in enumerate(cur)])
+        quantize_append(qc, k_new.contiguous(), v_new.contiguous(), bt_g,
+                        torch.tensor(cur, dtype=torch.int32, device="cuda"), resid)
+    want = quantize_paged_cache(kc_g, vc_g, bt_g, gpu(sl1), fmt)
+    torch.cuda.synchronize()
+    slots = valid_slots(bt, sl1, bs)
+    for name in ("k_codes", "v_codes"):
+        g = getattr(qc, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
+        w = getattr(want, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
+        assert np.array_equal(g, w), f"{name} D={D}"
+    lead = lead_blocks(bt, sl1, bs)
+    for name in ("k_scale", "k_zero"):
+        assert np.array_equal(getattr(qc, name).cpu().numpy()[lead],
+                              getattr(want, name).cpu().numpy()[lead]), name
+    for name in ("v_scale", "v_zero"):
+        g = getattr(qc, name).cpu().numpy()[slots[:, 0], :, slots[:, 1]]
+        w = getattr(want, name).cpu().numpy()[slots[:, 0], :, slots[:, 1]]
+        assert np.array_equal(g, w), name
+
+
 def _tie_rows(rng, n, width, fmt):
     """n rows of `width` fp16 values whose first two entries are the row's min and max,
     chosen so that scale and zero come out exact (INT: z = -1.5, s = 2^-6; FP8: z = 0,
