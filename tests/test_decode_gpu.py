@@ -182,3 +182,63 @@ def test_baseline_configs_match_oracle(B, ctx, pool, splits):
     ref = paged_decode_attention_ref(q.cpu().numpy(), kc.cpu().numpy(), vc.cpu().numpy(),
                                      bt.cpu().numpy(), sl.cpu().numpy(), out_dtype=np.float32)
     check_close(out, ref, f"B={B} ctx={ctx} splits={splits}")
+
+
+def _torch_ref(q, k_pool, v_pool, bt, lens, scale):
+    """float32 attention over each sequence's gathered pages, on the GPU, one kv head at a
+    time (the reference for contexts too long for the numpy oracle)."""
+    B, Hq, D = q.shape
+    Hkv = k_pool.shape[2]
+    G = Hq // Hkv
+    out = torch.empty(B, Hq, D, dtype=torch.float32, device=q.device)
+    for b in range(B):
+        L = int(lens[b])
+        pages = bt[b, :-(-L // k_pool.shape[1])].long()
+        for h in range(Hkv):
+            kh = k_pool[pages, :, h].reshape(-1, D)[:L].float()
+            s = (q[b, h * G:(h + 1) * G].float() @ kh.T) * scale
+            del kh
+            p = torch.softmax(s, dim=1)
+            vh = v_pool[pages, :, h].reshape(-1, D)[:L].float()
+            out[b, h * G:(h + 1) * G] = p @ vh
+            del vh
+    return out
+
+
+def test_maximum_context():
+    """Two sequences of 65536 pages (1,048,576 and 1,048,571 tokens) over a 2 GiB-per-cache
+    pool, with needle keys at each sequence's last token and in its middle: the split plan,
+    the single pass, work units and the default plan all match a float32 reference, and the
+    needle heads return the needle values."""
+    from kvq_decode_amd import paged_decode_attention
+    g = torch.Generator(device="cuda").manual_seed(5)
+    Hq, Hkv, D, bs, pages = 32, 8, 128, 16, 65536
+    lens = [pages * bs, pages * bs - 5]
+    print(f"\n[max context] lens={lens}", flush=True)
+    k = torch.randn(pages, bs, Hkv, D, generator=g, device="cuda").half()
+    v = torch.randn(pages, bs, Hkv, D, generator=g, device="cuda").half()
+    q = torch.randn(2, Hq, D, generator=g, device="cuda").half()
+    bt = torch.stack([torch.randperm(pages, generator=g, device="cuda"),
+                      torch.randperm(pages, generator=g, device="cuda")]).int()
+    scale = 1.0 / math.sqrt(D)
+    # needles: q head 4h of each sequence sees one key of score ~30 (in natural-log units)
+    for b, L in enumerate(lens):
+        for h in range(Hkv):
+            t = L - 1 if h % 2 == 0 else L // 2 + 7 * h
+            qv = q[b, 4 * h].float()
+            k[bt[b, t // bs].long(), t % bs, h] = (qv * (30.0 / scale / float(qv @ qv))).half()
+    sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    ref = _torch_ref(q, k, v, bt, lens, scale)
+    for kw in ({"num_splits": 64}, {"num_splits": 1}, {"units": 64}, {}):
+        out = paged_decode_attention(q, k, v, bt, sl, **kw).float()
+        torch.cuda.synchronize()
+        diff = (out - ref).abs()
+        print(f"[max context {kw}] max_abs={diff.max().item():.3e}", flush=True)
+        assert torch.isfinite(out).all()
+        assert diff.max().item() < ATOL
+        assert bool((diff <= ATOL + RTOL * ref.abs()).all())
+        for b, L in enumerate(lens):
+            for h in range(Hkv):
+                t = L - 1 if h % 2 == 0 else L // 2 + 7 * h
+                needle = v[bt[b, t // bs].long(), t % bs, h].float()
+                assert (out[b, 4 * h] - needle).abs().max().item() < 1e-2, (kw, b, h)
