@@ -437,3 +437,69 @@ def _full_size_case(fmt, lens, check_seqs):
         ref = paged_decode_attention_ref(q[b:b + 1].cpu().numpy().astype(np.float32), kd, vd,
                                          sub_bt, sub_sl, out_dtype=np.float32)
         check_close(out[b:b + 1], ref, f"{fmt} full-size seq {b} len {n}")
+
+
+def _dequant_int4_torch(qc, bt, b, L, h, bs, group=128):
+    """float32 K, V [L, D] of kv head h of sequence b from an INT4 cache (x = c s + z;
+    low nibble = even channel; K pairs in the group's first block, V pairs per token)."""
+    pages = bt[b, :-(-L // bs)].long()
+
+    def codes(c):
+        c = c[pages, :, h].reshape(-1, c.shape[-1])[:L]
+        return torch.stack([c & 15, c >> 4], dim=-1).reshape(L, -1).float()
+    t = torch.arange(L, device=bt.device)
+    lead = bt[b, (t // group) * group // bs].long()
+    ksz = qc.k_sz[lead, h].float()                       # [L, D, 2]
+    k = codes(qc.k_codes) * ksz[..., 0] + ksz[..., 1]
+    vsz = qc.v_sz[pages, h].reshape(-1, 2)[:L].float()   # [L, 2]
+    v = codes(qc.v_codes) * vsz[:, :1] + vsz[:, 1:]
+    return k, v
+
+
+def test_int4_maximum_context():
+    """INT4 at the quantizers' limit: two sequences of 65535 pages (1,048,560 tokens and 37
+    fewer) over a 65536-block pool, needle keys at the last token and mid-sequence: the
+    default plan (work units), 64 splits and the single pass against float32 attention over
+    the dequantized cache."""
+    from kvq_decode_amd import paged_decode_attention
+    from kvq_decode_amd.quant import quantize_paged_cache
+    g = torch.Generator(device="cuda").manual_seed(6)
+    Hq, Hkv, D, bs, pool, pages = 32, 8, 128, 16, 65536, 65535
+    lens = [pages * bs, pages * bs - 37]
+    print(f"\n[int4 max context] lens={lens}", flush=True)
+    k = torch.randn(pool, bs, Hkv, D, generator=g, device="cuda").half()
+    v = torch.randn(pool, bs, Hkv, D, generator=g, device="cuda").half()
+    q = torch.randn(2, Hq, D, generator=g, device="cuda").half()
+    bt = torch.stack([torch.randperm(pool, generator=g, device="cuda")[:pages]
+                      for _ in range(2)]).int()
+    scale = 1.0 / np.sqrt(D)
+    needles = {}
+    for b, L in enumerate(lens):
+        for h in range(Hkv):
+            t = L - 1 if h % 2 == 0 else L // 2 + 11 * h
+            qv = q[b, 4 * h].float()
+            k[bt[b, t // bs].long(), t % bs, h] = (qv * (30.0 / scale / float(qv @ qv))).half()
+            needles[(b, h)] = t
+    sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    qc = quantize_paged_cache(k, v, bt, sl, "int4")
+    del k, v
+    ref = torch.empty(2, Hq, D, dtype=torch.float32, device="cuda")
+    vneedle = {}
+    for b, L in enumerate(lens):
+        for h in range(Hkv):
+            kd, vd = _dequant_int4_torch(qc, bt, b, L, h, bs)
+            p = torch.softmax((q[b, 4 * h:4 * h + 4].float() @ kd.T) * scale, dim=1)
+            ref[b, 4 * h:4 * h + 4] = p @ vd
+            vneedle[(b, h)] = vd[needles[(b, h)]].clone()
+            del kd, vd, p
+    for kw in ({}, {"num_splits": 64}, {"num_splits": 1}):
+        out = paged_decode_attention(q, qc.k_codes, qc.v_codes, bt, sl, **kw,
+                                     **qc.decode_kwargs()).float()
+        torch.cuda.synchronize()
+        diff = (out - ref).abs()
+        print(f"[int4 max context {kw}] max_abs={diff.max().item():.3e}", flush=True)
+        assert torch.isfinite(out).all()
+        assert diff.max().item() < ATOL
+        assert bool((diff <= ATOL + RTOL * ref.abs()).all())
+        for (b, h), want in vneedle.items():
+            assert (out[b, 4 * h] - want).abs().max().item() < 2e-2, (kw, b, h)
