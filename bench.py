@@ -16,8 +16,9 @@ B * ctx * Hkv * 2 * D * 2 bytes for fp16.
 --layers N times a whole-model decode step instead: N layers, each with its own cache of
 the --config shape, decoded back to back - eagerly, and replayed from one captured HIP
 graph - and prints one JSON line with µs per step (one token per sequence) and the
-aggregate KV-read TB/s (reference src/bpt/roofline.py:42-63 models the same 32-layer
-step for Llama-3-8B).
+aggregate KV-read TB/s (reference src/bpt/roofline.py:42-63 models the same step).
+--model picks the head shape and layer count from the reference's model table
+(llama3-8b, llama3-70b, llama2-7b, qwen2.5-7b).
 
 Prints progress on stderr and ONE JSON line on stdout.
 """
@@ -35,6 +36,15 @@ if REPO not in sys.path:
 METRIC = ("achieved KV-read TB/s & % of 8 TB/s HBM peak; µs per decode step (1 layer)")
 PEAK_GBPS = 8000.0
 HQ, HKV, D, BS = 32, 8, 128, 16
+
+# Whole-model shapes (layers, q heads, kv heads, head_dim) of the reference's model table
+# (src/bpt/roofline.py:42-48), for --layers / --model.
+MODELS = {
+    "llama3-8b": (32, 32, 8, 128),
+    "llama3-70b": (80, 64, 8, 128),
+    "llama2-7b": (32, 32, 32, 128),
+    "qwen2.5-7b": (28, 28, 4, 128),
+}
 
 # name -> (batch, ctx, pool blocks, kv_format, description). ctx None = ragged lengths
 # U[1024, 32768]; pool None = sum of the sequences' pages.
@@ -66,23 +76,25 @@ def seq_lengths(B, ctx, seed=0):
     return np.random.default_rng(seed).integers(1024, 32769, B).tolist()
 
 
-def make_inputs(B, ctx, pool, seed=0, kv_format="fp16"):
+def make_inputs(B, ctx, pool, seed=0, kv_format="fp16", shape=(HQ, HKV, D)):
     """q, K, V ~ N(0,1) fp16 (K with 4 random outlier channels per kv head scaled x10 for
     the quantized configs, BASELINE.json configs[3-4]), a block table that is a random
     permutation of the pool, and the sequence lengths. Quantized caches are built with
-    the library's own bulk quantizer. Returns (q, k, v, bt, sl, fmt_kwargs)."""
+    the library's own bulk quantizer. `shape` = (q heads, kv heads, head_dim). Returns
+    (q, k, v, bt, sl, fmt_kwargs)."""
     import torch
+    hq, hkv, d = shape
     g = torch.Generator(device="cuda").manual_seed(seed)
     lens = seq_lengths(B, ctx, seed)
     pages = [-(-n // BS) for n in lens]
     pool = pool if pool is not None else sum(pages)
-    q = torch.randn(B, HQ, D, generator=g, device="cuda").half()
-    k = torch.randn(pool, BS, HKV, D, generator=g, device="cuda")
+    q = torch.randn(B, hq, d, generator=g, device="cuda").half()
+    k = torch.randn(pool, BS, hkv, d, generator=g, device="cuda")
     if kv_format != "fp16":
-        for h in range(HKV):
-            k[:, :, h, torch.randperm(D, generator=g, device="cuda")[:4]] *= 10
+        for h in range(hkv):
+            k[:, :, h, torch.randperm(d, generator=g, device="cuda")[:4]] *= 10
     k = k.half()
-    v = torch.randn(pool, BS, HKV, D, generator=g, device="cuda").half()
+    v = torch.randn(pool, BS, hkv, d, generator=g, device="cuda").half()
     perm = torch.randperm(pool, generator=g, device="cuda").int()
     bt = torch.zeros(B, max(pages), dtype=torch.int32, device="cuda")
     o = 0
@@ -101,10 +113,10 @@ def make_inputs(B, ctx, pool, seed=0, kv_format="fp16"):
     return q, k, v, bt, sl, fmt
 
 
-def kv_bytes(lens, kv_format):
+def kv_bytes(lens, kv_format, hkv=HKV, d=D):
     """Algorithmic KV bytes of one step (reference roofline.py:50-63 per token-head)."""
     from kvq_decode_amd.roofline import bytes_per_token_head
-    return int(round(sum(lens) * HKV * bytes_per_token_head(D, kv_format)))
+    return int(round(sum(lens) * hkv * bytes_per_token_head(d, kv_format)))
 
 
 class Step:
@@ -121,16 +133,16 @@ class Step:
         self.ctypes = ctypes
         self.L = _lib.lib()
         self.check = _lib.check
-        B = q.shape[0]
+        B, hq, d = q.shape
         self.out = torch.empty_like(q)
         self.units = units
         self.splits, self.pps = (0, 0) if units else ops.normalize_splits(splits, bt.shape[1])
-        self.args = ops.build_args(q, k, v, bt, sl, self.out, 1.0 / math.sqrt(D),
+        self.args = ops.build_args(q, k, v, bt, sl, self.out, 1.0 / math.sqrt(d),
                                    waves_per_group=waves, pipeline=pipeline, **(fmt or {}))
         if units:
-            o_shape, l_shape = ops.units_workspace_shapes(B, HQ, D, units)
+            o_shape, l_shape = ops.units_workspace_shapes(B, hq, d, units)
         else:
-            o_shape, l_shape = ops.workspace_shapes(B, HQ, D, self.splits)
+            o_shape, l_shape = ops.workspace_shapes(B, hq, d, self.splits)
         self.o_part = torch.empty(o_shape, dtype=torch.float32, device="cuda")
         self.lse = torch.empty(l_shape, dtype=torch.float32, device="cuda")
         self.stream = torch.cuda.current_stream().cuda_stream
@@ -168,7 +180,8 @@ class Step:
             self.check("kvq_decode_merge",
                        self.L.kvq_decode_merge(self.o_part.data_ptr(), self.lse.data_ptr(),
                                                self.out.data_ptr(), self.out.stride(0),
-                                               self.out.stride(1), self.B, HQ, D, self.splits,
+                                               self.out.stride(1), self.B, self.out.shape[1],
+                                               self.out.shape[2], self.splits,
                                                self.stream))
 
     def __call__(self):
@@ -387,7 +400,7 @@ def traffic_summary(config, pmc_dir):
     log(f"wrote {path}")
 
 
-def default_plan(config, B, max_pages, cu_count=None):
+def default_plan(config, B, max_pages, cu_count=None, hkv=HKV):
     """(splits, waves, units) the op would use with num_splits=None: the work-unit plan
     (units > 0) where the library prefers it, else the split plan (C1: no split,
     configs[0])."""
@@ -397,10 +410,10 @@ def default_plan(config, B, max_pages, cu_count=None):
         return 1, 0, 0
     cus = cu_count or _sm_count(0)
     fmt_name = CONFIGS[config][3]
-    units, waves = plan_units(B, HKV, BS, max_pages, cus, fmt_name)
+    units, waves = plan_units(B, hkv, BS, max_pages, cus, fmt_name)
     if units:
         return 0, waves, units
-    return (*plan_decode(B, HKV, BS, max_pages, cus, fmt_name), 0)
+    return (*plan_decode(B, hkv, BS, max_pages, cus, fmt_name), 0)
 
 
 def run_config(config, steps, warmup, splits=None, waves=0, pipeline=0, flushed=True,
@@ -444,22 +457,27 @@ def run_config(config, steps, warmup, splits=None, waves=0, pipeline=0, flushed=
     return res, (q, k, v, bt, sl)
 
 
-def run_layers(config, layers, steps, warmup):
-    """Whole-model decode step: `layers` independent caches of the config's shape, one
-    decode each, back to back; timed eagerly and as replays of one captured HIP graph."""
+def run_layers(config, layers, steps, warmup, model="llama3-8b"):
+    """Whole-model decode step: `layers` (0 = the model's count) independent caches of the
+    config's batch and lengths in the model's head shape, one decode each, back to back;
+    timed eagerly and as replays of one captured HIP graph."""
     import torch
     B, ctx, pool, fmt_name, desc = CONFIGS[config]
+    model_layers, hq, hkv, d = MODELS[model]
+    layers = layers or model_layers
     step_list, lens = [], None
     for layer in range(layers):
-        q, k, v, bt, sl, fmt = make_inputs(B, ctx, pool, seed=layer, kv_format=fmt_name)
+        q, k, v, bt, sl, fmt = make_inputs(B, ctx, pool, seed=layer, kv_format=fmt_name,
+                                           shape=(hq, hkv, d))
         lens = lens or [int(x) for x in sl.tolist()]
-        splits, waves, units = default_plan(config, B, bt.shape[1])
+        splits, waves, units = default_plan(config, B, bt.shape[1], hkv=hkv)
         step_list.append(Step(q, k, v, bt, sl, splits, waves, 0, fmt, units))
+        del q, k, v, bt, sl, fmt
         if layer == 0:
-            log(f"{config} x {layers} layers: {desc}; {plan_text(step_list[0])} "
-                f"waves={waves}")
+            log(f"{config} x {layers} layers, {model} ({hq}q/{hkv}kv, D={d}): {desc}; "
+                f"{plan_text(step_list[0])} waves={waves}")
     torch.cuda.synchronize()
-    nbytes = kv_bytes(lens, fmt_name) * layers
+    nbytes = kv_bytes(lens, fmt_name, hkv, d) * layers
 
     def model_step():
         for st in step_list:
@@ -492,7 +510,8 @@ def run_layers(config, layers, steps, warmup):
         "roofline_min_us": round(nbytes / (PEAK_GBPS * 1e9) * 1e6, 2),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": fmt_name,
         "data": "synthetic: per-layer q, K, V ~ N(0,1) fp16 (seed = layer index)",
-        "config": {"workload": f"{desc}, {layers} layers", "layers": layers, "batch": B,
+        "config": {"workload": f"{desc}, {layers} layers of {model} ({hq} q / {hkv} kv heads, "
+                               f"head_dim {d})", "layers": layers, "batch": B,
                    "sum_seq_lens": sum(lens), "kv_bytes_per_step": nbytes,
                    "partition": plan_text(step_list[0]), "graph": True,
                    "kv_format": fmt_name},
@@ -552,6 +571,9 @@ def main():
                     help="only STEPS untimed steps of --config (run under rocprofv3 --pmc)")
     ap.add_argument("--layers", type=int, default=0,
                     help="time a whole-model step of N layers of --config (HIP graph)")
+    ap.add_argument("--model", default=None, choices=sorted(MODELS),
+                    help="head shape (and, without --layers, layer count) of the whole-model "
+                         "step; default llama3-8b")
     ap.add_argument("--traffic-summary", metavar="PMC_DIR",
                     help="write profiles/decode_<config>_traffic.txt from PMC_DIR/"
                          "{copy_fetch,copy_write,fetch,write}")
@@ -573,9 +595,9 @@ def main():
     if args.sweep:
         sweep(args)
         return
-    if args.layers:
-        print(json.dumps(run_layers(args.config, args.layers, args.steps, args.warmup)),
-              flush=True)
+    if args.layers or args.model:
+        print(json.dumps(run_layers(args.config, args.layers, args.steps, args.warmup,
+                                    args.model or "llama3-8b")), flush=True)
         return
     import torch
     names = list(CONFIGS) if args.suite else [args.config]
