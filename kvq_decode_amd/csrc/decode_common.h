@@ -323,7 +323,7 @@ __device__ __forceinline__ void for_unit_segments(const DecodeParams& p, Fn&& fn
 // [split * pps, min((split + 1) * pps, cdiv(seq_len, block_size))) (reference
 // triton_fp16.py:114-116), cut into 16-token chunks, cut into W contiguous runs.
 struct WaveRange {
-    int seq_len, n_pages, w_lo, w_hi, c_full;
+    int seq_len, w_lo, w_hi;
 };
 
 template <int W>
@@ -333,16 +333,15 @@ __device__ __forceinline__ WaveRange wave_range(const DecodeParams& p, int b, in
     int seq_len = p.seq_lens[b];
     seq_len = min(max(seq_len, 0), p.max_blocks * p.block_size);
     r.seq_len = seq_len;
-    r.n_pages = cdiv(seq_len, p.block_size);
+    const int n_pages = cdiv(seq_len, p.block_size);
     const int pg_lo = split * p.pages_per_split;
-    const int pg_hi = min(pg_lo + p.pages_per_split, r.n_pages);
+    const int pg_hi = min(pg_lo + p.pages_per_split, n_pages);
     const int c_lo = pg_lo << p.cpp_shift;
     const int c_hi = min(pg_hi << p.cpp_shift, cdiv(seq_len, 16));
     const int nch = max(c_hi - c_lo, 0);
     const int per = cdiv(nch, W);
     r.w_lo = c_lo + wave * per;
     r.w_hi = min(r.w_lo + per, c_hi);
-    r.c_full = seq_len >> 4;  // chunks below this index are fully valid
     return r;
 }
 
