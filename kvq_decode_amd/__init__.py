@@ -14,6 +14,7 @@ from kvq_decode_amd.ops import (  # noqa: F401
     paged_decode_attention,
     plan_decode,
     plan_units,
+    plan_workspace_shapes,
     units_workspace_shapes,
     workspace_shapes,
 )
@@ -26,6 +27,7 @@ __all__ = [
     "normalize_splits",
     "workspace_shapes",
     "units_workspace_shapes",
+    "plan_workspace_shapes",
     "plan_decode",
     "plan_units",
     "TARGET_PROGRAMS_PER_SM",

@@ -123,6 +123,21 @@ def units_workspace_shapes(batch: int, q_heads: int, head_dim: int, units: int):
     return (q_heads, units + batch, head_dim), (q_heads, units + batch)
 
 
+def plan_workspace_shapes(batch: int, q_heads: int, kv_heads: int, head_dim: int,
+                          block_size: int, max_pages: int, cu_count: int,
+                          kv_format: str = "fp16"):
+    """Shapes of the workspace (o_part, lse) the op needs with num_splits=None for these
+    sizes (work units or splits, as `plan_units` / `plan_decode` choose), or None when
+    the plan runs a single pass and needs none. For callers that preallocate, e.g. before
+    a graph capture."""
+    units, _ = plan_units(batch, kv_heads, block_size, max_pages, cu_count, kv_format)
+    if units:
+        return units_workspace_shapes(batch, q_heads, head_dim, units)
+    splits, _ = plan_decode(batch, kv_heads, block_size, max_pages, cu_count, kv_format)
+    splits = normalize_splits(splits, max_pages)[0]
+    return None if splits == 1 else workspace_shapes(batch, q_heads, head_dim, splits)
+
+
 def check_scale_pairs(scale: torch.Tensor, zero: torch.Tensor, shape, name: str) -> None:
     """The scale / zero tensors of a quantized cache are views of one interleaved fp16
     [..., 2] tensor of (scale, zero) pairs (include/kvq.h): element strides
@@ -213,7 +228,8 @@ def paged_decode_attention(
     each sequence n ways. Returns [B, Hq, D] fp16 (written into `out` when given).
     `workspace` = (o_part, lse) float32 buffers of at least the shapes
     `workspace_shapes(B, Hq, D, S)` for the normalized split count S (work units:
-    `units_workspace_shapes(B, Hq, D, units)`). With num_splits=None the partition comes
+    `units_workspace_shapes(B, Hq, D, units)`; with num_splits=None,
+    `plan_workspace_shapes` gives whichever the plan needs). With num_splits=None the partition comes
     from `plan_units` (work units: batches of 2 to 256 with 4096-token contexts or that the
     split plan would split) or else `plan_decode` (`choose_num_splits` keeps the reference's formula for callers
     that want it). `units` > 0 (B <= 256) asks for the work-unit partition: per kv head,

@@ -143,6 +143,17 @@ def test_plan_units():
         _lib.KVQ_ERR_NULL_POINTER
 
 
+def test_plan_workspace_shapes():
+    """The workspace shapes the default plan needs: work units, splits, or none."""
+    from kvq_decode_amd.ops import plan_workspace_shapes
+    # C2: 32 units per kv head -> [Hq, units + B, D]
+    assert plan_workspace_shapes(8, 32, 8, 128, 16, 2048, 256) == ((32, 40, 128), (32, 40))
+    # one sequence: the split plan, 32 splits of 64k tokens
+    assert plan_workspace_shapes(1, 32, 8, 128, 16, 4096, 256) == ((1, 32, 32, 128), (1, 32, 32))
+    # a single pass over short contexts needs none
+    assert plan_workspace_shapes(64, 32, 8, 128, 16, 64, 256) is None
+
+
 def test_normalize_splits():
     L = _lib.lib()
     s, pps = ctypes.c_int32(), ctypes.c_int32()

@@ -199,3 +199,19 @@ def test_units_larger_pages(fmt, bs):
         out = paged_decode_attention(*args, units=units, **kw)
         torch.cuda.synchronize()
         check_close(out, ref, f"{fmt} bs={bs} units={units}")
+
+
+@pytest.mark.parametrize("lens", [[3000, 17, 900, 64], [5000], [300] * 64])
+def test_plan_workspace_shapes_fit_the_default_plan(lens):
+    """A workspace preallocated from plan_workspace_shapes serves the default plan (work
+    units, splits or a single pass) and gives the same output as the op's own."""
+    from kvq_decode_amd import _sm_count, paged_decode_attention, plan_workspace_shapes
+    q, kc, vc, bt, sl = make(32, 8, 128, 16, lens, seed=17)
+    args = to_gpu(q, kc, vc, bt, sl)
+    shapes = plan_workspace_shapes(len(lens), 32, 8, 128, 16, bt.shape[1], _sm_count(0))
+    ws = None if shapes is None else tuple(
+        torch.empty(s, dtype=torch.float32, device="cuda") for s in shapes)
+    a = paged_decode_attention(*args, workspace=ws)
+    b = paged_decode_attention(*args)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
