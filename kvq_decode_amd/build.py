@@ -58,7 +58,30 @@ def build(verbose=False):
         for m in msgs:
             print(m)
         print(f"built {LIB_PATH} in {time.time() - t0:.1f}s")
+    build_checks(verbose)
     return LIB_PATH
+
+
+# GPU check programs of the test suite (tests/gpu_checks/*.hip -> executables beside them)
+CHECKS_DIR = os.path.join(REPO_DIR, "tests", "gpu_checks")
+
+
+def build_checks(verbose=False):
+    if not os.path.isdir(CHECKS_DIR):
+        return
+    for name in sorted(os.listdir(CHECKS_DIR)):
+        if not name.endswith(".hip"):
+            continue
+        src = os.path.join(CHECKS_DIR, name)
+        out = src[:-len(".hip")]
+        cmd = [hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17",
+               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", src, "-o", out]
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        if proc.returncode != 0:
+            raise RuntimeError("hipcc failed (%d) on %s:\n%s"
+                               % (proc.returncode, src, proc.stderr[-3000:]))
+        if verbose:
+            print(f"built {out}")
 
 
 if __name__ == "__main__":
