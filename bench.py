@@ -579,8 +579,9 @@ def main():
                          "{copy_fetch,copy_write,fetch,write}")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); the "
-              "multi-GPU sharding of the path is described in DESIGN.md", file=sys.stderr)
+        print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); the path "
+              "would shard by kv heads or by sequence ranges, which is not built here",
+              file=sys.stderr)
         sys.exit(2)
 
     if args.traffic_summary:
