@@ -215,3 +215,22 @@ def test_plan_workspace_shapes_fit_the_default_plan(lens):
     b = paged_decode_attention(*args)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("fmt", ["fp16"] + QFORMATS)
+@pytest.mark.parametrize("Hq,Hkv", [(16, 2), (32, 2), (8, 1), (4, 2)])
+def test_units_head_groups(fmt, Hq, Hkv):
+    """Work units for every q-head group the kernels specialise: 2 (chunk pairs), 8 (one
+    MFMA chain with hi / lo columns, MQA here too) and 16 (two chains), ragged lengths."""
+    from kvq_decode_amd import paged_decode_attention
+    lens = [900, 5, 2100, 300]
+    if fmt == "fp16":
+        q, kc, vc, bt, sl = make(Hq, Hkv, 128, 16, lens, seed=19)
+        ref = paged_decode_attention_ref(q, kc, vc, bt, sl, out_dtype=np.float32)
+        args, kw = to_gpu(q, kc, vc, bt, sl), {}
+    else:
+        args, kw, ref = _quant_case(fmt, lens, Hq=Hq, Hkv=Hkv, seed=19)
+    for units in (9, 64):
+        out = paged_decode_attention(*args, units=units, **kw)
+        torch.cuda.synchronize()
+        check_close(out, ref, f"{fmt} Hq={Hq} Hkv={Hkv} units={units}")
