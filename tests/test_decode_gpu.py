@@ -101,10 +101,11 @@ def test_stage1_partials_match_oracle(num_splits):
     assert np.all(o[np.isneginf(l_ref)] == 0)
 
 
-@pytest.mark.parametrize("num_splits", [1, 4])
+@pytest.mark.parametrize("num_splits", [1, 4, "units5", "units64"])
 def test_nan_garbage_in_unused_slots(num_splits):
     """Unused slots of each sequence's last page hold NaN/inf: the kernel never reads them
-    (rows past seq_len are redirected to the last valid token and masked)."""
+    (rows past seq_len are redirected to the last valid token and masked). Split, single
+    pass and work-unit ("unitsN") paths."""
     from kvq_decode_amd import paged_decode_attention
     lens = [37, 1, 250]
     q, kc, vc, bt, sl = make(32, 8, 128, 16, lens)
@@ -115,8 +116,10 @@ def test_nan_garbage_in_unused_slots(num_splits):
             vc[blk, n % 16:] = np.inf
     ref = paged_decode_attention_ref(q, np.nan_to_num(kc), np.nan_to_num(vc), bt, sl,
                                      out_dtype=np.float32)
-    out = paged_decode_attention(*to_gpu(q, kc, vc, bt, sl), num_splits=num_splits)
-    check_close(out, ref, f"nan-garbage splits={num_splits}")
+    kw = ({"units": int(num_splits[5:])} if isinstance(num_splits, str)
+          else {"num_splits": num_splits})
+    out = paged_decode_attention(*to_gpu(q, kc, vc, bt, sl), **kw)
+    check_close(out, ref, f"nan-garbage {kw}")
 
 
 @pytest.mark.parametrize("waves,pipeline", [(1, 1), (2, 2), (4, 1), (8, 2), (16, 1), (16, 2),
