@@ -503,3 +503,31 @@ def test_int4_maximum_context():
         assert bool((diff <= ATOL + RTOL * ref.abs()).all())
         for (b, h), want in vneedle.items():
             assert (out[b, 4 * h] - want).abs().max().item() < 2e-2, (kw, b, h)
+
+
+@pytest.mark.parametrize("kw", [{"num_splits": 3}, {"units": 7}, {}],
+                         ids=["splits3", "units7", "default"])
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_nan_garbage_in_unused_quantized_slots(fmt, kw):
+    """Slots past each sequence's end in its last page hold 0xFF codes and NaN (scale,
+    zero) pairs: the decode never lets them into the result (masked scores, zero weights)."""
+    from kvq_decode_amd import paged_decode_attention
+    from kvq_decode_amd.quant import quantize_paged_cache
+    lens = [37, 1, 250, 129]
+    q, kc, vc, bt, sl = make(lens, 16, seed=23)
+    qc = quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt)
+    host = {n: getattr(qc, n).cpu().numpy() for n in
+            ("k_codes", "v_codes", "k_scale", "k_zero", "v_scale", "v_zero")}
+    kd, vd = kivi.dequantize_paged_cache(host, bt, sl, fmt)
+    ref = paged_decode_attention_ref(q.astype(np.float32), kd, vd, bt, sl, out_dtype=np.float32)
+    nan16 = torch.tensor(float("nan"), dtype=torch.float16)
+    for b, n in enumerate(lens):
+        if n % 16:
+            blk = int(bt[b, (n - 1) // 16])
+            qc.k_codes[blk, n % 16:] = 0xFF
+            qc.v_codes[blk, n % 16:] = 0xFF
+            qc.v_sz[blk, :, n % 16:] = nan16
+    out = paged_decode_attention(gpu(q), qc.k_codes, qc.v_codes, gpu(bt), gpu(sl), **kw,
+                                 **qc.decode_kwargs())
+    torch.cuda.synchronize()
+    check_close(out, ref, f"{fmt} nan-garbage {kw}")
