@@ -20,6 +20,9 @@ aggregate KV-read TB/s (reference src/bpt/roofline.py:42-63 models the same step
 --model picks the head shape and layer count from the reference's model table
 (llama3-8b, llama3-70b, llama2-7b, qwen2.5-7b).
 
+--write-path times the KV write path of --config instead: the bulk quantizer and the
+one-token append for a quantized format, the fp16 append otherwise.
+
 Prints progress on stderr and ONE JSON line on stdout.
 """
 import argparse
@@ -518,6 +521,79 @@ def run_layers(config, layers, steps, warmup, model="llama3-8b"):
     }
 
 
+def write_path_bytes(lens, kv_format, k_group, hkv=HKV, d=D):
+    """Algorithmic bytes of writing a batch's cache. fp16: every token-head's K and V rows
+    read and written. Quantized: the fp16 rows read, and their codes plus the (scale, zero)
+    fp16 pairs written (V: one pair per token-head; K: one pair per channel per group of
+    k_group tokens)."""
+    th = sum(lens) * hkv
+    if kv_format == "fp16":
+        return 2 * th * d * 2 * 2
+    code = d // 2 if kv_format == "int4" else d
+    k_groups = sum(-(-n // k_group) for n in lens) * hkv
+    return 2 * th * d * 2 + 2 * th * code + th * 4 + k_groups * d * 4
+
+
+def run_write_path(config, steps, warmup):
+    """The KV write path for the --config batch, one JSON line.
+
+    Quantized formats: the bulk quantizer (kvq_quantize_cache of every token into a
+    preallocated cache; events around `steps` calls) and the decode-time append
+    (kvq_quantize_append of one token per sequence at position seq_len - 1, which also
+    re-quantizes that sequence's open K group from its fp16 residual). fp16: the append
+    (kvq_append_kv). Each append is timed eagerly (µs per call, host overhead included)
+    and from a captured HIP graph of `steps` appends (µs per append, GPU only)."""
+    import torch
+
+    from kvq_decode_amd.cache import append_kv
+    from kvq_decode_amd.quant import (DEFAULT_K_GROUP, allocate_quantized_cache,
+                                      init_k_residual, quantize_append, quantize_paged_cache)
+    B, ctx, pool, fmt, desc = CONFIGS[config]
+    q, k, v, bt, sl, _ = make_inputs(B, ctx, pool, kv_format="fp16")
+    lens = sl.tolist()
+    hkv, d = k.shape[2], k.shape[3]
+    g = torch.Generator(device="cuda").manual_seed(1)
+    k_new = torch.randn(B, hkv, d, generator=g, device="cuda").half()
+    v_new = torch.randn(B, hkv, d, generator=g, device="cuda").half()
+    res = {"metric": "KV write path: µs per bulk quantization and per one-token append",
+           "config": {"workload": desc, "batch": B, "kv_format": fmt,
+                      "sum_seq_lens": int(sum(lens)), "kv_heads": hkv, "head_dim": d,
+                      "block_size": BS}, "steps": steps, "warmup": warmup,
+           "data": "synthetic: K, V ~ N(0,1) fp16, new tokens ~ N(0,1), seed 0/1"}
+    if fmt == "fp16":
+        def append():
+            append_kv(k, v, k_new, v_new, bt, sl)
+    else:
+        qc = allocate_quantized_cache(k.shape[0], BS, hkv, d, fmt, k.device)
+        nbytes = write_path_bytes(lens, fmt, DEFAULT_K_GROUP, hkv, d)
+        wall_ms, ev_ms = time_steps(lambda: quantize_paged_cache(k, v, bt, sl, fmt, out=qc),
+                                    steps, warmup)
+        res["bulk_us"] = round(ev_ms * 1e3, 1)
+        res["bulk_bytes"] = nbytes
+        res["bulk_tb_s"] = round(nbytes / (ev_ms * 1e-3) / 1e12, 3)
+        resid = init_k_residual(k, bt, sl)
+
+        def append():
+            quantize_append(qc, k_new, v_new, bt, sl, resid)
+    wall_ms, _ = time_steps(append, steps, warmup)
+    res["append_us_eager"] = round(wall_ms * 1e3, 2)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(steps):
+            append()
+    graph.replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(3):
+        graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    res["append_us_graph"] = round(ev0.elapsed_time(ev1) * 1e3 / (3 * steps), 2)
+    log(f"write path {config}: {res}")
+    return res
+
+
 def sweep(args):
     import torch
     B, ctx, pool, fmt_name, _ = CONFIGS[args.config]
@@ -574,6 +650,9 @@ def main():
     ap.add_argument("--model", default=None, choices=sorted(MODELS),
                     help="head shape (and, without --layers, layer count) of the whole-model "
                          "step; default llama3-8b")
+    ap.add_argument("--write-path", action="store_true",
+                    help="time the KV write path of --config instead (bulk quantizer and "
+                         "one-token append; fp16: append only)")
     ap.add_argument("--traffic-summary", metavar="PMC_DIR",
                     help="write profiles/decode_<config>_traffic.txt from PMC_DIR/"
                          "{copy_fetch,copy_write,fetch,write}")
@@ -595,6 +674,9 @@ def main():
         return
     if args.sweep:
         sweep(args)
+        return
+    if args.write_path:
+        print(json.dumps(run_write_path(args.config, args.steps, args.warmup)), flush=True)
         return
     if args.layers or args.model:
         print(json.dumps(run_layers(args.config, args.layers, args.steps, args.warmup,

@@ -127,9 +127,8 @@ __device__ __forceinline__ void store8(uint8_t* row, int c, const uint32_t* code
 // Append: the group holding the newest token, read from the fp16 residual except the new
 // row itself (from k_new), which also joins the residual for later appends.
 template <int FMT, int D, bool APPEND>
-__global__ __launch_bounds__(256) void quant_k_kernel(const QuantParams p) {
+__device__ __forceinline__ void quant_k_group(const QuantParams& p, int kvh, int grp, int b) {
     constexpr int LPR = D / 8, RS = 256 / LPR, CACHE = 8;
-    const int kvh = blockIdx.x, grp = blockIdx.y, b = blockIdx.z;
     const int c = threadIdx.x % LPR, rs = threadIdx.x / LPR;
     const int n = seq_len_of(p, b);
     int t0 = grp * p.k_group, t1 = min(t0 + p.k_group, n);
@@ -246,14 +245,14 @@ __global__ __launch_bounds__(256) void quant_k_kernel(const QuantParams p) {
 
 // V: one token row (D channels of one kv head) per D/8 lanes, each lane 8 channels (one
 // 16-byte load, one 4- or 8-byte code store). Bulk: workgroup = kVRows token rows of one
-// (kv head, sequence), 256 threads; append: the newest token, D/8 threads.
+// (kv head, sequence), 256 threads; append: the newest token, on the first D/8 lanes of
+// the append kernel's V workgroup.
 constexpr int kVRows = 64;
 
 template <int FMT, int D, bool APPEND>
-__global__ __launch_bounds__(256) void quant_v_kernel(const QuantParams p) {
+__device__ __forceinline__ void quant_v_rows(const QuantParams& p, int kvh, int tile, int b) {
     constexpr int LPR = D / 8, RPP = 256 / LPR;  // lanes per row, rows per pass
     constexpr int PASSES = APPEND ? 1 : kVRows / RPP;
-    const int kvh = blockIdx.x, b = blockIdx.z;
     const int c = threadIdx.x % LPR;
     const int n = seq_len_of(p, b);
     // every pass's row is loaded first, so the workgroup waits on memory once
@@ -261,7 +260,7 @@ __global__ __launch_bounds__(256) void quant_v_kernel(const QuantParams p) {
     h8q row[PASSES];
 #pragma unroll
     for (int i = 0; i < PASSES; ++i) {
-        tok[i] = APPEND ? n - 1 : blockIdx.y * kVRows + i * RPP + threadIdx.x / LPR;
+        tok[i] = APPEND ? n - 1 : tile * kVRows + i * RPP + threadIdx.x / LPR;
         if (tok[i] < 0 || tok[i] >= n) continue;  // whole rows (LPR-lane groups) skip together
         phys[i] = phys_of(p, b, tok[i] >> p.bs_shift);
         const _Float16* src =
@@ -302,16 +301,42 @@ __global__ __launch_bounds__(256) void quant_v_kernel(const QuantParams p) {
     }
 }
 
+template <int FMT, int D>
+__global__ __launch_bounds__(256) void quant_k_kernel(const QuantParams p) {
+    quant_k_group<FMT, D, false>(p, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+template <int FMT, int D>
+__global__ __launch_bounds__(256) void quant_v_kernel(const QuantParams p) {
+    quant_v_rows<FMT, D, false>(p, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+// Append in one launch: workgroup (kv head, role, sequence), role 0 re-quantizes the K
+// group holding the newest token, role 1 (its first D/8 lanes) quantizes the newest V row.
+// The two roles write disjoint memory (K codes, pairs and residual; V codes and pairs).
+template <int FMT, int D>
+__global__ __launch_bounds__(256) void quant_append_kernel(const QuantParams p) {
+    if (blockIdx.y == 0) {
+        quant_k_group<FMT, D, true>(p, blockIdx.x, 0, blockIdx.z);
+    } else if (threadIdx.x < D / 8) {
+        quant_v_rows<FMT, D, true>(p, blockIdx.x, 0, blockIdx.z);
+    }
+}
+
 template <int FMT, int D, bool APPEND>
 hipError_t launch_fmt_d(const QuantParams& p, hipStream_t stream) {
-    const int groups = APPEND ? 1 : p.max_groups;
-    hipLaunchKernelGGL((quant_k_kernel<FMT, D, APPEND>), dim3(p.kv_heads, groups, p.batch),
+    if (APPEND) {
+        hipLaunchKernelGGL((quant_append_kernel<FMT, D>), dim3(p.kv_heads, 2, p.batch),
+                           dim3(256), 0, stream, p);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL((quant_k_kernel<FMT, D>), dim3(p.kv_heads, p.max_groups, p.batch),
                        dim3(256), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int tiles = APPEND ? 1 : (p.max_blocks * p.block_size + kVRows - 1) / kVRows;
-    hipLaunchKernelGGL((quant_v_kernel<FMT, D, APPEND>), dim3(p.kv_heads, tiles, p.batch),
-                       dim3(APPEND ? D / 8 : 256), 0, stream, p);
+    const int tiles = (p.max_blocks * p.block_size + kVRows - 1) / kVRows;
+    hipLaunchKernelGGL((quant_v_kernel<FMT, D>), dim3(p.kv_heads, tiles, p.batch), dim3(256),
+                       0, stream, p);
     return hipGetLastError();
 }
 
