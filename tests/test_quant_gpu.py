@@ -531,3 +531,45 @@ def test_nan_garbage_in_unused_quantized_slots(fmt, kw):
                                  **qc.decode_kwargs())
     torch.cuda.synchronize()
     check_close(out, ref, f"{fmt} nan-garbage {kw}")
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_append_skips_empty_sequences(fmt):
+    """One append launch over a batch holding an empty sequence (seq_len 0): the other
+    sequences' new tokens land bit-exact with the bulk quantization, and no byte of the
+    cache outside their new slots and K groups changes."""
+    from kvq_decode_amd.quant import init_k_residual, quantize_append, quantize_paged_cache
+    bs, n0, n1 = 16, [20, 0, 127], [21, 0, 128]
+    q, kc, vc, bt, sl1 = make(n1, bs, Hkv=2, seed=29)
+    kc_g, vc_g, bt_g = gpu(kc), gpu(vc), gpu(bt)
+    sl0 = torch.tensor(n0, dtype=torch.int32, device="cuda")
+    qc = quantize_paged_cache(kc_g, vc_g, bt_g, sl0, fmt)
+    resid = init_k_residual(kc_g, bt_g, sl0)
+    names = ("k_codes", "v_codes", "k_scale", "k_zero", "v_scale", "v_zero")
+    before = {n: getattr(qc, n).clone() for n in names}
+    k_new = torch.zeros((3, kc.shape[2], kc.shape[3]), dtype=torch.float16, device="cuda")
+    v_new = torch.zeros_like(k_new)
+    for b in (0, 2):
+        t = n1[b] - 1
+        k_new[b] = kc_g[bt_g[b, t // bs], t % bs]
+        v_new[b] = vc_g[bt_g[b, t // bs], t % bs]
+    quantize_append(qc, k_new, v_new, bt_g, gpu(sl1), resid)
+    want = quantize_paged_cache(kc_g, vc_g, bt_g, gpu(sl1), fmt)
+    torch.cuda.synchronize()
+    slots = valid_slots(bt, sl1, bs)
+    for name in ("k_codes", "v_codes"):
+        g = getattr(qc, name).cpu().numpy()
+        assert np.array_equal(g[slots[:, 0], slots[:, 1]],
+                              getattr(want, name).cpu().numpy()[slots[:, 0], slots[:, 1]]), name
+        # everything except the valid slots is as before the append
+        mask = np.ones(g.shape[:2], bool)
+        mask[slots[:, 0], slots[:, 1]] = False
+        assert np.array_equal(g[mask], before[name].cpu().numpy()[mask]), name
+    lead = lead_blocks(bt, sl1, bs)
+    bits = lambda t: t.view(torch.int16).cpu().numpy()  # unwritten memory may hold NaNs
+    for name in ("k_scale", "k_zero"):
+        g = bits(getattr(qc, name))
+        assert np.array_equal(g[lead], bits(getattr(want, name))[lead]), name
+        mask = np.ones(g.shape[0], bool)
+        mask[lead] = False
+        assert np.array_equal(g[mask], bits(before[name])[mask]), name
