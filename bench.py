@@ -13,6 +13,11 @@ decode of the whole batch (stage 1 + stage 2), inputs resident in HBM. Algorithm
 bytes = KV reads only (reference src/bpt/roofline.py:1-4, bench/bench_triton_fp16.py:58):
 B * ctx * Hkv * 2 * D * 2 bytes for fp16.
 
+The default C2 line also carries the north star's other targets, timed the same way:
+fp16 batch 1 at 64k tokens (b1_64k_*: >= 50% of the peak) and INT4 against fp16 at batch
+16 / 32k tokens (b16_*, int4_speedup: >= 3x fewer µs per step); --no-targets skips them.
+roofline.kernel_us is stage 1 timed over back-to-back stage-1 launches.
+
 --layers N times a whole-model decode step instead: N layers, each with its own cache of
 the --config shape, decoded back to back - eagerly, and replayed from one captured HIP
 graph - and prints one JSON line with µs per step (one token per sequence) and the
@@ -32,6 +37,8 @@ import os
 import sys
 import time
 
+import numpy as np
+
 REPO = os.path.dirname(os.path.abspath(__file__))
 if REPO not in sys.path:
     sys.path.insert(0, REPO)
@@ -39,15 +46,6 @@ if REPO not in sys.path:
 METRIC = ("achieved KV-read TB/s & % of 8 TB/s HBM peak; µs per decode step (1 layer)")
 PEAK_GBPS = 8000.0
 HQ, HKV, D, BS = 32, 8, 128, 16
-
-# Whole-model shapes (layers, q heads, kv heads, head_dim) of the reference's model table
-# (src/bpt/roofline.py:42-48), for --layers / --model.
-MODELS = {
-    "llama3-8b": (32, 32, 8, 128),
-    "llama3-70b": (80, 64, 8, 128),
-    "llama2-7b": (32, 32, 32, 128),
-    "qwen2.5-7b": (28, 28, 4, 128),
-}
 
 # name -> (batch, ctx, pool blocks, kv_format, description). ctx None = ragged lengths
 # U[1024, 32768]; pool None = sum of the sequences' pages.
@@ -117,9 +115,10 @@ def make_inputs(B, ctx, pool, seed=0, kv_format="fp16", shape=(HQ, HKV, D)):
 
 
 def kv_bytes(lens, kv_format, hkv=HKV, d=D):
-    """Algorithmic KV bytes of one step (reference roofline.py:50-63 per token-head)."""
-    from kvq_decode_amd.roofline import bytes_per_token_head
-    return int(round(sum(lens) * hkv * bytes_per_token_head(d, kv_format)))
+    """Algorithmic KV bytes of one step (kvq_decode_amd/roofline.py; the reference's count,
+    src/bpt/roofline.py:50-58, per token-head)."""
+    from kvq_decode_amd.roofline import step_bytes
+    return step_bytes(lens, hkv, d, kv_format)
 
 
 class Step:
@@ -210,21 +209,26 @@ def time_steps(step, steps, warmup):
 
 
 def time_stage1(step, iters):
-    """Average duration of the dominant kernel (stage 1) from HIP events recorded on the
-    stream it is launched on, back to back."""
+    """Average duration of the dominant kernel (stage 1): `iters` stage-1 launches back to
+    back between one pair of HIP events recorded on the stream they are launched on, with
+    nothing else between them. The inter-launch gaps are included, so this is an upper
+    bound of the rocprofv3 kernel-trace average of the same kernel."""
     import torch
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
-    for i in range(iters):
-        starts[i].record()
+    for _ in range(3):
         step.stage1()
-        ends[i].record()
-        step.stage2()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        step.stage1()
+    e1.record()
     torch.cuda.synchronize()
-    return sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / iters
+    return e0.elapsed_time(e1) / iters
 
 
-def time_flushed(step, iters):
+FLUSH_SAMPLES = 60
+
+
+def time_flushed(step, iters=FLUSH_SAMPLES):
     """Median step time with the 256 MB Infinity Cache flushed before each step (a 1 GiB
     scratch buffer is read, leaving clean lines), per-iteration events around the step."""
     import torch
@@ -243,25 +247,66 @@ def time_flushed(step, iters):
     return ts[len(ts) // 2]
 
 
-def cpu_baseline(q, k, v, bt, sl):
-    """The numpy oracle (oracle/attention.py, fp32) on the full fp16 workload on the host:
-    one BLAS thread, 1 warmup + 3 timed reps. Checker code, timed only as the CPU
-    baseline."""
-    from threadpoolctl import threadpool_limits
+def cpu_threads():
+    """Host threads the CPU baseline may use: the cores this process may run on, capped by
+    OMP_NUM_THREADS when it is set (the GPU box sets it to the box's CPU share)."""
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(n, int(env))) if env.isdigit() and int(env) > 0 else n
+
+
+def _oracle_step(qn, kn, vn, btn, sln, threads):
+    """One decode step of the numpy oracle over the whole batch. With threads > 1 the
+    (sequence, kv head) pairs - independent attention problems - run on a thread pool
+    (numpy releases the GIL in its gathers, casts, exps and matmuls), one BLAS thread
+    each; the oracle function itself is unchanged."""
+    from concurrent.futures import ThreadPoolExecutor
 
     from oracle.attention import paged_decode_attention_ref
+    B, hq, _ = qn.shape
+    hkv = kn.shape[2]
+    g = hq // hkv
+    if threads == 1:
+        return paged_decode_attention_ref(qn, kn, vn, btn, sln)
+    out = np.empty_like(qn)
+
+    def piece(bh):
+        b, h = bh
+        out[b:b + 1, h * g:(h + 1) * g] = paged_decode_attention_ref(
+            qn[b:b + 1, h * g:(h + 1) * g], kn[:, :, h:h + 1], vn[:, :, h:h + 1],
+            btn[b:b + 1], sln[b:b + 1])
+
+    with ThreadPoolExecutor(max_workers=threads) as pool:
+        list(pool.map(piece, [(b, h) for b in range(B) for h in range(hkv)]))
+    return out
+
+
+def cpu_baseline(q, k, v, bt, sl):
+    """The numpy oracle (oracle/attention.py, fp32) on the full fp16 workload on the host:
+    all of this process's host threads (cpu_threads(); the figure reported), then one
+    thread (beside it); 1 warmup + 3 timed reps each. Checker code, timed only as the CPU
+    baseline."""
+    from threadpoolctl import threadpool_limits
     qn, kn, vn, btn, sln = (t.cpu().numpy() for t in (q, k, v, bt, sl))
     nbytes = kv_bytes([int(x) for x in sln], "fp16")
-    with threadpool_limits(limits=1):
-        paged_decode_attention_ref(qn, kn, vn, btn, sln)
-        reps = 3
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            paged_decode_attention_ref(qn, kn, vn, btn, sln)
-        sec = (time.perf_counter() - t0) / reps
-    return {"value": nbytes / sec / 1e12, "unit": "TB/s", "cores": 1, "kind": "port",
-            "sample": f"full workload step (B={qn.shape[0]}, ctx={int(sln[0])}), numpy fp32 "
-                      f"oracle, 1 BLAS thread, 1 warmup + {reps} reps: {sec * 1e3:.0f} ms/step",
+    reps = 3
+    secs, outs = {}, {}
+    n = cpu_threads()
+    for threads in sorted({n, 1}, reverse=True):
+        with threadpool_limits(limits=1):
+            outs[threads] = _oracle_step(qn, kn, vn, btn, sln, threads)
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                _oracle_step(qn, kn, vn, btn, sln, threads)
+            secs[threads] = (time.perf_counter() - t0) / reps
+    # the thread pool only splits the batch: same attention problems, same results
+    assert np.allclose(outs[n].astype(np.float32), outs[1].astype(np.float32), atol=1e-3)
+    sec = secs[n]
+    sample = (f"full workload step (B={qn.shape[0]}, ctx={int(sln[0])}), numpy fp32 oracle, "
+              f"{n} threads over (sequence, kv head) pairs, 1 BLAS thread each, 1 warmup + "
+              f"{reps} reps: {sec * 1e3:.0f} ms/step; 1 thread: {secs[1] * 1e3:.0f} ms/step")
+    return {"value": nbytes / sec / 1e12, "unit": "TB/s", "cores": n, "kind": "port",
+            "sample": sample, "one_thread_value": nbytes / secs[1] / 1e12,
             "s_per_step": sec}
 
 
@@ -466,6 +511,7 @@ def run_layers(config, layers, steps, warmup, model="llama3-8b"):
     timed eagerly and as replays of one captured HIP graph."""
     import torch
     B, ctx, pool, fmt_name, desc = CONFIGS[config]
+    from kvq_decode_amd.roofline import MODELS
     model_layers, hq, hkv, d = MODELS[model]
     layers = layers or model_layers
     step_list, lens = [], None
@@ -634,6 +680,9 @@ def main():
     ap.add_argument("--waves", type=int, default=0)
     ap.add_argument("--pipeline", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-targets", action="store_true",
+                    help="C2 only: skip timing the north star's B1/64k and INT4-vs-fp16 "
+                         "targets")
     ap.add_argument("--sweep", action="store_true", help="split/waves sweep, table on stderr")
     ap.add_argument("--sweep-splits", default="1,2,4,8,16,32,64,128")
     ap.add_argument("--sweep-waves", default="1,2,4,8")
@@ -647,7 +696,8 @@ def main():
                     help="only STEPS untimed steps of --config (run under rocprofv3 --pmc)")
     ap.add_argument("--layers", type=int, default=0,
                     help="time a whole-model step of N layers of --config (HIP graph)")
-    ap.add_argument("--model", default=None, choices=sorted(MODELS),
+    ap.add_argument("--model", default=None,
+                    choices=("llama3-8b", "llama3-70b", "llama2-7b", "qwen2.5-7b"),
                     help="head shape (and, without --layers, layer count) of the whole-model "
                          "step; default llama3-8b")
     ap.add_argument("--write-path", action="store_true",
@@ -696,14 +746,48 @@ def main():
                           "table, seed 0"}
         fmt_name = CONFIGS[name][3]
         if not args.no_cpu_baseline and not args.suite and fmt_name == "fp16":
-            log("cpu baseline (numpy oracle) ...")
+            log(f"cpu baseline (numpy oracle, {cpu_threads()} threads, then 1) ...")
             cb = cpu_baseline(*inputs)
             log(f"cpu baseline: {cb['s_per_step'] * 1e3:.0f} ms/step")
             cb.pop("s_per_step")
             result["cpu_baseline"] = cb
         del inputs
         torch.cuda.empty_cache()
+        if (not args.suite and not args.no_targets and name == "C2" and args.splits is None
+                and not args.units):
+            result.update(north_star_targets(args.steps, args.warmup))
         print(json.dumps(result), flush=True)
+
+
+def north_star_targets(steps, warmup):
+    """The north star's other two targets, timed like the headline (same steps and warmup,
+    default plans, wall clock per step): fp16 batch 1 at 64k tokens against >= 50% of the
+    HBM peak, and INT4 against fp16 at batch 16 / 32k tokens against >= 3x fewer µs per
+    step. Returns the extra keys of the JSON line."""
+    import torch
+    out = {}
+    b1, _ = run_config("B1_64K", steps, warmup)
+    torch.cuda.empty_cache()
+    out["b1_64k_us_per_step"] = b1["us_per_step"]
+    out["b1_64k_pct_of_peak"] = b1["pct_of_hbm_peak"]
+    out["b1_64k_pct_of_peak_flushed"] = round(
+        100 * b1["config"]["kv_bytes_per_step"] / (b1["us_per_step_flushed_median"] * 1e-6)
+        / (PEAK_GBPS * 1e9), 2)
+    fp16, _ = run_config("B16_FP16", steps, warmup)
+    torch.cuda.empty_cache()
+    int4, _ = run_config("B16_INT4", steps, warmup)
+    torch.cuda.empty_cache()
+    out["b16_fp16_us_per_step"] = fp16["us_per_step"]
+    out["b16_int4_us_per_step"] = int4["us_per_step"]
+    out["int4_speedup"] = round(fp16["us_per_step"] / int4["us_per_step"], 3)
+    out["b16_fp16_stage1_us"] = fp16["roofline"]["kernel_us"]
+    out["b16_int4_stage1_us"] = int4["roofline"]["kernel_us"]
+    out["b16_int4_stage1_frac"] = int4["roofline"]["frac"]
+    out["int4_speedup_flushed"] = round(fp16["us_per_step_flushed_median"]
+                                        / int4["us_per_step_flushed_median"], 3)
+    log(f"targets: B1/64k {out['b1_64k_pct_of_peak']}% of peak (>= 50); INT4 vs fp16 at "
+        f"B16/32k {out['int4_speedup']}x (>= 3)")
+    return out
 
 
 if __name__ == "__main__":

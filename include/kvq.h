@@ -220,7 +220,11 @@ int kvq_decode_units_merge(const kvq_decode_args* args, int32_t units, const flo
  * quantized KV is "not started", README.md:16; its byte model is roofline.py:6-9).
  * For each sequence b and kv head, writes codes for the seq_lens[b] valid token slots of
  * both caches, K scales/zeros per channel per k_group tokens (stored in the group's first
- * block) and V scales/zeros per token. Slots past a sequence's length are not written.
+ * block) and V scales/zeros per token. Slots past a sequence's length are not written;
+ * seq_lens[b] is limited to the max_blocks * block_size slots its table row addresses.
+ * A token whose block-table entry lies outside [0, num_blocks) is neither read nor
+ * written (it does not enter its K group's min / max), and a K group whose first page
+ * lies outside the pool (where its (scale, zero) pairs would go) writes nothing.
  * k_src/v_src: fp16 caches with the given element strides (args->k_cache / v_cache are
  * the destination code caches, args->kv_format the target format); 16-byte aligned, with
  * strides that are multiples of 8 elements (KVQ_ERR_ALIGNMENT otherwise): each lane
@@ -235,8 +239,12 @@ int kvq_quantize_cache(const kvq_decode_args* args, const void* k_src, const voi
  * to the fp16 residual k_resid [batch, kv_heads, k_group, head_dim] at row p % k_group,
  * and the group containing p is (re)quantized from the residual rows 0..p%k_group, so
  * the cache always equals kvq_quantize_cache of all tokens so far.
- * args->seq_lens must already count the new token. k_new, v_new and k_resid are
- * contiguous and 16-byte aligned (KVQ_ERR_ALIGNMENT otherwise). */
+ * args->seq_lens must already count the new token. A sequence whose seq_lens[b] is below
+ * 1 or above max_blocks * block_size writes nothing (codes, pairs and residual), and a
+ * row whose block-table entry lies outside [0, num_blocks) is not written (a K group
+ * whose first page lies outside the pool writes nothing), as kvq_append_kv skips such
+ * slots. k_new, v_new and k_resid are contiguous and 16-byte aligned (KVQ_ERR_ALIGNMENT
+ * otherwise). */
 int kvq_quantize_append(const kvq_decode_args* args, const void* k_new, const void* v_new,
                         void* k_resid, kvq_stream_t stream);
 

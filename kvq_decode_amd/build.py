@@ -2,19 +2,22 @@
 
     python -m kvq_decode_amd.build          # or: python kvq_decode_amd/build.py
 
-Compiles csrc/*.hip and csrc/*.cpp with hipcc into kvq_decode_amd/libkvq.so. Always
-recompiles (the build check runs it on every call); a failed compile raises.
+Compiles csrc/*.hip and csrc/*.cpp with hipcc (one process per source, in parallel) and
+links kvq_decode_amd/libkvq.so. Always recompiles (the build check runs it on every call);
+a failed compile raises.
 """
 import os
 import subprocess
 import sys
 import time
+from concurrent.futures import ThreadPoolExecutor
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_PATH = os.path.join(PKG_DIR, "libkvq.so")
+OBJ_DIR = os.path.join(PKG_DIR, "_build")  # objects (not committed, not shipped)
 
 ARCH = "gfx950"
 SOURCES = ["capi.cpp", "decode.hip", "decode_q.hip", "quant.hip", "append.hip"]
@@ -41,18 +44,42 @@ def hipcc():
     return os.environ.get("HIPCC", os.path.join(rocm, "bin", "hipcc"))
 
 
-def build(verbose=False):
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *srcs, "-o", tmp]
-    t0 = time.time()
+def _compile(src, obj, cmd_base):
+    cmd = [*cmd_base, "-c", src, "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
+    return proc, cmd
+
+
+def _filter(proc):
     noise = ("packed-fp32-ops", "is not a recognized feature")
-    msgs = [ln for ln in (proc.stdout + proc.stderr).splitlines()
+    return [ln for ln in (proc.stdout + proc.stderr).splitlines()
             if not any(n in ln for n in noise)]
+
+
+def build(verbose=False):
+    """Compiles every source to an object in parallel (one hipcc per source), then links
+    libkvq.so. The kernels of different sources call nothing across files, so no
+    relocatable device code is needed."""
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    base = [hipcc(), *flags, f"-I{INCLUDE}", f"-I{CSRC}"]
+    t0 = time.time()
+    jobs = [(os.path.join(CSRC, s), os.path.join(OBJ_DIR, s + ".o")) for s in SOURCES]
+    with ThreadPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 1)) as pool:
+        results = list(pool.map(lambda j: _compile(j[0], j[1], base), jobs))
+    msgs = []
+    for proc, cmd in results:
+        msgs += _filter(proc)
+        if proc.returncode != 0:
+            raise RuntimeError("hipcc failed (%d):\n%s\ncommand: %s"
+                               % (proc.returncode, "\n".join(_filter(proc)), " ".join(cmd)))
+    tmp = LIB_PATH + ".tmp"
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC",
+           *[o for _, o in jobs], "-o", tmp]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
-        raise RuntimeError("hipcc failed (%d):\n%s\ncommand: %s"
-                           % (proc.returncode, "\n".join(msgs), " ".join(cmd)))
+        raise RuntimeError("link failed (%d):\n%s\ncommand: %s"
+                           % (proc.returncode, "\n".join(_filter(proc)), " ".join(cmd)))
     os.replace(tmp, LIB_PATH)
     if verbose:
         for m in msgs:

@@ -78,12 +78,27 @@ __device__ __forceinline__ uint32_t encode(float x, ScaleZero p) {
     return (uint32_t)__builtin_rintf(fminf(fmaxf(t, 0.f), R));
 }
 
+// Physical block of page `page` of sequence b, or -1 when the block-table entry lies
+// outside [0, num_blocks). The write paths neither read nor write a row whose page is
+// outside the pool (the fp16 append skips such slots the same way), so a bad table entry
+// cannot redirect codes or pairs into another sequence's block.
 __device__ __forceinline__ int phys_of(const QuantParams& p, int b, int page) {
-    return clampi(p.bt[(int64_t)b * p.bt_sb + page], 0, p.num_blocks - 1);
+    const int e = p.bt[(int64_t)b * p.bt_sb + page];
+    return (e >= 0 && e < p.num_blocks) ? e : -1;
 }
 
+// Tokens of sequence b the bulk quantizer covers: seq_lens[b], limited to the slots its
+// block-table row addresses.
 __device__ __forceinline__ int seq_len_of(const QuantParams& p, int b) {
     return clampi(p.seq_lens[b], 0, p.max_blocks * p.block_size);
+}
+
+// The append's sequence length: seq_lens[b] counts the new token, at position
+// seq_lens[b] - 1. A length below 1 or past the block table's last slot has no slot for
+// that token; the append then writes nothing for the sequence (-1).
+__device__ __forceinline__ int append_len_of(const QuantParams& p, int b) {
+    const int n = p.seq_lens[b];
+    return (n >= 1 && n <= p.max_blocks * p.block_size) ? n : -1;
 }
 
 typedef _Float16 h8q __attribute__((ext_vector_type(8)));
@@ -126,11 +141,15 @@ __device__ __forceinline__ void store8(uint8_t* row, int c, const uint32_t* code
 // zero). Codes go to each token's page slot, the pairs to the group's first block.
 // Append: the group holding the newest token, read from the fp16 residual except the new
 // row itself (from k_new), which also joins the residual for later appends.
+// Rows whose page lies outside the pool are not written (bulk: not read either, so they
+// do not enter the group's min / max); a group whose first page lies outside the pool
+// writes nothing. An append whose length has no slot (append_len_of) writes nothing, the
+// residual included.
 template <int FMT, int D, bool APPEND>
 __device__ __forceinline__ void quant_k_group(const QuantParams& p, int kvh, int grp, int b) {
     constexpr int LPR = D / 8, RS = 256 / LPR, CACHE = 8;
     const int c = threadIdx.x % LPR, rs = threadIdx.x / LPR;
-    const int n = seq_len_of(p, b);
+    const int n = APPEND ? append_len_of(p, b) : seq_len_of(p, b);
     int t0 = grp * p.k_group, t1 = min(t0 + p.k_group, n);
     if (APPEND) {  // only the group holding the newest token, rows 0..(n-1) % k_group
         if (n < 1) return;
@@ -138,6 +157,10 @@ __device__ __forceinline__ void quant_k_group(const QuantParams& p, int kvh, int
         t1 = n;
     }
     if (t0 >= t1) return;  // uniform over the workgroup
+    // the group's (scale, zero) pairs live in its first page: without it the group's codes
+    // could not be read back, so a group whose first page is outside the pool writes nothing
+    const int lead = phys_of(p, b, t0 >> p.bs_shift);
+    if (lead < 0) return;
     const int64_t resid = ((int64_t)b * p.kv_heads + kvh) * p.k_group * D + 8 * c;
     const _Float16* kn = p.k_new + ((int64_t)b * p.kv_heads + kvh) * D + 8 * c;
     if (APPEND && rs == 0)  // the new token's K joins the fp16 residual of its group
@@ -169,18 +192,22 @@ __device__ __forceinline__ void quant_k_group(const QuantParams& p, int kvh, int
         }
     };
     h8q cache[CACHE];
-    int cphys[CACHE];  // the cached rows' pages, for the code stores of pass 2
+    int cphys[CACHE];  // the cached rows' pages (-1: outside the pool), for pass 2
 #pragma unroll
     for (int i = 0; i < CACHE; ++i) {
         const int t = t0 + rs + i * RS;
+        cphys[i] = -1;
         if (t < t1) {
             cphys[i] = phys_of(p, b, t >> p.bs_shift);
-            cache[i] = load(t, cphys[i]);
-            reduce(cache[i]);
+            if (APPEND || cphys[i] >= 0) {  // append rows come from the residual
+                cache[i] = load(t, cphys[i]);
+                reduce(cache[i]);
+            }
         }
     }
     for (int t = t0 + rs + CACHE * RS; t < t1; t += RS) {
-        reduce(load(t, phys_of(p, b, t >> p.bs_shift)));
+        const int phys = phys_of(p, b, t >> p.bs_shift);
+        if (APPEND || phys >= 0) reduce(load(t, phys));
     }
 
     __shared__ float4 part[256][4];  // per thread: min 0-3, min 4-7, max 0-3, max 4-7
@@ -201,9 +228,8 @@ __device__ __forceinline__ void quant_k_group(const QuantParams& p, int kvh, int
                 mx[e] = fmaxf(mx[e], oM[e]);
             }
         }
-        // (scale, zero) pairs of channels 8c .. 8c + 7: two 16-byte stores
-        const int lead = phys_of(p, b, t0 >> p.bs_shift);
-        const int64_t sz = ((int64_t)lead * p.kv_heads + kvh) * D + 8 * c;
+        // (scale, zero) pairs of channels 8c .. 8c + 7: two 16-byte stores into the lead
+        // page, which also holds row t0, so min / max saw at least that row
         h8q pairs[2];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -212,6 +238,7 @@ __device__ __forceinline__ void quant_k_group(const QuantParams& p, int kvh, int
             pairs[e / 4][2 * (e % 4)] = (_Float16)q.s;
             pairs[e / 4][2 * (e % 4) + 1] = (_Float16)q.z;
         }
+        const int64_t sz = ((int64_t)lead * p.kv_heads + kvh) * D + 8 * c;
         *(h8q*)(p.k_scale + 2 * sz) = pairs[0];
         *(h8q*)(p.k_scale + 2 * sz + 8) = pairs[1];
     }
@@ -235,11 +262,11 @@ __device__ __forceinline__ void quant_k_group(const QuantParams& p, int kvh, int
 #pragma unroll
     for (int i = 0; i < CACHE; ++i) {
         const int t = t0 + rs + i * RS;
-        if (t < t1) emit(t, cphys[i], cache[i]);
+        if (t < t1 && cphys[i] >= 0) emit(t, cphys[i], cache[i]);
     }
     for (int t = t0 + rs + CACHE * RS; t < t1; t += RS) {
         const int phys = phys_of(p, b, t >> p.bs_shift);
-        emit(t, phys, load(t, phys));
+        if (phys >= 0) emit(t, phys, load(t, phys));
     }
 }
 
@@ -254,15 +281,23 @@ __device__ __forceinline__ void quant_v_rows(const QuantParams& p, int kvh, int 
     constexpr int LPR = D / 8, RPP = 256 / LPR;  // lanes per row, rows per pass
     constexpr int PASSES = APPEND ? 1 : kVRows / RPP;
     const int c = threadIdx.x % LPR;
-    const int n = seq_len_of(p, b);
-    // every pass's row is loaded first, so the workgroup waits on memory once
+    const int n = APPEND ? append_len_of(p, b) : seq_len_of(p, b);
+    // every pass's row is loaded first, so the workgroup waits on memory once. A row past
+    // the sequence or in a page outside the pool is neither read nor written (tok = -1).
     int tok[PASSES], phys[PASSES];
     h8q row[PASSES];
 #pragma unroll
     for (int i = 0; i < PASSES; ++i) {
         tok[i] = APPEND ? n - 1 : tile * kVRows + i * RPP + threadIdx.x / LPR;
-        if (tok[i] < 0 || tok[i] >= n) continue;  // whole rows (LPR-lane groups) skip together
+        if (tok[i] < 0 || tok[i] >= n) {  // whole rows (LPR-lane groups) skip together
+            tok[i] = -1;
+            continue;
+        }
         phys[i] = phys_of(p, b, tok[i] >> p.bs_shift);
+        if (phys[i] < 0) {
+            tok[i] = -1;
+            continue;
+        }
         const _Float16* src =
             APPEND ? p.v_new + ((int64_t)b * p.kv_heads + kvh) * D + 8 * c
                    : p.v_src + (int64_t)phys[i] * p.s_sblk + (int64_t)(tok[i] & (p.block_size - 1)) * p.s_stok +
@@ -271,7 +306,7 @@ __device__ __forceinline__ void quant_v_rows(const QuantParams& p, int kvh, int 
     }
 #pragma unroll
     for (int i = 0; i < PASSES; ++i) {
-        if (tok[i] < 0 || tok[i] >= n) continue;
+        if (tok[i] < 0) continue;
         const int slot = tok[i] & (p.block_size - 1);
         float x[8];
         to_float8(row[i], x);

@@ -111,12 +111,21 @@ def _qargs(cache: QuantizedKVCache, block_table, seq_lens, head_dim):
 
 
 def _check_cache(cache: QuantizedKVCache, block_table, seq_lens, head_dim):
+    """Every check the quantizer entry points share; all of them run on tensor metadata
+    before any launch, so a mismatch raises instead of reading or writing out of bounds."""
     _require(cache.kv_format in QUANT_FORMATS, f"kv_format must be one of {QUANT_FORMATS}")
     _require(block_table.dtype == seq_lens.dtype == torch.int32,
              "block_table and seq_lens must be int32")
+    _require(block_table.dim() == 2 and seq_lens.dim() == 1
+             and block_table.shape[0] == seq_lens.shape[0],
+             "block_table must be [B, max_blocks] and seq_lens [B]")
     _require(block_table.stride(1) == 1 and seq_lens.is_contiguous(),
              "block_table rows and seq_lens must be contiguous")
     nb, bs, hkv, dc = cache.k_codes.shape
+    _require(tuple(cache.v_codes.shape) == (nb, bs, hkv, dc),
+             "k_codes and v_codes shapes differ")
+    _require(cache.k_codes.dtype == cache.v_codes.dtype == torch.uint8,
+             "code caches must be uint8")
     _require(dc == (head_dim // 2 if cache.kv_format == "int4" else head_dim),
              "code cache width does not match head_dim")
     check_scale_pairs(cache.k_scale, cache.k_zero, (nb, hkv, head_dim), "k")
@@ -124,6 +133,13 @@ def _check_cache(cache: QuantizedKVCache, block_table, seq_lens, head_dim):
     _require(cache.k_group % bs == 0, "k_group must be a multiple of block_size")
     dev = cache.k_codes.device
     _require(dev.type == "cuda", "kvq runs on the GPU only (no CPU fallback)")
+    _check_devices(dev, v_codes=cache.v_codes, k_scale=cache.k_scale, v_scale=cache.v_scale,
+                   block_table=block_table, seq_lens=seq_lens)
+
+
+def _check_devices(dev, **tensors):
+    for name, t in tensors.items():
+        _require(t.device == dev, f"{name} must be on the cache's device {dev} (got {t.device})")
 
 
 def quantize_paged_cache(k_cache: torch.Tensor, v_cache: torch.Tensor,
@@ -144,7 +160,11 @@ def quantize_paged_cache(k_cache: torch.Tensor, v_cache: torch.Tensor,
         out = allocate_quantized_cache(nb, bs, hkv, d, kv_format, k_cache.device, k_group)
     _require(out.kv_format == kv_format and out.k_group == k_group,
              "out cache format / group differ")
+    _require(tuple(out.k_codes.shape[:3]) == (nb, bs, hkv),
+             f"out cache [num_blocks, block_size, kv_heads] = {tuple(out.k_codes.shape[:3])} "
+             f"differs from the source caches' {(nb, bs, hkv)}")
     _check_cache(out, block_table, seq_lens, d)
+    _check_devices(out.k_codes.device, k_cache=k_cache, v_cache=v_cache)
     args = _qargs(out, block_table, seq_lens, d)
     stream = torch.cuda.current_stream(k_cache.device).cuda_stream
     _lib.check("kvq_quantize_cache",
@@ -182,12 +202,18 @@ def quantize_append(cache: QuantizedKVCache, k_new: torch.Tensor, v_new: torch.T
     k_new / v_new: fp16 [B, Hkv, D]. V is quantized per token into its slot. K joins the
     fp16 residual k_resid [B, Hkv, k_group, D] of its group, and the group is re-quantized
     from the residual, so the cache always equals quantize_paged_cache of all tokens."""
+    _require(k_new.dim() == 3, "k_new must be [B, kv_heads, head_dim]")
     B, hkv, d = k_new.shape
     _check_cache(cache, block_table, seq_lens, d)
+    _require(block_table.shape[0] == B,
+             f"block_table has {block_table.shape[0]} rows for a batch of {B} new tokens")
+    _require(cache.k_codes.shape[2] == hkv,
+             f"the cache has {cache.k_codes.shape[2]} kv heads, k_new {hkv}")
     for name, t, shape in (("k_new", k_new, (B, hkv, d)), ("v_new", v_new, (B, hkv, d)),
                            ("k_resid", k_resid, (B, hkv, cache.k_group, d))):
         _require(t.dtype == torch.float16 and tuple(t.shape) == shape and t.is_contiguous(),
                  f"{name} must be contiguous fp16 of shape {shape}")
+    _check_devices(cache.k_codes.device, k_new=k_new, v_new=v_new, k_resid=k_resid)
     args = _qargs(cache, block_table, seq_lens, d)
     stream = torch.cuda.current_stream(k_new.device).cuda_stream
     _lib.check("kvq_quantize_append",

@@ -1,44 +1,44 @@
-"""KV bytes read per decode step and the bandwidth-bound minimum time.
+"""Algorithmic KV-read bytes of a decode step: the byte count every bandwidth figure of
+this package (TB/s, % of the HBM peak, roofline.frac) divides by.
 
-Restates the reference's byte model (pawaryd/kvq-decode src/bpt/roofline.py:1-67) with two
-changes: MI355X is in the GPU table, and FP8 carries fp16 scale + zero like INT8 (this
-build's FP8 format is KIVI-style with scales; the reference modelled FP8 as a plain cast,
-roofline.py:9, 25). Only KV-cache reads are counted - q, the output, the block table and
-the split-KV partials are excluded (roofline.py:1-4).
+What is counted, and why it matches the reference's model (pawaryd/kvq-decode
+src/bpt/roofline.py:1-9, 50-58) term for term, so that bandwidth figures compare across
+the two projects:
+  * only the KV cache: the query, the output, the block table and the split-KV partials
+    are left out;
+  * per context token and kv head: the K and V codes, 2 * head_dim * (bytes per code);
+  * for formats with (scale, zero) pairs (fp16 each, 4 bytes a pair): one pair per
+    channel per K group of `group_size` tokens for K, one pair per token for V.
+
+Format keys are this library's kv_format names ('fp16', 'int8', 'fp8_e4m3', 'int4') plus
+the reference's 'fp8', which its model prices as a bare one-byte cast without pairs. The
+library's 'fp8_e4m3' cache carries pairs like INT8 and is priced that way.
 """
-from dataclasses import dataclass
-from typing import Dict
+from typing import Dict, Iterable, NamedTuple, Tuple
 
-# Peak HBM bandwidth, GB/s (1e9 B/s). The first four are the reference's (roofline.py:15-20).
-GPUS: Dict[str, float] = {
-    "T4": 320.0,
-    "A100-80GB": 2039.0,
-    "H100-SXM": 3350.0,
-    "B200": 8000.0,
-    "MI355X": 8000.0,
-}
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, GB/s (1e9 bytes/s)
 
-# (bytes per element, has scale/zero) - roofline.py:23-28, FP8 with scales here.
-KV_DTYPES: Dict[str, tuple] = {
+PAIR_BYTES = 4  # one fp16 scale and one fp16 zero
+
+# kv format -> (bytes per code, carries (scale, zero) pairs)
+KV_DTYPES: Dict[str, Tuple[float, bool]] = {
     "fp16": (2.0, False),
-    "fp8_e4m3": (1.0, True),
+    "fp8": (1.0, False),      # the reference's plain-cast FP8 (no pairs)
+    "fp8_e4m3": (1.0, True),  # this library's FP8 cache (KVQ_KV_FP8_E4M3)
     "int8": (1.0, True),
     "int4": (0.5, True),
 }
 
-SCALE_BYTES = 2   # fp16 (roofline.py:30)
-ZP_PER_SCALE = 2  # scale + zero (roofline.py:31)
 
-
-@dataclass(frozen=True)
-class ModelShape:
+class ModelShape(NamedTuple):
     layers: int
     q_heads: int
     kv_heads: int
     head_dim: int
 
 
-# roofline.py:42-47
+# The attention shapes of the reference's model table (roofline.py:42-47), used for the
+# whole-model decode step.
 MODELS: Dict[str, ModelShape] = {
     "llama3-8b": ModelShape(32, 32, 8, 128),
     "llama3-70b": ModelShape(80, 64, 8, 128),
@@ -48,27 +48,31 @@ MODELS: Dict[str, ModelShape] = {
 
 
 def bytes_per_token_head(head_dim: int, kv_dtype: str, group_size: int = 128) -> float:
-    """KV bytes read per context token per kv head per layer: K + V payload plus, for
-    quantized formats, K per-channel scale+zero amortized over `group_size` tokens and V
-    per-token scale+zero (roofline.py:50-58)."""
-    elem, quant = KV_DTYPES[kv_dtype]
-    per_head = 2 * head_dim * elem
-    if quant:
-        per_head += head_dim * SCALE_BYTES * ZP_PER_SCALE / group_size
-        per_head += SCALE_BYTES * ZP_PER_SCALE
-    return per_head
+    """Bytes a decode reads for one context token of one kv head in one layer: K and V
+    codes, plus, for paired formats, the token's V pair and its 1/group_size share of the
+    K group's head_dim pairs. At head_dim 128 and groups of 128: fp16 512, int8 and
+    fp8_e4m3 264, int4 136 (the reference's 'fp8': 256)."""
+    code_bytes, paired = KV_DTYPES[kv_dtype]
+    total = 2 * head_dim * code_bytes
+    if paired:
+        total += PAIR_BYTES * head_dim / group_size + PAIR_BYTES
+    return total
 
 
-def kv_bytes_per_token(shape: ModelShape, kv_dtype: str, group_size: int = 128) -> float:
-    """KV bytes read per context token per decode step, summed over all layers."""
-    return shape.layers * shape.kv_heads * bytes_per_token_head(shape.head_dim, kv_dtype,
+def kv_bytes_per_token(model: ModelShape, kv_dtype: str, group_size: int = 128) -> float:
+    """Bytes one decode step reads per context token across all of a model's layers
+    (Llama-3-8B fp16: 128 KiB)."""
+    return model.layers * model.kv_heads * bytes_per_token_head(model.head_dim, kv_dtype,
                                                                 group_size)
 
 
-def bytes_per_step(shape: ModelShape, ctx: int, batch: int, kv_dtype: str,
-                   group_size: int = 128) -> float:
-    return kv_bytes_per_token(shape, kv_dtype, group_size) * ctx * batch
+def step_bytes(seq_lens: Iterable[int], kv_heads: int, head_dim: int, kv_dtype: str,
+               group_size: int = 128) -> int:
+    """Algorithmic bytes of one single-layer decode over a batch with these lengths."""
+    th = sum(int(n) for n in seq_lens) * kv_heads
+    return int(round(th * bytes_per_token_head(head_dim, kv_dtype, group_size)))
 
 
-def min_time_ms(nbytes: float, gpu: str) -> float:
-    return nbytes / (GPUS[gpu] * 1e9) * 1e3
+def min_time_us(nbytes: float, peak_gbps: float = HBM_PEAK_GBPS) -> float:
+    """Time to move `nbytes` at the HBM peak: the roofline floor of a step, µs."""
+    return nbytes / (peak_gbps * 1e9) * 1e6

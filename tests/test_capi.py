@@ -50,6 +50,24 @@ def test_struct_layout_matches_header():
     assert fields == [f[0] for f in DecodeArgs._fields_]
 
 
+def test_struct_abi_matches_c_compiler(tmp_path):
+    """Offsets, sizes and total size of kvq_decode_args as gcc lays it out from the header
+    (tests/cpu_checks/abi_layout.c) equal the ctypes mirror's: a type change in the header
+    (int32 -> int64, a field inserted) would misalign every call, even with the names and
+    their order unchanged."""
+    exe = tmp_path / "abi_layout"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", f"-I{os.path.join(REPO, 'include')}",
+                    os.path.join(REPO, "tests", "cpu_checks", "abi_layout.c"), "-o", str(exe)],
+                   check=True)
+    lines = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    c_fields = [ln.split() for ln in lines if ln and not ln.startswith("sizeof")]
+    c_size = int([ln for ln in lines if ln.startswith("sizeof")][0].split()[1])
+    py = [(name, getattr(DecodeArgs, name).offset, getattr(DecodeArgs, name).size)
+          for name, _ in DecodeArgs._fields_]
+    assert [(n, int(o), int(s)) for n, o, s in c_fields] == py
+    assert c_size == ctypes.sizeof(DecodeArgs)
+
+
 def test_version_and_status_strings():
     assert _lib.version().startswith("kvq ")
     L = _lib.lib()
