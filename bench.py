@@ -208,21 +208,28 @@ def time_steps(step, steps, warmup):
     return wall_ms, ev0.elapsed_time(ev1) / steps
 
 
-def time_stage1(step, iters):
-    """Average duration of the dominant kernel (stage 1): `iters` stage-1 launches back to
-    back between one pair of HIP events recorded on the stream they are launched on, with
-    nothing else between them. The inter-launch gaps are included, so this is an upper
-    bound of the rocprofv3 kernel-trace average of the same kernel."""
+def time_stage1(step, iters, blocks=5):
+    """Average duration of the dominant kernel (stage 1): `blocks` runs of `iters` stage-1
+    launches back to back, each run between one pair of HIP events recorded on the stream
+    the launches go to, with nothing else between them; the median run. Inter-launch gaps
+    are included, so this bounds the rocprofv3 kernel-trace average of the same kernel from
+    above. The median over runs keeps a run that meets a clock dip (MI355X lowers its
+    clock under sustained load for a few ms at a time) from setting the figure."""
+    import statistics
+
     import torch
     for _ in range(3):
         step.stage1()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(iters):
-        step.stage1()
-    e1.record()
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / iters
+    runs = []
+    for _ in range(blocks):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            step.stage1()
+        e1.record()
+        torch.cuda.synchronize()
+        runs.append(e0.elapsed_time(e1) / iters)
+    return statistics.median(runs)
 
 
 FLUSH_SAMPLES = 60
@@ -442,6 +449,100 @@ def traffic_summary(config, pmc_dir):
         f"traffic_over_algorithmic = {(rd + wr) / algo:.4f}",
     ]
     path = os.path.join(REPO, "profiles", f"decode_{config}_traffic.txt")
+    with open(path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    log("\n".join(lines))
+    log(f"wrote {path}")
+
+
+# Counter passes of --counter-summary: rocprofv3 collects a limited number of counters per
+# block in one run, so each pass is a run of its own (PMC_DIR/<pass>/).
+COUNTER_PASSES = {
+    "sq": "SQ_WAVES SQ_BUSY_CYCLES SQ_WAVE_CYCLES SQ_WAIT_INST_ANY SQ_WAIT_ANY "
+          "SQ_INSTS_VMEM_RD SQ_INSTS_VALU SQ_INSTS_LDS",
+    "tp": "TA_TA_BUSY TA_ADDR_STALLED_BY_TC_CYCLES TD_TC_STALL TD_TD_BUSY "
+          "TCP_TCP_TA_DATA_STALL_CYCLES TCP_PENDING_STALL_CYCLES TCP_TCC_READ_REQ_LATENCY "
+          "TCP_TCC_READ_REQ GRBM_GUI_ACTIVE",
+    "tc": "TCC_EA0_RDREQ_DRAM_CREDIT_STALL TCC_TAG_STALL TCC_HIT TCC_MISS",
+}
+XCDS, CUS = 8, 256  # GRBM_GUI_ACTIVE sums one instance per XCD; TA / TD one per CU
+
+
+def _pmc_dispatches(csv_dir, name_has):
+    """{dispatch id: {counter: value summed over instances, "_us": duration}} for the
+    dispatches of kernels whose name contains `name_has`."""
+    import csv
+    import glob
+    out = {}
+    for path in glob.glob(os.path.join(csv_dir, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(path)):
+            if name_has not in r["Kernel_Name"]:
+                continue
+            d = out.setdefault(r["Dispatch_Id"], {"_us": (int(r["End_Timestamp"]) -
+                                                          int(r["Start_Timestamp"])) / 1e3})
+            d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    if not out:
+        raise SystemExit(f"no dispatch of a kernel containing {name_has!r} under {csv_dir}")
+    return out
+
+
+def counter_summary(config, pmc_dir):
+    """Writes profiles/decode_<config>_counters.txt from the rocprofv3 --pmc passes under
+    pmc_dir (COUNTER_PASSES, each over `--profile-run 10` of the config): per-dispatch means
+    of each counter over the stage-1 dispatches after the first (which starts cold), and
+    the ratios that say where the stage-1 kernel's time goes."""
+    import statistics
+    B, ctx, pool, fmt_name, desc = CONFIGS[config]
+    lens = seq_lengths(B, ctx)
+    max_pages = max(-(-x // BS) for x in lens)
+    splits, waves, units = default_plan(config, B, max_pages, cu_count=CUS)
+    kernel = stage1_kernel(fmt_name, units)
+    mean, durs = {}, []
+    for name in COUNTER_PASSES:
+        ds = _pmc_dispatches(os.path.join(pmc_dir, name), kernel)
+        rows = [ds[k] for k in sorted(ds, key=int)][1:]
+        durs += [r["_us"] for r in rows]
+        for c in COUNTER_PASSES[name].split():
+            mean[c] = statistics.mean(r[c] for r in rows)
+    us = statistics.median(durs)
+    cyc = mean["GRBM_GUI_ACTIVE"] / XCDS
+    algo = kv_bytes(lens, fmt_name)
+    cmd = " ".join(f"{n}=\"{c}\"" for n, c in COUNTER_PASSES.items())
+    lines = [
+        f"# Counters of one stage-1 launch ({kernel}), {desc}",
+        "# rocprofv3 --pmc, one pass per block group; per-dispatch means over dispatches 2..10",
+        "# commands (D = an output directory; each pass its own run):",
+        f"#   for p in sq tp tc: rocprofv3 --pmc <COUNTER_PASSES[p]> -d D/$p -o p -f csv -- "
+        f"python3 bench.py --config {config} --profile-run 10",
+        f"#   python3 bench.py --config {config} --counter-summary D",
+        f"#   COUNTER_PASSES: {cmd}",
+        f"config = {config}",
+        f"plan = {'units ' + str(units) if units else 'splits ' + str(splits)}",
+        f"waves_per_group = {waves}",
+        f"median_dispatch_us = {us:.2f}",
+        f"algorithmic_bytes = {algo}",
+        f"achieved_tb_s = {algo / (us * 1e-6) / 1e12:.3f}",
+    ]
+    lines += [f"{c} = {v:.6g}" for c, v in sorted(mean.items())]
+    waves_n = mean["SQ_WAVES"]
+    lines += [
+        "# derived",
+        f"clock_mhz = {cyc / us:.0f}  # GRBM_GUI_ACTIVE per XCD / duration",
+        f"valu_insts_per_wave = {mean['SQ_INSTS_VALU'] / waves_n:.0f}",
+        f"vmem_read_insts_per_wave = {mean['SQ_INSTS_VMEM_RD'] / waves_n:.0f}",
+        f"lds_insts_per_wave = {mean['SQ_INSTS_LDS'] / waves_n:.0f}",
+        f"valu_insts_per_kib = {mean['SQ_INSTS_VALU'] / (algo / 1024):.2f}",
+        f"wave_frac_waiting_for_issue = {mean['SQ_WAIT_INST_ANY'] / mean['SQ_WAVE_CYCLES']:.3f}"
+        "  # SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES",
+        f"wave_frac_waiting_any = {mean['SQ_WAIT_ANY'] / mean['SQ_WAVE_CYCLES']:.3f}"
+        "  # SQ_WAIT_ANY / SQ_WAVE_CYCLES",
+        f"ta_busy_frac = {mean['TA_TA_BUSY'] / CUS / cyc:.3f}",
+        f"td_busy_frac = {mean['TD_TD_BUSY'] / CUS / cyc:.3f}",
+        f"td_stalled_on_tc_frac = {mean['TD_TC_STALL'] / CUS / cyc:.3f}",
+        f"l2_read_latency_cycles = {mean['TCP_TCC_READ_REQ_LATENCY'] / mean['TCP_TCC_READ_REQ']:.0f}",
+        f"l2_hit_rate = {mean['TCC_HIT'] / (mean['TCC_HIT'] + mean['TCC_MISS']):.3f}",
+    ]
+    path = os.path.join(REPO, "profiles", f"decode_{config}_counters.txt")
     with open(path, "w") as f:
         f.write("\n".join(lines) + "\n")
     log("\n".join(lines))
@@ -703,6 +804,8 @@ def main():
     ap.add_argument("--write-path", action="store_true",
                     help="time the KV write path of --config instead (bulk quantizer and "
                          "one-token append; fp16: append only)")
+    ap.add_argument("--counter-summary", metavar="PMC_DIR",
+                    help="write profiles/decode_<config>_counters.txt from PMC_DIR/{sq,tp,tc}")
     ap.add_argument("--traffic-summary", metavar="PMC_DIR",
                     help="write profiles/decode_<config>_traffic.txt from PMC_DIR/"
                          "{copy_fetch,copy_write,fetch,write}")
@@ -715,6 +818,9 @@ def main():
 
     if args.traffic_summary:
         traffic_summary(args.config, args.traffic_summary)
+        return
+    if args.counter_summary:
+        counter_summary(args.config, args.counter_summary)
         return
     if args.calibrate_copy:
         calibrate_copy()
