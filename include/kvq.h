@@ -47,7 +47,8 @@ typedef enum kvq_status {
     KVQ_ERR_ALIGNMENT = -4,     /* pointer or stride breaks the 16-byte vector-load alignment */
     KVQ_ERR_SPLITS = -5,        /* num_splits / pages_per_split inconsistent with max_blocks */
     KVQ_ERR_FORMAT = -6,        /* unknown kv_format or missing scale/zero tensors */
-    KVQ_ERR_HIP = -7            /* a HIP launch failed (hipGetLastError) */
+    KVQ_ERR_HIP = -7,           /* a HIP launch failed (hipGetLastError) */
+    KVQ_ERR_SCRATCH = -8        /* the workspace exceeds the static scratch buffer */
 } kvq_status;
 
 /* KV cache storage formats. F16 is the reference's format; the quantized ones follow the
@@ -269,6 +270,25 @@ int kvq_reshape_and_cache(const kvq_decode_args* args, const void* k_new, const 
                           int64_t new_stride_tok, int64_t new_stride_head,
                           const int64_t* slot_mapping, int32_t num_tokens,
                           kvq_stream_t stream);
+
+/* Bytes of the static device buffer kvq_paged_decode_static takes its workspace from: 16 MiB
+ * per GPU the library runs on, held until the process ends. */
+#define KVQ_STATIC_SCRATCH_BYTES (16 * 1024 * 1024)
+
+/* Allocation-free decode. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid allocation). units == 0: kvq_paged_decode(args, num_splits, ...); units > 0:
+ * kvq_decode_units(args, units, ...) - same kernels, same results - with the split-KV
+ * workspace (o_part, lse) taken from a static device buffer of KVQ_STATIC_SCRATCH_BYTES
+ * instead of caller memory. The call allocates and frees nothing; its first call on a device
+ * resolves that device's copy of the buffer (hipGetSymbolAddress). Returns KVQ_ERR_SCRATCH
+ * when the workspace, (o_part + lse floats) * 4 bytes with the lse part 256-byte aligned,
+ * exceeds the buffer: splits batch * q_heads * S * (head_dim + 1) floats for the normalized
+ * split count S (none for a single pass), units q_heads * (units + batch) *
+ * (head_dim + 1). Every call on a GPU shares that GPU's buffer: calls that overlap on one
+ * GPU (concurrent streams) race. */
+int kvq_paged_decode_static(const kvq_decode_args* args, int32_t num_splits, int32_t units,
+                            kvq_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -19,6 +19,10 @@ KVQ_ERR_ALIGNMENT = -4
 KVQ_ERR_SPLITS = -5
 KVQ_ERR_FORMAT = -6
 KVQ_ERR_HIP = -7
+KVQ_ERR_SCRATCH = -8
+
+# KVQ_STATIC_SCRATCH_BYTES: the static device buffer of kvq_paged_decode_static
+STATIC_SCRATCH_BYTES = 16 * 1024 * 1024
 
 # kvq_kv_format
 KV_FORMATS = {"fp16": 0, "int8": 1, "fp8_e4m3": 2, "int4": 3}
@@ -43,6 +47,7 @@ EXPORTED_SYMBOLS = (
     "kvq_quantize_append",
     "kvq_append_kv",
     "kvq_reshape_and_cache",
+    "kvq_paged_decode_static",
 )
 
 _i32 = ctypes.c_int32
@@ -128,6 +133,8 @@ def lib():
         L.kvq_append_kv.argtypes = [args_p, _vp, _vp, _vp]
         L.kvq_reshape_and_cache.restype = ctypes.c_int
         L.kvq_reshape_and_cache.argtypes = [args_p, _vp, _vp, _i64, _i64, _vp, _i32, _vp]
+        L.kvq_paged_decode_static.restype = ctypes.c_int
+        L.kvq_paged_decode_static.argtypes = [args_p, _i32, _i32, _vp]
         _lib = L
     return _lib
 

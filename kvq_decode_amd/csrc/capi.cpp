@@ -343,6 +343,7 @@ const char* kvq_status_string(int status) {
         case KVQ_ERR_SPLITS: return "invalid split configuration";
         case KVQ_ERR_FORMAT: return "invalid kv format or missing scales";
         case KVQ_ERR_HIP: return "HIP launch error";
+        case KVQ_ERR_SCRATCH: return "workspace exceeds the static scratch buffer";
         default: return "unknown status";
     }
 }

@@ -365,3 +365,22 @@ def test_python_op_argument_errors_and_no_cpu_fallback():
         paged_decode_attention(q, kc, kc, bt, sl, num_splits=2, units=8)
     with pytest.raises(KvqArgumentError, match="GPU only"):
         paged_decode_attention(q, kc, kc, bt, sl)
+
+
+def test_static_entry_point_rejects_on_the_host():
+    """kvq_paged_decode_static refuses, before touching a GPU, a workspace beyond its
+    KVQ_STATIC_SCRATCH_BYTES buffer (64 x 32 heads x 32 splits x 129 floats = 33.8 MB) and
+    negative unit counts; the header and the Python mirror agree on the buffer size."""
+    header = open(HEADER).read()
+    m = re.search(r"#define KVQ_STATIC_SCRATCH_BYTES \((\d+) \* (\d+) \* (\d+)\)", header)
+    assert m and int(m.group(1)) * int(m.group(2)) * int(m.group(3)) == _lib.STATIC_SCRATCH_BYTES
+    L = _lib.lib()
+    a = good_args()
+    a.batch = 64
+    assert L.kvq_paged_decode_static(ctypes.byref(a), 32, 0, None) == _lib.KVQ_ERR_SCRATCH
+    units = _lib.STATIC_SCRATCH_BYTES // (4 * 32 * 129)
+    assert L.kvq_paged_decode_static(ctypes.byref(a), 0, units, None) == _lib.KVQ_ERR_SCRATCH
+    assert L.kvq_paged_decode_static(ctypes.byref(a), 0, -1, None) == _lib.KVQ_ERR_SPLITS
+    assert L.kvq_paged_decode_static(None, 4, 0, None) == _lib.KVQ_ERR_NULL_POINTER
+    assert L.kvq_status_string(_lib.KVQ_ERR_SCRATCH) == \
+        b"workspace exceeds the static scratch buffer"
