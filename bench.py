@@ -549,16 +549,16 @@ def counter_summary(config, pmc_dir):
     log(f"wrote {path}")
 
 
-def default_plan(config, B, max_pages, cu_count=None, hkv=HKV):
+def default_plan(config, B, max_pages, cu_count=None, hkv=HKV, fmt_name=None):
     """(splits, waves, units) the op would use with num_splits=None: the work-unit plan
     (units > 0) where the library prefers it, else the split plan (C1: no split,
-    configs[0])."""
+    configs[0]). `fmt_name` defaults to the config's format."""
     from kvq_decode_amd import _sm_count
     from kvq_decode_amd.ops import plan_decode, plan_units
     if config == "C1":
         return 1, 0, 0
     cus = cu_count or _sm_count(0)
-    fmt_name = CONFIGS[config][3]
+    fmt_name = fmt_name or CONFIGS[config][3]
     units, waves = plan_units(B, hkv, BS, max_pages, cus, fmt_name)
     if units:
         return 0, waves, units
@@ -578,9 +578,14 @@ def run_config(config, steps, warmup, splits=None, waves=0, pipeline=0, flushed=
     step = Step(q, k, v, bt, sl, splits, waves, pipeline, fmt, units)
     nbytes = kv_bytes(lens, fmt_name)
     log(f"{config}: {desc}; {plan_text(step)} pages/split={step.pps} KV bytes/step={nbytes}")
-    wall_ms, ev_ms = time_steps(step, steps, warmup)
+    # Kernel-level figures first, the headline steps last: MI355X raises its clock over the
+    # first tens of ms of sustained load after idle (measured: C2 steps 169 us in the first
+    # 20 ms of a process, 159 us after), so the timed steps run at the steady clock of a
+    # serving GPU rather than during the ramp. They are still exactly `warmup` untimed and
+    # `steps` timed steps.
     stage1_ms = time_stage1(step, max(20, min(steps, 100)))
-    flushed_ms = time_flushed(step, 30) if flushed else None
+    flushed_ms = time_flushed(step) if flushed else None
+    wall_ms, ev_ms = time_steps(step, steps, warmup)
     log(f"  wall {wall_ms * 1e3:.1f} us/step (events {ev_ms * 1e3:.1f}), stage 1 "
         f"{stage1_ms * 1e3:.1f} us" + (f", flushed median {flushed_ms * 1e3:.1f} us" if flushed else ""))
     tbs = nbytes / (wall_ms * 1e-3) / 1e12
@@ -606,44 +611,62 @@ def run_config(config, steps, warmup, splits=None, waves=0, pipeline=0, flushed=
     return res, (q, k, v, bt, sl)
 
 
-def run_layers(config, layers, steps, warmup, model="llama3-8b"):
-    """Whole-model decode step: `layers` (0 = the model's count) independent caches of the
-    config's batch and lengths in the model's head shape, one decode each, back to back;
-    timed eagerly and as replays of one captured HIP graph."""
-    import torch
-    B, ctx, pool, fmt_name, desc = CONFIGS[config]
-    from kvq_decode_amd.roofline import MODELS
-    model_layers, hq, hkv, d = MODELS[model]
-    layers = layers or model_layers
+def build_layers(B, ctx, pool, fmt_name, layers, shape=(HQ, HKV, D), config=None):
+    """`layers` independent decode steps, each over its own cache of the given batch,
+    lengths and head shape (seed = layer index), with the op's default plan. Returns
+    (steps, lens)."""
     step_list, lens = [], None
     for layer in range(layers):
         q, k, v, bt, sl, fmt = make_inputs(B, ctx, pool, seed=layer, kv_format=fmt_name,
-                                           shape=(hq, hkv, d))
+                                           shape=shape)
         lens = lens or [int(x) for x in sl.tolist()]
-        splits, waves, units = default_plan(config, B, bt.shape[1], hkv=hkv)
+        splits, waves, units = default_plan(config, B, bt.shape[1], hkv=shape[1],
+                                            fmt_name=fmt_name)
         step_list.append(Step(q, k, v, bt, sl, splits, waves, 0, fmt, units))
         del q, k, v, bt, sl, fmt
-        if layer == 0:
-            log(f"{config} x {layers} layers, {model} ({hq}q/{hkv}kv, D={d}): {desc}; "
-                f"{plan_text(step_list[0])} waves={waves}")
-    torch.cuda.synchronize()
-    nbytes = kv_bytes(lens, fmt_name, hkv, d) * layers
+    return step_list, lens
 
-    def model_step():
-        for st in step_list:
-            st()
 
-    eager_wall, eager_ev = time_steps(model_step, steps, warmup)
+def run_model_step(step_list):
+    """One whole-model decode step: every layer's decode, back to back on one stream."""
+    for st in step_list:
+        st()
+
+
+def capture_layers(step_list):
+    """A HIP graph of one whole-model step, captured on a side stream; the steps launch on
+    the current stream again afterwards."""
+    import torch
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=side):
         for st in step_list:
             st.use_current_stream()
-        model_step()
+        run_model_step(step_list)
     for st in step_list:
         st.use_current_stream()
     torch.cuda.synchronize()
+    return graph
+
+
+def run_layers(config, layers, steps, warmup, model="llama3-8b"):
+    """Whole-model decode step: `layers` (0 = the model's count) independent caches of the
+    config's batch and lengths in the model's head shape, one decode each, back to back;
+    timed eagerly and as replays of one captured HIP graph."""
+    import torch
+
+    from kvq_decode_amd.roofline import MODELS
+    B, ctx, pool, fmt_name, desc = CONFIGS[config]
+    model_layers, hq, hkv, d = MODELS[model]
+    layers = layers or model_layers
+    step_list, lens = build_layers(B, ctx, pool, fmt_name, layers, (hq, hkv, d), config)
+    log(f"{config} x {layers} layers, {model} ({hq}q/{hkv}kv, D={d}): {desc}; "
+        f"{plan_text(step_list[0])} waves={step_list[0].args.waves_per_group}")
+    torch.cuda.synchronize()
+    nbytes = kv_bytes(lens, fmt_name, hkv, d) * layers
+    eager_wall, eager_ev = time_steps(lambda: run_model_step(step_list), steps, warmup)
+    graph = capture_layers(step_list)
     graph_wall, graph_ev = time_steps(graph.replay, steps, warmup)
     log(f"  eager {eager_wall * 1e3:.1f} us/step (events {eager_ev * 1e3:.1f}); graph "
         f"{graph_wall * 1e3:.1f} us/step (events {graph_ev * 1e3:.1f}); "

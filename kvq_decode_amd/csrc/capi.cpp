@@ -69,19 +69,10 @@ int check_decode_args(const kvq_decode_args* a, bool need_out) {
             return KVQ_ERR_UNSUPPORTED;
         if (!scale_pairs(a)) return KVQ_ERR_FORMAT;
         if (!aligned16(a->k_scale) || !aligned16(a->v_scale)) return KVQ_ERR_ALIGNMENT;
-        // The quantized kernels address each kv head's codes and scales through 32-bit
-        // offsets from the head's base: every offset must stay below 2^32 bytes.
-        const int64_t lim32 = int64_t(1) << 32;
-        const int64_t row = a->kv_format == KVQ_KV_INT4 ? a->head_dim / 2 : a->head_dim;
+        // The quantized kernels address a chunk from its block's 64-bit address: the pool
+        // may have any size; offsets inside a block are checked below.
         if (a->k_stride_blk < 0 || a->v_stride_blk < 0 || a->k_stride_tok < 0 ||
             a->v_stride_tok < 0)
-            return KVQ_ERR_UNSUPPORTED;
-        if (int64_t(a->num_blocks - 1) * a->k_stride_blk +
-                    int64_t(a->block_size - 1) * a->k_stride_tok + row >= lim32 ||
-            int64_t(a->num_blocks - 1) * a->v_stride_blk +
-                    int64_t(a->block_size - 1) * a->v_stride_tok + row >= lim32 ||
-            int64_t(a->num_blocks) * a->kv_heads * 4 * a->head_dim >= lim32 ||
-            int64_t(a->num_blocks) * a->kv_heads * 4 * a->block_size >= lim32)
             return KVQ_ERR_UNSUPPORTED;
     }
     // Vector loads: 16-byte aligned bases and row strides that keep every row aligned.

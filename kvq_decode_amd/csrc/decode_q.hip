@@ -232,29 +232,36 @@ __device__ __forceinline__ QLaneOff lane_offsets(const DecodeParams& p, int i16,
     return o;
 }
 
-// Buffer resources of one kv head's data, made once per wave (the head offset folded
-// into each base), and the strides a chunk's offset needs. Every offset from these bases
-// is below 2^32 bytes (checked on the host), so a chunk's loads take its offset as one
-// 32-bit scalar (soffset) plus the lane's 32-bit offset (voffset): a few scalar
-// multiplies per chunk and no vector address arithmetic.
+// Addressing of one kv head's data, made once per wave: the head's base in each tensor
+// (64-bit) and the strides a chunk's address needs. A chunk's loads go through buffer
+// resources based at its block - base + block * block stride, a 64-bit scalar product, so
+// pools of any size work - with the token slot as one 32-bit scalar offset (soffset) and
+// the lane's 32-bit offset (voffset): a few scalar operations per chunk and no vector
+// address arithmetic. Offsets inside a block are below 2^31 bytes (checked on the host).
 struct QBase {
-    __amdgpu_buffer_rsrc_t k, v, vs, ks;  // codes, and the (scale, zero) pair tensors
+    const char* k;   // codes of kv head kvh in block 0
+    const char* v;
+    const char* vs;  // V (scale, zero) pairs of kv head kvh in block 0
+    const char* ks;  // K (scale, zero) pairs of kv head kvh in block 0
     uint32_t k_sblk, v_sblk, k_stok, v_stok;
     uint32_t vs_blk, ks_blk;  // bytes per block of the V / K pair tensors
     uint32_t cmask;           // 16-token chunks per page - 1
 };
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rsrc(const void* base, int64_t off) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>((const char*)base + off), (short)0,
-                                             -1, 0x00020000);
+// Buffer resource at a wave-uniform address: stride 0, the full 32-bit range (offsets from
+// it stay below 2^31), dword data format.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const char* base, int phys,
+                                                             uint32_t blk_bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(base + (uint64_t)(uint32_t)phys * blk_bytes), (short)0, -1, 0x00020000);
 }
 
 __device__ __forceinline__ QBase q_base(const DecodeParams& p, int kvh) {
     QBase B;
-    B.k = head_rsrc(p.k, (int64_t)kvh * p.k_sh);
-    B.v = head_rsrc(p.v, (int64_t)kvh * p.v_sh);
-    B.vs = head_rsrc(p.v_scale, (int64_t)kvh * 4 * p.block_size);
-    B.ks = head_rsrc(p.k_scale, (int64_t)kvh * 4 * 128);
+    B.k = (const char*)p.k + (int64_t)kvh * p.k_sh;
+    B.v = (const char*)p.v + (int64_t)kvh * p.v_sh;
+    B.vs = (const char*)p.v_scale + (int64_t)kvh * 4 * p.block_size;
+    B.ks = (const char*)p.k_scale + (int64_t)kvh * 4 * 128;
     B.k_sblk = (uint32_t)p.k_sblk;
     B.v_sblk = (uint32_t)p.v_sblk;
     B.k_stok = (uint32_t)p.k_stok;
@@ -277,22 +284,22 @@ __device__ __forceinline__ void load_chunk_q(const QBase& B, int c, const QLaneO
                                              int lead, ChunkQ<FMT>& ch) {
     typedef QFmt<FMT> Q;
     const uint32_t slot = ((uint32_t)c & B.cmask) << 4;
-    const uint32_t ko = (uint32_t)phys * B.k_sblk + slot * B.k_stok;
-    const uint32_t vo = (uint32_t)phys * B.v_sblk + slot * B.v_stok;
+    const auto rk = block_rsrc(B.k, phys, B.k_sblk);
+    const auto rv = block_rsrc(B.v, phys, B.v_sblk);
 #pragma unroll
     for (int j = 0; j < Q::KLOADS; ++j)
-        ch.k[j] = __builtin_amdgcn_raw_buffer_load_b128(B.k, lo.k[j], ko, kNT);
+        ch.k[j] = __builtin_amdgcn_raw_buffer_load_b128(rk, lo.k[j], slot * B.k_stok, kNT);
 #pragma unroll
     for (int j = 0; j < Q::VLOADS; ++j)
-        ch.vr[j] = __builtin_amdgcn_raw_buffer_load_b128(B.v, lo.v[j], vo, kNT);
+        ch.vr[j] = __builtin_amdgcn_raw_buffer_load_b128(rv, lo.v[j], slot * B.v_stok, kNT);
     // V (scale, zero) pairs of tokens slot + 4g .. +3 (16 bytes; slots past the sequence
     // hold garbage and are masked by selects, never multiplied)
-    const uint32_t so = (uint32_t)phys * B.vs_blk + 4 * slot;
-    ch.vsz = __builtin_amdgcn_raw_buffer_load_b128(B.vs, lo.vs, so, kNT);
+    ch.vsz = __builtin_amdgcn_raw_buffer_load_b128(block_rsrc(B.vs, phys, B.vs_blk), lo.vs,
+                                                   4 * slot, kNT);
     // K group (scale, zero) pairs, stored with the group's first page `lead`
     if constexpr (WITH_K) {
-        const uint32_t go = (uint32_t)lead * B.ks_blk;
-        ch.ksz = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(B.ks, lo.ks, go, 0));
+        ch.ksz = __builtin_bit_cast(
+            u2, __builtin_amdgcn_raw_buffer_load_b64(block_rsrc(B.ks, lead, B.ks_blk), lo.ks, 0, 0));
     }
 }
 
