@@ -58,6 +58,8 @@ int check_decode_args(const kvq_decode_args* a, bool need_out) {
     if (a->head_dim < 32 || a->head_dim > 256) return KVQ_ERR_UNSUPPORTED;
     if (a->q_heads / a->kv_heads > kMaxGroup) return KVQ_ERR_UNSUPPORTED;
     if (a->block_size > 4096) return KVQ_ERR_UNSUPPORTED;
+    // token positions are 32-bit
+    if (int64_t(a->max_blocks) * a->block_size > INT32_MAX) return KVQ_ERR_UNSUPPORTED;
     if (!(a->scale == a->scale)) return KVQ_ERR_SHAPE;  // NaN scale
     if (a->kv_format < KVQ_KV_F16 || a->kv_format > KVQ_KV_INT4) return KVQ_ERR_FORMAT;
     if (a->kv_format != KVQ_KV_F16) {
@@ -208,8 +210,10 @@ int check_quant_args(const kvq_decode_args* a) {
     if (a->head_dim < 32 || a->head_dim > 256) return KVQ_ERR_UNSUPPORTED;
     if (a->k_group < a->block_size || a->k_group % a->block_size != 0) return KVQ_ERR_UNSUPPORTED;
     if (a->batch > 65535 || a->kv_heads > 65535) return KVQ_ERR_UNSUPPORTED;
+    // 1-D grids over (kv head, K group) and (kv head, 64-row tile); tokens are int32
     const int64_t tokens = int64_t(a->max_blocks) * a->block_size;
-    if (tokens / 16 > 65535 || cdiv(tokens, a->k_group) > 65535) return KVQ_ERR_UNSUPPORTED;
+    if (tokens > INT32_MAX || int64_t(a->kv_heads) * ((tokens + 63) / 64) > INT32_MAX)
+        return KVQ_ERR_UNSUPPORTED;
     if (a->k_stride_blk % 16 || a->k_stride_tok % 16 || a->k_stride_head % 16 ||
         a->v_stride_blk % 16 || a->v_stride_tok % 16 || a->v_stride_head % 16)
         return KVQ_ERR_ALIGNMENT;

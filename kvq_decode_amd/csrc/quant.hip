@@ -338,12 +338,16 @@ __device__ __forceinline__ void quant_v_rows(const QuantParams& p, int kvh, int 
 
 template <int FMT, int D>
 __global__ __launch_bounds__(256) void quant_k_kernel(const QuantParams p) {
-    quant_k_group<FMT, D, false>(p, blockIdx.x, blockIdx.y, blockIdx.z);
+    // grid (kv_heads * groups, batch): the groups of a sequence need no 16-bit grid axis
+    quant_k_group<FMT, D, false>(p, blockIdx.x % p.kv_heads, blockIdx.x / p.kv_heads,
+                                 blockIdx.y);
 }
 
 template <int FMT, int D>
 __global__ __launch_bounds__(256) void quant_v_kernel(const QuantParams p) {
-    quant_v_rows<FMT, D, false>(p, blockIdx.x, blockIdx.y, blockIdx.z);
+    // grid (kv_heads * row tiles, batch)
+    quant_v_rows<FMT, D, false>(p, blockIdx.x % p.kv_heads, blockIdx.x / p.kv_heads,
+                                blockIdx.y);
 }
 
 // Append in one launch: workgroup (kv head, role, sequence), role 0 re-quantizes the K
@@ -365,12 +369,12 @@ hipError_t launch_fmt_d(const QuantParams& p, hipStream_t stream) {
                            dim3(256), 0, stream, p);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL((quant_k_kernel<FMT, D>), dim3(p.kv_heads, p.max_groups, p.batch),
+    hipLaunchKernelGGL((quant_k_kernel<FMT, D>), dim3(p.kv_heads * p.max_groups, p.batch),
                        dim3(256), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int tiles = (p.max_blocks * p.block_size + kVRows - 1) / kVRows;
-    hipLaunchKernelGGL((quant_v_kernel<FMT, D>), dim3(p.kv_heads, tiles, p.batch), dim3(256),
+    const int tiles = (int)(((int64_t)p.max_blocks * p.block_size + kVRows - 1) / kVRows);
+    hipLaunchKernelGGL((quant_v_kernel<FMT, D>), dim3(p.kv_heads * tiles, p.batch), dim3(256),
                        0, stream, p);
     return hipGetLastError();
 }

@@ -457,21 +457,23 @@ def _dequant_int4_torch(qc, bt, b, L, h, bs, group=128):
 
 
 def test_int4_maximum_context():
-    """INT4 at the quantizers' limit: two sequences of 65535 pages (1,048,560 tokens and 37
-    fewer) over a 65536-block pool, needle keys at the last token and mid-sequence: the
-    default plan (work units), 64 splits and the single pass against float32 attention over
-    the dequantized cache."""
+    """INT4 past a million tokens: two sequences of 70000 pages (1,120,000 tokens and 37
+    fewer; more than the 65535 16-token chunks a 16-bit grid axis would allow the
+    quantizers) on disjoint blocks of a 140016-block pool, needle keys at the last token and
+    mid-sequence: the default plan (work units), 64 splits and the single pass against
+    float32 attention over the dequantized cache."""
     from kvq_decode_amd import paged_decode_attention
     from kvq_decode_amd.quant import quantize_paged_cache
     g = torch.Generator(device="cuda").manual_seed(6)
-    Hq, Hkv, D, bs, pool, pages = 32, 8, 128, 16, 65536, 65535
+    Hq, Hkv, D, bs, pool, pages = 32, 8, 128, 16, 140016, 70000
     lens = [pages * bs, pages * bs - 37]
     print(f"\n[int4 max context] lens={lens}", flush=True)
     k = torch.randn(pool, bs, Hkv, D, generator=g, device="cuda").half()
     v = torch.randn(pool, bs, Hkv, D, generator=g, device="cuda").half()
     q = torch.randn(2, Hq, D, generator=g, device="cuda").half()
-    bt = torch.stack([torch.randperm(pool, generator=g, device="cuda")[:pages]
-                      for _ in range(2)]).int()
+    # disjoint tables: a block shared by both sequences would hold the K pairs of only one
+    # of the two groups it leads
+    bt = torch.randperm(pool, generator=g, device="cuda")[:2 * pages].view(2, pages).int()
     scale = 1.0 / np.sqrt(D)
     needles = {}
     for b, L in enumerate(lens):
