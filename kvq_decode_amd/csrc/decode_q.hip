@@ -179,16 +179,17 @@ struct QFmt<KVQ_KV_INT4> {
     }
 };
 
-// Raw codes of one 16-token chunk as held by one lane, the (scale, zero) pairs of its 4
-// tokens (vsz[r]: token 4g + r, scale in the low half), and (lane l) the pairs of channels
-// 2l, 2l+1 of the chunk's K group (ksz). The group data is loaded with every chunk that
+// Raw codes of one 16-token chunk as held by one lane, the (scale, zero) pair of token
+// 4g + (l & 3) (vsz, scale in the low half; pv_weights gives every lane of the quad the
+// pairs of all 4 of its tokens 4g .. 4g + 3), and (lane l) the pairs of channels 2l, 2l+1 of
+// the chunk's K group (ksz). The group data is loaded with every chunk that
 // may start a group's use, not only with a group's first one: loads issued on every path
 // keep the compiler's wait counts exact, so no chunk waits for loads it does not use.
 template <int FMT>
 struct ChunkQ {
     u4v k[QFmt<FMT>::KLOADS];
     u4v vr[QFmt<FMT>::VLOADS];  // V whole rows (vstage_i4 / vstage_i8 give the layouts)
-    u4v vsz;
+    uint32_t vsz;
     u2 ksz;
 };
 
@@ -201,8 +202,9 @@ struct ChunkQ {
 //     rows reach the k-operand layout through the wave's LDS tile (kstage_q);
 //   V, the same whole-row pattern: INT4 row min(l/4, last) bytes [16(l%4), +16); INT8 /
 //     FP8 load j row min(8j + l/8, last) bytes [16(l%8), +16) (regrouped by vstage_*);
-//   the V (scale, zero) pairs of tokens 4g..4g+3 (16 bytes), and the K group's pairs of
-//   channels 2l, 2l+1 (8 bytes).
+//   the V (scale, zero) pair of token 4g + (l & 3) (4 bytes: the 64 bytes of the chunk's
+//   16 pairs reach the wave once per row of 16 lanes, not once per lane), and the K group's
+//   pairs of channels 2l, 2l+1 (8 bytes).
 struct QLaneOff {
     uint32_t k[2], v[2], vs, ks;
 };
@@ -227,7 +229,7 @@ __device__ __forceinline__ QLaneOff lane_offsets(const DecodeParams& p, int i16,
         for (int j = 0; j < 2; ++j)
             o.v[j] = (uint32_t)(min(8 * j + (lane >> 3), last) * (int)p.v_stok + 16 * (lane & 7));
     }
-    o.vs = 16 * g;
+    o.vs = 16 * g + 4 * (lane & 3);
     o.ks = 8 * lane;
     return o;
 }
@@ -292,10 +294,10 @@ __device__ __forceinline__ void load_chunk_q(const QBase& B, int c, const QLaneO
 #pragma unroll
     for (int j = 0; j < Q::VLOADS; ++j)
         ch.vr[j] = __builtin_amdgcn_raw_buffer_load_b128(rv, lo.v[j], slot * B.v_stok, kNT);
-    // V (scale, zero) pairs of tokens slot + 4g .. +3 (16 bytes; slots past the sequence
-    // hold garbage and are masked by selects, never multiplied)
-    ch.vsz = __builtin_amdgcn_raw_buffer_load_b128(block_rsrc(B.vs, phys, B.vs_blk), lo.vs,
-                                                   4 * slot, kNT);
+    // V (scale, zero) pair of token slot + 4g + (l & 3) (slots past the sequence hold
+    // garbage and are masked by selects, never multiplied)
+    ch.vsz = __builtin_amdgcn_raw_buffer_load_b32(block_rsrc(B.vs, phys, B.vs_blk), lo.vs,
+                                                  4 * slot, kNT);
     // K group (scale, zero) pairs, stored with the group's first page `lead`
     if constexpr (WITH_K) {
         ch.ksz = __builtin_bit_cast(
@@ -466,15 +468,24 @@ __device__ __forceinline__ void softmax_step(float* s2, SoftmaxState<128>& st, f
 // v_fma_mix on the fp16 scale) and lo = fp16(p s_t - hi): one fp16 rounding of p s_t
 // would be an error of up to 2^-11 (V - z) when one token dominates. corr accumulates
 // p z_t in fp32. Rows r with !ok (past the sequence: garbage scales) give 0.
+// vsz: lane r of each quad holds the pair of token 4g + r (ChunkQ::vsz); a DPP quad
+// broadcast (quad_perm [r, r, r, r]) hands it to the quad's other lanes. The quad's lanes
+// must all pass the same chunk's vsz.
+template <int R>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x55 * R, 0xf, 0xf, false);
+}
+
 template <bool MASK>
-__device__ __forceinline__ void pv_weights(const float* pr, u4v vsz, int valid, int g, h4& phi,
-                                           h4& plo, float& corr) {
+__device__ __forceinline__ void pv_weights(const float* pr, uint32_t vsz, int valid, int g,
+                                           h4& phi, h4& plo, float& corr) {
+    const uint32_t pairs[4] = {quad_bcast<0>(vsz), quad_bcast<1>(vsz), quad_bcast<2>(vsz),
+                               quad_bcast<3>(vsz)};
     float cadd = 0.f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const bool ok = !MASK || 4 * g + r < valid;
-        // element copied out first: a bit cast of the subscript itself reads element 0
-        const uint32_t pair = vsz[r];
+        const uint32_t pair = pairs[r];
         const h2 sz = __builtin_bit_cast(h2, pair);
         const float sv = (float)sz[0];
         const _Float16 hi = (_Float16)__builtin_fmaf(pr[r], sv, 0.f);
@@ -595,7 +606,7 @@ __device__ __forceinline__ void chunk_pair(const ChunkQ<FMT>& ca, const ChunkQ<F
     }
     float pr[4];
     softmax_step(s2, st, corr, pr);
-    const u4v vsz = slot ? cb.vsz : ca.vsz;
+    const uint32_t vsz = slot ? cb.vsz : ca.vsz;  // slot is uniform over each quad
     h4 phi, plo;
     pv_weights<MASK>(pr, vsz, valid, g, phi, plo, corr);
     // B operand: k-slots 8g + r (chunk a's token 4g + r) and 8g + 4 + r (chunk b's); the
