@@ -218,8 +218,13 @@ def time_stage1(step, iters, blocks=5):
     import statistics
 
     import torch
-    for _ in range(3):
-        step.stage1()
+    # spin the clock up first: at least SPIN_UP_S of back-to-back launches (MI355X takes
+    # tens of ms of sustained load to reach its steady clock after idle)
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < SPIN_UP_S:
+        for _ in range(10):
+            step.stage1()
+        torch.cuda.synchronize()
     runs = []
     for _ in range(blocks):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -233,6 +238,7 @@ def time_stage1(step, iters, blocks=5):
 
 
 FLUSH_SAMPLES = 60
+SPIN_UP_S = 0.05
 
 
 def time_flushed(step, iters=FLUSH_SAMPLES):
@@ -453,6 +459,54 @@ def traffic_summary(config, pmc_dir):
         f.write("\n".join(lines) + "\n")
     log("\n".join(lines))
     log(f"wrote {path}")
+
+
+def stats_summary(config, kt_dir, steps=200, warmup=20):
+    """Writes profiles/decode_<config>_kernel_stats.txt from a rocprofv3 --kernel-trace
+    --stats run of `bench.py --config <config> --steps <steps> --warmup <warmup>
+    --no-cpu-baseline --no-targets` (kt_dir/kt_kernel_stats.csv): the library's kernels,
+    their calls and average / min / max durations, and the stage-1 kernel's achieved
+    bandwidth from its average."""
+    import csv
+    import glob
+    B, ctx, pool, fmt_name, desc = CONFIGS[config]
+    lens = seq_lengths(B, ctx)
+    max_pages = max(-(-x // BS) for x in lens)
+    splits, waves, units = default_plan(config, B, max_pages, cu_count=CUS)
+    kernel = stage1_kernel(fmt_name, units)
+    path = glob.glob(os.path.join(kt_dir, "**", "*kernel_stats.csv"), recursive=True)[0]
+    rows = [r for r in csv.DictReader(open(path)) if "kvq::" in r["Name"]]
+    algo = kv_bytes(lens, fmt_name)
+    lines = [
+        f"# rocprofv3 kernel-trace statistics, {desc}",
+        "# (block_size 16, Llama-3-8B GQA shape; the library's default plan: "
+        f"{'units ' + str(units) if units else 'splits ' + str(splits)}, {waves} waves per workgroup)",
+        "# command:",
+        f"#   rocprofv3 --kernel-trace --stats -d D -o kt -f csv -- python3 bench.py --config {config} "
+        f"--steps {steps} --warmup {warmup} --no-cpu-baseline --no-targets",
+        f"#   python3 bench.py --config {config} --stats-summary D",
+        "# stage-1 launches: back-to-back runs (time_stage1), the flushed steps and the timed steps",
+        "",
+        f"{'kernel':60s}{'calls':>8s}{'avg_us':>10s}{'min_us':>10s}{'max_us':>10s}",
+    ]
+    stage1_avg = None
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
+        name = r["Name"].split("(")[0].replace("void ", "")
+        avg = float(r["AverageNs"]) / 1e3
+        lines.append(f"{name[:60]:60s}{int(r['Calls']):>8d}{avg:>10.2f}"
+                     f"{float(r['MinNs']) / 1e3:>10.2f}{float(r['MaxNs']) / 1e3:>10.2f}")
+        if kernel in name and stage1_avg is None:
+            stage1_avg = avg
+    lines += ["", f"stage-1 kernel = {kernel}",
+              f"stage-1 algorithmic KV bytes per launch = {algo}",
+              f"stage-1 average = {stage1_avg:.2f} us",
+              f"stage-1 achieved = {algo / (stage1_avg * 1e-6) / 1e9:.1f} GB/s = "
+              f"{algo / (stage1_avg * 1e-6) / (PEAK_GBPS * 1e9):.4f} of {PEAK_GBPS:.0f} GB/s"]
+    out = os.path.join(REPO, "profiles", f"decode_{config}_kernel_stats.txt")
+    with open(out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    log("\n".join(lines))
+    log(f"wrote {out}")
 
 
 # Counter passes of --counter-summary: rocprofv3 collects a limited number of counters per
@@ -827,6 +881,9 @@ def main():
     ap.add_argument("--write-path", action="store_true",
                     help="time the KV write path of --config instead (bulk quantizer and "
                          "one-token append; fp16: append only)")
+    ap.add_argument("--stats-summary", metavar="KT_DIR",
+                    help="write profiles/decode_<config>_kernel_stats.txt from a rocprofv3 "
+                         "--kernel-trace --stats output directory")
     ap.add_argument("--counter-summary", metavar="PMC_DIR",
                     help="write profiles/decode_<config>_counters.txt from PMC_DIR/{sq,tp,tc}")
     ap.add_argument("--traffic-summary", metavar="PMC_DIR",
@@ -844,6 +901,9 @@ def main():
         return
     if args.counter_summary:
         counter_summary(args.config, args.counter_summary)
+        return
+    if args.stats_summary:
+        stats_summary(args.config, args.stats_summary)
         return
     if args.calibrate_copy:
         calibrate_copy()
