@@ -383,15 +383,22 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ o_
 // Stage 2 of the work units (decode_common.h UnitSpace): sequence b's partials of q head hq
 // are rows hq * (units + B) + u + b for its units u = first .. last, where first / last
 // hold its first / last chunk. Workgroup = (q head, sequence), 256 threads; the prefix P_b
-// and the total N come from one block reduction over seq_lens (B <= 256).
+// and the total N come from one block reduction over seq_lens (thread t sums sequences
+// t, t + 256, ...; B <= kUnitMaxBatch).
 template <int D>
 __global__ __launch_bounds__(256) void merge_units_kernel(const DecodeParams p) {
     const int hq = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
     const int cap = p.max_blocks * p.block_size;
     const int n_b = cdiv(min(max(p.seq_lens[b], 0), cap), 16);
-    int n_t = 0;
-    if (t < p.batch) n_t = cdiv(min(max(p.seq_lens[t], 0), cap), 16);
-    const int tot = wave_sum(n_t), pre = wave_sum(t < b ? n_t : 0);
+    int n_t = 0, n_pre = 0;
+#pragma unroll
+    for (int j = 0; j < kUnitMaxBatch / 256; ++j) {
+        const int bb = t + 256 * j;
+        const int n = bb < p.batch ? cdiv(min(max(p.seq_lens[bb], 0), cap), 16) : 0;
+        n_t += n;
+        n_pre += bb < b ? n : 0;
+    }
+    const int tot = wave_sum(n_t), pre = wave_sum(n_pre);
     __shared__ int red[2][4];
     if ((t & 63) == 0) {
         red[0][t >> 6] = tot;

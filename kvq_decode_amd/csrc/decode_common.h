@@ -245,6 +245,39 @@ struct __attribute__((aligned(16))) UnitLds {
     int len[kUnitMaxBatch];
 };
 
+// The chunk prefix of the batch, lane t of one wave taking sequences per * t .. + per - 1
+// (per <= PER): pref[b] = P_b, pref[B] = N, len[b] = the clamped length. Every load is
+// issued before the first is used (unrolled, predicated on e < per).
+template <int PER>
+__device__ __forceinline__ void unit_prefix(const DecodeParams& p, int* pref, int* len_out,
+                                            int t, int per) {
+    const int B = p.batch, cap = p.max_blocks * p.block_size;
+    int n[PER], local = 0;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+        const int b = per * t + e;
+        const bool mine = e < per && b < B;
+        const int len = mine ? min(max(p.seq_lens[b], 0), cap) : 0;
+        if (mine) len_out[b] = len;
+        n[e] = cdiv(len, 16);
+        local += n[e];
+    }
+    int incl = local;  // inclusive scan over the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o);
+        if (t >= o) incl += y;
+    }
+    int run = incl - local;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+        const int b = per * t + e;
+        if (e < per && b < B) pref[b] = run;
+        run += n[e];
+    }
+    if (t == 63) pref[B] = incl;
+}
+
 // Runs fn(kvh, b, seq_len, w_lo, w_hi, part_base, part_stride) for each segment of this
 // workgroup's unit (workgroup = (kv head, unit), W waves), in batch order, with a
 // barrier between segments (they reuse the LDS of the range functions). [w_lo, w_hi) is
@@ -267,30 +300,12 @@ __device__ __forceinline__ void for_unit_segments(const DecodeParams& p, Fn&& fn
     }
     const int t = threadIdx.x, B = p.batch;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    if (t < 64) {  // lane t: sequences 4t .. 4t + 3
-        const int cap = p.max_blocks * p.block_size;
-        int n[4], local = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int b = 4 * t + e;
-            const int len = b < B ? min(max(p.seq_lens[b], 0), cap) : 0;
-            if (b < B) s.len[b] = len;
-            n[e] = cdiv(len, 16);
-            local += n[e];
-        }
-        int incl = local;  // inclusive scan over the wave
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o);
-            if (t >= o) incl += y;
-        }
-        int run = incl - local;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            if (4 * t + e < B) s.pref[4 * t + e] = run;
-            run += n[e];
-        }
-        if (t == 63) s.pref[B] = incl;
+    if (t < 64) {  // lane t: sequences per * t .. per * t + per - 1
+        const int per = (B + 63) >> 6;
+        if (per <= 4)  // batches up to 256: the short scan
+            unit_prefix<4>(p, s.pref, s.len, t, per);
+        else
+            unit_prefix<kUnitMaxBatch / 64>(p, s.pref, s.len, t, per);
     }
     __syncthreads();
     UnitSpace us;

@@ -68,7 +68,7 @@ hipError_t launch_decode_q(const DecodeParams& p, int kv_format, int head_dim, b
 // Work units (decode_common.h UnitSpace): stage 1 over p.units units per kv head of
 // `waves`-wave workgroups, and the merge of each sequence's partial rows into p.out.
 // Batch at most kUnitMaxBatch; quantized formats head_dim 128.
-constexpr int kUnitMaxBatch = 256;
+constexpr int kUnitMaxBatch = 1024;  // a multiple of 64
 hipError_t launch_decode_units(const DecodeParams& p, int kv_format, int head_dim, int waves,
                                int ring, hipStream_t stream);
 hipError_t launch_merge_units(const DecodeParams& p, int head_dim, hipStream_t stream);

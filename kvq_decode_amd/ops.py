@@ -99,7 +99,7 @@ def normalize_splits(num_splits: int, max_pages: int) -> Tuple[int, int]:
 def plan_units(batch: int, kv_heads: int, block_size: int, max_pages: int,
                cu_count: int, kv_format: str = "fp16") -> Tuple[int, int]:
     """(units, waves_per_group) of the work-unit partition when the library prefers it
-    for num_splits=None, else (0, 0) (kvq_plan_units): batches of 2 to 256 sequences
+    for num_splits=None, else (0, 0) (kvq_plan_units): batches of 2 to 1024 sequences
     whose split plan (`plan_decode`) has 2 or more splits, or whose longest context is at
     least 4096 tokens, get 2 waves per CU in 2-wave
     unit workgroups (fp16), 4 in 4-wave workgroups (INT8, FP8) or 8 in 2-wave workgroups
@@ -230,9 +230,9 @@ def paged_decode_attention(
     `workspace_shapes(B, Hq, D, S)` for the normalized split count S (work units:
     `units_workspace_shapes(B, Hq, D, units)`; with num_splits=None,
     `plan_workspace_shapes` gives whichever the plan needs). With num_splits=None the partition comes
-    from `plan_units` (work units: batches of 2 to 256 with 4096-token contexts or that the
+    from `plan_units` (work units: batches of 2 to 1024 with 4096-token contexts or that the
     split plan would split) or else `plan_decode` (`choose_num_splits` keeps the reference's formula for callers
-    that want it). `units` > 0 (B <= 256) asks for the work-unit partition: per kv head,
+    that want it). `units` > 0 (B <= 1024) asks for the work-unit partition: per kv head,
     all sequences' 16-token chunks in batch order cut into `units` equal ranges
     (`kvq_decode_units`)."""
     _require(kv_format in KV_FORMATS, f"unknown kv_format {kv_format!r}")

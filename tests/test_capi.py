@@ -145,7 +145,8 @@ def test_plan_units():
         (64, 64, "fp16", (0, 0)),       # a single pass over 1024-token contexts
         (64, 256, "fp16", (32, 2)),     # a single pass in the split plan, 4096 tokens
         (64, 255, "fp16", (0, 0)),
-        (257, 2048, "fp16", (0, 0)),    # beyond one workgroup's prefix table
+        (1024, 256, "fp16", (32, 2)),   # the largest batch one workgroup's prefix table holds
+        (1025, 2048, "fp16", (0, 0)),   # beyond it
     ]
     for batch, pages, fmt, want in cases:
         assert plan_units(batch, 8, 16, pages, 256, fmt) == want, (batch, pages, fmt)
@@ -316,7 +317,7 @@ def test_units_reject():
         assert fn(ctypes.byref(a), 0, op, lse, None) == _lib.KVQ_ERR_SPLITS
         assert fn(ctypes.byref(a), 8, 0, lse, None) == _lib.KVQ_ERR_NULL_POINTER
         assert fn(None, 8, op, lse, None) == _lib.KVQ_ERR_NULL_POINTER
-    a.batch = 257  # one workgroup reads every seq_len of the batch
+    a.batch = 1025  # one workgroup reads every seq_len of the batch
     assert L.kvq_decode_units(ctypes.byref(a), 8, op, lse, None) == _lib.KVQ_ERR_UNSUPPORTED
     a.batch = 2
     a.waves_per_group = 8  # unit workgroups: 1, 2 or 4 waves

@@ -43,19 +43,21 @@ def test_units_head_dims_and_ring_depths(D, pipeline):
     check_close(out, ref, f"units=13 D={D} pipeline={pipeline}")
 
 
-def test_units_full_batch_ragged():
-    """256 sequences (the work-unit limit) of lengths 1 .. 600, fewer units than sequences
-    and more."""
+@pytest.mark.parametrize("B", [65, 256, 257, 1000, 1024])
+def test_units_full_batch_ragged(B):
+    """Up to 1024 sequences (the work-unit limit; past 64 every lane of the prefix scan
+    takes several sequences, past 256 every merge thread several) of lengths 1 .. 600,
+    fewer units than sequences and more, against the oracle."""
     from kvq_decode_amd import paged_decode_attention
-    rng = np.random.default_rng(7)
-    lens = [int(x) for x in rng.integers(1, 600, 256)]
+    rng = np.random.default_rng(7 + B)
+    lens = [int(x) for x in rng.integers(1, 600, B)]
     q, kc, vc, bt, sl = make(8, 2, 64, 16, lens, seed=7)
     ref = paged_decode_attention_ref(q, kc, vc, bt, sl, out_dtype=np.float32)
     args = to_gpu(q, kc, vc, bt, sl)
     for units in (40, 300, 5000):
         out = paged_decode_attention(*args, units=units)
         torch.cuda.synchronize()
-        check_close(out, ref, f"B=256 units={units}")
+        check_close(out, ref, f"B={B} units={units}")
 
 
 def test_units_empty_sequences_give_zero_rows():
@@ -98,7 +100,7 @@ def test_units_workspace_and_limits():
         paged_decode_attention(q, kc, vc, bt, sl, units=units,
                                workspace=(ws[0][:, :units].contiguous(), ws[1]))
     # more sequences than one workgroup's prefix table holds
-    q2, kc2, vc2, bt2, sl2 = to_gpu(*make(2, 1, 32, 16, [5] * 257, seed=2))
+    q2, kc2, vc2, bt2, sl2 = to_gpu(*make(2, 1, 32, 16, [5] * 1025, seed=2))
     with pytest.raises(KvqError):
         paged_decode_attention(q2, kc2, vc2, bt2, sl2, units=8)
 
