@@ -150,6 +150,40 @@ def test_append_equals_bulk_other_head_dims(fmt, D):
         assert np.array_equal(g, w), name
 
 
+@pytest.mark.parametrize("k_group", [16, 64, 256])
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_append_equals_bulk_other_k_groups(fmt, k_group):
+    """Quantize-on-append with K groups of 16-256 tokens (256: more rows than a lane keeps
+    in registers), appended one token at a time across group boundaries: the cache equals
+    the bulk quantization of all tokens with the same group size, bit for bit."""
+    from kvq_decode_amd.quant import init_k_residual, quantize_append, quantize_paged_cache
+    bs, Hkv = 16, 2
+    n0, n1 = [250, 15, 60, 1], [258, 17, 66, 6]
+    q, kc, vc, bt, sl1 = make(n1, bs, Hq=4, Hkv=Hkv, seed=23)
+    kc_g, vc_g, bt_g = gpu(kc), gpu(vc), gpu(bt)
+    sl0 = torch.tensor(n0, dtype=torch.int32, device="cuda")
+    qc = quantize_paged_cache(kc_g, vc_g, bt_g, sl0, fmt, k_group=k_group)
+    resid = init_k_residual(kc_g, bt_g, sl0, k_group)
+    cur = list(n0)
+    while cur != n1:
+        cur = [min(c + 1, e) for c, e in zip(cur, n1)]
+        k_new = torch.stack([kc_g[bt_g[b, (t - 1) // bs], (t - 1) % bs] for b, t in enumerate(cur)])
+        v_new = torch.stack([vc_g[bt_g[b, (t - 1) // bs], (t - 1) % bs] for b, t in enumerate(cur)])
+        quantize_append(qc, k_new.contiguous(), v_new.contiguous(), bt_g,
+                        torch.tensor(cur, dtype=torch.int32, device="cuda"), resid)
+    want = quantize_paged_cache(kc_g, vc_g, bt_g, gpu(sl1), fmt, k_group=k_group)
+    torch.cuda.synchronize()
+    slots = valid_slots(bt, sl1, bs)
+    for name in ("k_codes", "v_codes"):
+        g = getattr(qc, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
+        w = getattr(want, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
+        assert np.array_equal(g, w), f"{name} k_group={k_group}"
+    lead = lead_blocks(bt, sl1, bs, k_group)
+    for name in ("k_scale", "k_zero"):
+        assert np.array_equal(getattr(qc, name).cpu().numpy()[lead],
+                              getattr(want, name).cpu().numpy()[lead]), name
+
+
 def _tie_rows(rng, n, width, fmt):
     """n rows of `width` fp16 values whose first two entries are the row's min and max,
     chosen so that scale and zero come out exact (INT: z = -1.5, s = 2^-6; FP8: z = 0,
@@ -233,11 +267,11 @@ def test_decode_matches_fp32_attention_over_dequantized_cache(fmt, bs, num_split
 @pytest.mark.parametrize("fmt", FORMATS)
 def test_decode_group8_and_mqa_heads(fmt):
     """Other GQA groups over a quantized cache: 1, 2 and 3 q heads per kv head (the
-    chunk-pair kernel with padded head columns), 5 and 8 (one QK chain with hi / lo
-    columns), MQA, and 16 (two chains)."""
+    chunk-pair kernel with padded head columns), 5, 7 (Qwen2.5-7B's 28 / 4) and 8 (one QK
+    chain with hi / lo columns), MQA, and 16 (two chains)."""
     from kvq_decode_amd import paged_decode_attention
     from kvq_decode_amd.quant import quantize_paged_cache
-    for Hq, Hkv in ((8, 8), (4, 2), (6, 2), (10, 2), (16, 2), (8, 1), (32, 2)):
+    for Hq, Hkv in ((8, 8), (4, 2), (6, 2), (10, 2), (28, 4), (16, 2), (8, 1), (32, 2)):
         q, kc, vc, bt, sl = make([700, 3], 16, Hq=Hq, Hkv=Hkv, seed=2)
         qc = quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt)
         host = {n: getattr(qc, n).cpu().numpy() for n in
