@@ -128,6 +128,17 @@ int kvq_choose_num_splits(int32_t batch, int32_t kv_heads, int32_t block_size,
                           int32_t max_pages, int32_t cu_count, int32_t target_per_cu,
                           int32_t min_tokens_per_split);
 
+/* q-head blocks per kv head (no reference counterpart; the reference's kernel takes any
+ * q_heads / kv_heads group, triton_fp16.py:196). The kernels serve at most 16 q heads per
+ * kv head in one MFMA column block, so a group G > 16 is cut into k blocks of G / k heads,
+ * k the smallest divisor of G with G / k <= 16, and each block runs as a kv head of its own
+ * that reads the same cache head: the caches are read k times, and the kernels' grids
+ * count kv_heads * k kv heads. Pass kv_heads * k as `kv_heads` to kvq_plan_decode and
+ * kvq_plan_units. Returns k (1 for G <= 16), or KVQ_ERR_SHAPE when q_heads is not a
+ * positive multiple of kv_heads. The decode entry points return KVQ_ERR_UNSUPPORTED when
+ * kv_heads * k exceeds 65535. */
+int kvq_head_blocks(int32_t q_heads, int32_t kv_heads);
+
 /* MI355X work plan used when the caller gives no split count; takes the place of the
  * heuristic above (triton_fp16.py:175-180) on this hardware. It sizes the decomposition
  * in waves, because a workgroup here holds several waves that combine through LDS:

@@ -10,6 +10,7 @@ from kvq_decode_amd.ops import (  # noqa: F401
     KvqArgumentError,
     _sm_count,
     choose_num_splits,
+    head_blocks,
     normalize_splits,
     paged_decode_attention,
     plan_decode,
@@ -24,6 +25,7 @@ from kvq_decode_amd import library  # noqa: F401  (registers torch.ops.kvq.*)
 __all__ = [
     "paged_decode_attention",
     "choose_num_splits",
+    "head_blocks",
     "normalize_splits",
     "workspace_shapes",
     "units_workspace_shapes",

@@ -31,6 +31,7 @@ KV_FORMATS = {"fp16": 0, "int8": 1, "fp8_e4m3": 2, "int4": 3}
 EXPORTED_SYMBOLS = (
     "kvq_version",
     "kvq_cache_format_version",
+    "kvq_head_blocks",
     "kvq_status_string",
     "kvq_choose_num_splits",
     "kvq_plan_decode",
@@ -100,6 +101,8 @@ def lib():
         L.kvq_version.argtypes = []
         L.kvq_cache_format_version.restype = ctypes.c_int
         L.kvq_cache_format_version.argtypes = []
+        L.kvq_head_blocks.restype = ctypes.c_int
+        L.kvq_head_blocks.argtypes = [_i32, _i32]
         L.kvq_status_string.restype = ctypes.c_char_p
         L.kvq_status_string.argtypes = [ctypes.c_int]
         L.kvq_choose_num_splits.restype = ctypes.c_int

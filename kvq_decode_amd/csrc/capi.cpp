@@ -30,6 +30,22 @@ int64_t pow2_floor(int64_t x) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// q-head blocks per kv head. The kernels serve at most kMaxGroup q heads per kv head (one
+// MFMA column block), so a larger group G is cut into k blocks of G / k heads, k the
+// smallest divisor of G with G / k <= kMaxGroup; each block runs as a kv head of its own
+// that reads the same cache head, so the caches are read k times.
+int head_blocks(int64_t q_heads, int64_t kv_heads) {
+    const int64_t G = q_heads / kv_heads;
+    int64_t k = (G + kMaxGroup - 1) / kMaxGroup;
+    while (G % k) ++k;
+    return int(k);
+}
+
+// kv heads of the kernels' grids: kv_heads * head_blocks
+int64_t grid_heads(const kvq_decode_args* a) {
+    return int64_t(a->kv_heads) * head_blocks(a->q_heads, a->kv_heads);
+}
+
 // The zero of each quantized scale pair is the fp16 right after its scale (interleaved
 // (scale, zero) storage, include/kvq.h).
 bool scale_pairs(const kvq_decode_args* a) {
@@ -51,12 +67,12 @@ int check_decode_args(const kvq_decode_args* a, bool need_out) {
         return KVQ_ERR_SHAPE;
     if (a->batch > 65535 || a->kv_heads > 65535) return KVQ_ERR_UNSUPPORTED;
     if (a->q_heads % a->kv_heads != 0) return KVQ_ERR_SHAPE;
+    if (grid_heads(a) > 65535) return KVQ_ERR_UNSUPPORTED;
     // The reference requires power-of-two head_dim >= 16 and block_size >= 16
     // (triton_fp16.py:197-198); anything else is a shape error here too.
     if (!is_pow2(a->head_dim) || a->head_dim < 16) return KVQ_ERR_SHAPE;
     if (!is_pow2(a->block_size) || a->block_size < 16) return KVQ_ERR_SHAPE;
     if (a->head_dim < 32 || a->head_dim > 256) return KVQ_ERR_UNSUPPORTED;
-    if (a->q_heads / a->kv_heads > kMaxGroup) return KVQ_ERR_UNSUPPORTED;
     if (a->block_size > 4096) return KVQ_ERR_UNSUPPORTED;
     // token positions are 32-bit
     if (int64_t(a->max_blocks) * a->block_size > INT32_MAX) return KVQ_ERR_UNSUPPORTED;
@@ -131,8 +147,9 @@ kvq::DecodeParams make_params(const kvq_decode_args* a) {
     p.v_zero = static_cast<const _Float16*>(a->v_zero);
     p.batch = a->batch;
     p.q_heads = a->q_heads;
-    p.kv_heads = a->kv_heads;
-    p.group = a->q_heads / a->kv_heads;
+    p.kv_rep = head_blocks(a->q_heads, a->kv_heads);
+    p.kv_heads = a->kv_heads * p.kv_rep;
+    p.group = a->q_heads / p.kv_heads;
     p.block_size = a->block_size;
     p.max_blocks = a->max_blocks;
     p.num_blocks = a->num_blocks;
@@ -148,7 +165,7 @@ kvq::DecodeParams make_params(const kvq_decode_args* a) {
 }
 
 int64_t lds_bytes(const kvq_decode_args* a, int waves) {
-    const int group = a->q_heads / a->kv_heads;
+    const int group = int(a->q_heads / grid_heads(a));  // q heads per kernel kv head
     const int64_t combine = int64_t(4) * (int64_t(waves) * group * a->head_dim + 32 * waves);
     // fp16: the waves' K staging tiles (16 rows of head_dim halves each), which the
     // combine reuses; quantized: region 0 (combine or K tiles), a 512-byte K-scale slot
@@ -306,7 +323,7 @@ int units_params(const kvq_decode_args* args, int32_t units, float* o_part, floa
     if (st != KVQ_OK) return st;
     if (!o_part || !lse) return KVQ_ERR_NULL_POINTER;
     if (args->batch > kvq::kUnitMaxBatch) return KVQ_ERR_UNSUPPORTED;
-    if (units < 1 || int64_t(units) * args->kv_heads > INT32_MAX ||
+    if (units < 1 || int64_t(units) * grid_heads(args) > INT32_MAX ||
         int64_t(units) + args->batch > INT32_MAX)
         return KVQ_ERR_SPLITS;
     *waves = args->waves_per_group == 0 ? 2 : args->waves_per_group;
@@ -327,6 +344,11 @@ extern "C" {
 const char* kvq_version(void) { return "kvq 0.1.0 gfx950"; }
 
 int kvq_cache_format_version(void) { return KVQ_CACHE_FORMAT_VERSION; }
+
+int kvq_head_blocks(int32_t q_heads, int32_t kv_heads) {
+    if (q_heads < 1 || kv_heads < 1 || q_heads % kv_heads != 0) return KVQ_ERR_SHAPE;
+    return head_blocks(q_heads, kv_heads);
+}
 
 const char* kvq_status_string(int status) {
     switch (status) {
@@ -444,7 +466,7 @@ int kvq_decode_split(const kvq_decode_args* args, int32_t num_splits, int32_t pa
     if (!o_part || !lse) return KVQ_ERR_NULL_POINTER;
     if (num_splits < 1 || pages_per_split < 1 || num_splits > 65535) return KVQ_ERR_SPLITS;
     // the 1-D decode grid: kv_heads * (splits * batch rounded up to a multiple of 8)
-    if ((int64_t(num_splits) * args->batch + 7) / 8 * 8 * args->kv_heads > INT32_MAX)
+    if ((int64_t(num_splits) * args->batch + 7) / 8 * 8 * grid_heads(args) > INT32_MAX)
         return KVQ_ERR_UNSUPPORTED;
     if (int64_t(num_splits) * pages_per_split < args->max_blocks) return KVQ_ERR_SPLITS;
     const int waves = pick_waves(args, pages_per_split);
@@ -475,7 +497,7 @@ int kvq_decode_merge(const float* o_part, const float* lse, void* out, int64_t o
 int kvq_decode_single(const kvq_decode_args* args, kvq_stream_t stream) {
     int st = check_decode_args(args, true);
     if (st != KVQ_OK) return st;
-    if ((int64_t(args->batch) + 7) / 8 * 8 * args->kv_heads > INT32_MAX) return KVQ_ERR_UNSUPPORTED;
+    if ((int64_t(args->batch) + 7) / 8 * 8 * grid_heads(args) > INT32_MAX) return KVQ_ERR_UNSUPPORTED;
     const int waves = pick_waves(args, args->max_blocks);
     const int pipe = pick_pipeline(args);
     if (waves == 0 || pipe == 0) return KVQ_ERR_UNSUPPORTED;

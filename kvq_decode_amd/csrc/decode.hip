@@ -104,9 +104,9 @@ __device__ __forceinline__ typename HalfVec<DV>::type load_vrow(__amdgpu_buffer_
     }
 }
 
-// Loads chunk c (16 tokens of kv head kvh) from physical block `phys` through buffer
-// resources at the chunk's first row (64-bit scalar address math once per chunk, 32-bit
-// lane offsets).
+// Loads chunk c (16 tokens of the caches' kv head kvh) from physical block `phys` through
+// buffer resources at the chunk's first row (64-bit scalar address math once per chunk,
+// 32-bit lane offsets).
 template <int D>
 __device__ __forceinline__ void load_chunk_f16(const DecodeParams& p, int kvh, int c,
                                                const F16LaneOff<D>& lo, int phys,
@@ -217,6 +217,7 @@ __device__ __forceinline__ void f16_range(const DecodeParams& p, int kvh, int b,
     const int G = p.group;
     const bool head_ok = i16 < G;
     const int c_full = seq_len >> 4;  // chunks below this index are fully valid
+    const int kvc = cache_head(p, kvh);
 
     // Q^T operand: lane (head i16, g) holds Q[head][32*k + 8*g + 0..7]; padded heads = 0.
     h8 qop[NST];
@@ -253,7 +254,7 @@ __device__ __forceinline__ void f16_range(const DecodeParams& p, int kvh, int b,
         // ring's waits (vmcnt counts the loads issued after the awaited one) drain it.
 #pragma unroll
         for (int i = 0; i < P; ++i) {
-            load_chunk_f16<D>(p, kvh, min(w_lo + i, last), lo,
+            load_chunk_f16<D>(p, kvc, min(w_lo + i, last), lo,
                               __builtin_amdgcn_readlane(pg_cur, i), ring[i]);
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -263,7 +264,7 @@ __device__ __forceinline__ void f16_range(const DecodeParams& p, int kvh, int b,
 #pragma unroll
             for (int i = 0; i < P; ++i) {
                 if (c0 + i < r_hi) chunk_f16<D, false>(ring[i], qop, sl2, 16, g, kst, st);
-                load_chunk_f16<D>(p, kvh, min(c0 + i + P, last), lo,
+                load_chunk_f16<D>(p, kvc, min(c0 + i + P, last), lo,
                                   __builtin_amdgcn_readlane(pg_cur, i), ring[i]);
             }
         }
@@ -273,7 +274,7 @@ __device__ __forceinline__ void f16_range(const DecodeParams& p, int kvh, int b,
         const int valid = seq_len - (c << 4);
         const int pg = chunk_pages<1>(p, b, c, c, 0);
         ChunkF16<D> ch;
-        load_chunk_f16<D>(p, kvh, c, f16_lane_offsets<D>(p, i16, g, valid - 1),
+        load_chunk_f16<D>(p, kvc, c, f16_lane_offsets<D>(p, i16, g, valid - 1),
                           __builtin_amdgcn_readlane(pg, 0), ch);
         chunk_f16<D, true>(ch, qop, sl2, valid, g, kst, st);
     }

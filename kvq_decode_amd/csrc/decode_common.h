@@ -81,6 +81,11 @@ __device__ __forceinline__ uint64_t block_offset(int phys, int64_t stride) {
     return (uint64_t)(uint32_t)phys * (uint32_t)stride;
 }
 
+// The caches' kv head that the kernels' kv head `kvh` reads (DecodeParams::kv_rep).
+__device__ __forceinline__ int cache_head(const DecodeParams& p, int kvh) {
+    return p.kv_rep == 1 ? kvh : kvh / p.kv_rep;
+}
+
 // XCD-aware workgroup order. MI355X dispatches the workgroups of a launch to its 8 XCDs
 // round-robin by linear id, and each XCD has its own L2. The decode kernels run a 1-D grid
 // and map its ids to (kv head, split, sequence) units (U = splits * batch of them) in one

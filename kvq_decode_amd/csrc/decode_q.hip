@@ -258,7 +258,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const char* base, i
         const_cast<char*>(base + (uint64_t)(uint32_t)phys * blk_bytes), (short)0, -1, 0x00020000);
 }
 
+// kvh: the caches' kv head (cache_head).
 __device__ __forceinline__ QBase q_base(const DecodeParams& p, int kvh) {
+    const int hkv = p.kv_heads / p.kv_rep;  // the caches' kv heads
     QBase B;
     B.k = (const char*)p.k + (int64_t)kvh * p.k_sh;
     B.v = (const char*)p.v + (int64_t)kvh * p.v_sh;
@@ -268,8 +270,8 @@ __device__ __forceinline__ QBase q_base(const DecodeParams& p, int kvh) {
     B.v_sblk = (uint32_t)p.v_sblk;
     B.k_stok = (uint32_t)p.k_stok;
     B.v_stok = (uint32_t)p.v_stok;
-    B.vs_blk = (uint32_t)(p.kv_heads * 4 * p.block_size);
-    B.ks_blk = (uint32_t)(p.kv_heads * 4 * 128);
+    B.vs_blk = (uint32_t)(hkv * 4 * p.block_size);
+    B.ks_blk = (uint32_t)(hkv * 4 * 128);
     B.cmask = (1u << p.cpp_shift) - 1;
     return B;
 }
@@ -674,7 +676,7 @@ __device__ __forceinline__ void q_range(const DecodeParams& p, int kvh, int b, i
     const int G = p.group;
     const int c_full = seq_len >> 4;  // chunks below this index are fully valid
     const int kgs = p.k_group_shift;  // log2 of 16-token chunks per K group
-    const QBase base = q_base(p, kvh);
+    const QBase base = q_base(p, cache_head(p, kvh));
 
     // LDS: [region 0][K-scale slots, 512 B per wave][q, 4 KB] (launch_q). Region 0 holds
     // the cross-wave combine after the chunk loop and, before it, the waves' staging tiles
@@ -803,7 +805,7 @@ __device__ __forceinline__ void q2_range(const DecodeParams& p, int kvh, int b, 
     const bool lo_part = i16 >= 8;     // the column holds the lo parts
     const int c_full = seq_len >> 4;
     const int kgs = p.k_group_shift;
-    const QBase base = q_base(p, kvh);
+    const QBase base = q_base(p, cache_head(p, kvh));
 
     extern __shared__ float smem[];
     const int r0 = quant_lds_region0(W, G, FMT);

@@ -38,6 +38,9 @@ struct DecodeParams {
     float scale_log2;        // softmax scale * log2(e)
     int32_t xcd_group;       // workgroup order (decode_common.h wg_coord): 0 plain, 1 grouped
     int32_t units;           // work units per kv head (decode_common.h UnitSpace); 0 = splits
+    int32_t kv_rep;          // q-head blocks per cache kv head (more than 16 q heads per kv
+                             // head): the kernels' kv head v (kv_heads of them, `group` q
+                             // heads each) reads the caches' kv head v / kv_rep; 1 otherwise
 };
 
 // Launches the decode kernel for the format/head_dim in `fmt`/`head_dim`. `final_out`

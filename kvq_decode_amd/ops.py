@@ -59,6 +59,15 @@ def choose_num_splits(batch: int, kv_heads: int, block_size: int, max_pages: int
 
 
 @functools.lru_cache(maxsize=4096)  # a pure function of its arguments; saves a C call per op
+def head_blocks(q_heads: int, kv_heads: int) -> int:
+    """q-head blocks per kv head (kvq_head_blocks): a group of more than 16 q heads per kv
+    head runs as k blocks of q_heads / (kv_heads * k) heads, each reading the caches; the
+    plans below take kv_heads * k kv heads."""
+    k = _lib.lib().kvq_head_blocks(q_heads, kv_heads)
+    _require(k >= 1, "q heads must be a multiple of kv heads")
+    return k
+
+
 def plan_decode(batch: int, kv_heads: int, block_size: int, max_pages: int,
                 cu_count: int, kv_format: str = "fp16") -> Tuple[int, int]:
     """(num_splits, waves_per_group) for the MI355X kernels when num_splits is None: the
@@ -130,10 +139,11 @@ def plan_workspace_shapes(batch: int, q_heads: int, kv_heads: int, head_dim: int
     sizes (work units or splits, as `plan_units` / `plan_decode` choose), or None when
     the plan runs a single pass and needs none. For callers that preallocate, e.g. before
     a graph capture."""
-    units, _ = plan_units(batch, kv_heads, block_size, max_pages, cu_count, kv_format)
+    grid_heads = kv_heads * head_blocks(q_heads, kv_heads)
+    units, _ = plan_units(batch, grid_heads, block_size, max_pages, cu_count, kv_format)
     if units:
         return units_workspace_shapes(batch, q_heads, head_dim, units)
-    splits, _ = plan_decode(batch, kv_heads, block_size, max_pages, cu_count, kv_format)
+    splits, _ = plan_decode(batch, grid_heads, block_size, max_pages, cu_count, kv_format)
     splits = normalize_splits(splits, max_pages)[0]
     return None if splits == 1 else workspace_shapes(batch, q_heads, head_dim, splits)
 
@@ -282,8 +292,9 @@ def paged_decode_attention(
                  "out must be float16 [B, Hq, D] with a contiguous last dim")
 
     max_pages = block_table.shape[1]
+    grid_heads = Hkv * head_blocks(Hq, Hkv)  # the plans count the kernels' kv heads
     if num_splits is None and units == 0:
-        units, planned_waves = plan_units(B, Hkv, block_size, max_pages,
+        units, planned_waves = plan_units(B, grid_heads, block_size, max_pages,
                                           _sm_count(dev.index or 0), kv_format)
         if units > 0 and waves_per_group == 0:
             waves_per_group = planned_waves
@@ -306,7 +317,7 @@ def paged_decode_attention(
                                                lse.data_ptr(), _stream(dev)))
         return out
     if num_splits is None:
-        splits, planned_waves = plan_decode(B, Hkv, block_size, max_pages,
+        splits, planned_waves = plan_decode(B, grid_heads, block_size, max_pages,
                                             _sm_count(dev.index or 0), kv_format)
         if waves_per_group == 0:
             waves_per_group = planned_waves

@@ -83,6 +83,32 @@ def test_cache_format_version():
     assert m and int(m.group(1)) == cache_format_version() == CACHE_FORMAT_VERSION
 
 
+@pytest.mark.parametrize("q_heads,kv_heads,blocks", [
+    (32, 8, 1), (128, 8, 1), (16, 1, 1),   # up to 16 q heads per kv head: one block
+    (32, 1, 2), (48, 2, 2), (40, 2, 2),     # 32, 24, 20 -> blocks of 16, 12, 10
+    (48, 1, 3), (34, 1, 17), (71, 1, 71),   # 48 -> 16; 34 = 2 x 17 -> 2; 71 prime -> 1
+    (64, 1, 4), (256, 2, 8),
+])
+def test_head_blocks(q_heads, kv_heads, blocks):
+    """A group G > 16 runs as k blocks of G / k q heads, k the smallest divisor of G with
+    G / k <= 16 (checked here against a brute-force search)."""
+    G = q_heads // kv_heads
+    want = min(k for k in range(1, G + 1) if G % k == 0 and G // k <= 16)
+    assert want == blocks
+    assert _lib.lib().kvq_head_blocks(q_heads, kv_heads) == blocks
+    from kvq_decode_amd import head_blocks
+    assert head_blocks(q_heads, kv_heads) == blocks
+
+
+def test_head_blocks_rejects_and_grid_limit():
+    L = _lib.lib()
+    for qh, kvh in ((30, 8), (0, 1), (8, 0), (4, 8)):
+        assert L.kvq_head_blocks(qh, kvh) == _lib.KVQ_ERR_SHAPE
+    a = good_args()
+    a.q_heads, a.kv_heads = 71 * 1000, 1000  # 71 blocks per kv head: 71000 grid kv heads
+    assert L.kvq_decode_single(ctypes.byref(a), None) == _lib.KVQ_ERR_UNSUPPORTED
+
+
 def test_choose_num_splits_known_answers():
     """The reference's own recorded auto split counts (results/*.json, A100 108 SMs and
     T4 40 SMs, block_size 32) from its heuristic (triton_fp16.py:175-180)."""
@@ -209,7 +235,6 @@ BAD_CASES = [
     ("head_dim", 96, _lib.KVQ_ERR_SHAPE),          # not a power of two (reference asserts too)
     ("head_dim", 512, _lib.KVQ_ERR_UNSUPPORTED),   # valid for the reference, not built here
     ("block_size", 8, _lib.KVQ_ERR_SHAPE),
-    ("q_heads", 8 * 32, _lib.KVQ_ERR_UNSUPPORTED),  # group 32 > 16
     ("kv_format", 9, _lib.KVQ_ERR_FORMAT),
     ("kv_format", 1, _lib.KVQ_ERR_FORMAT),          # quantized without scale tensors
     ("q", (1 << 40) + 8, _lib.KVQ_ERR_ALIGNMENT),
