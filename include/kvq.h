@@ -61,11 +61,15 @@ typedef enum kvq_status {
  *                                               channel), z = min, s = (max-min)/15
  *   k_scale, k_zero  fp16 [nb, Hkv, D]: group g of sequence b lives in block
  *                    block_table[b][g * k_group / block_size]
- *   v_scale, v_zero  fp16 [nb, Hkv, block_size]: one pair per token slot
+ *   v_scale, v_zero  fp16 [nb, Hkv, VG], VG = max(block_size, 32): the pairs of tokens
+ *                    [j * VG, (j + 1) * VG) of sequence b live in block
+ *                    block_table[b][j * VG / block_size], token t at index t % VG (with
+ *                    16-token pages, a page pair's 32 pairs of one kv head fill one
+ *                    128-byte line; other blocks' entries are unused)
  * Scale and zero are stored interleaved: one fp16 [nb, Hkv, D, 2] (K) and one
- * [nb, Hkv, block_size, 2] (V) tensor of (scale, zero) pairs, so that a decode loads both
- * of a token (V) or a channel (K) with one access. k_scale / v_scale point at element 0
- * of that tensor and k_zero / v_zero one element (2 bytes) after it.                  */
+ * [nb, Hkv, VG, 2] (V) tensor of (scale, zero) pairs, so that a decode loads both of a
+ * token (V) or a channel (K) with one access. k_scale / v_scale point at element 0 of that
+ * tensor and k_zero / v_zero one element (2 bytes) after it.                           */
 typedef enum kvq_kv_format {
     KVQ_KV_F16 = 0,
     KVQ_KV_INT8 = 1,
@@ -77,7 +81,7 @@ typedef enum kvq_kv_format {
  * the interleaved (scale, zero) pairs, the K group's pairs in the group's first block, the
  * quantization formulas (kvq_quantize_cache) and their rounding. A cache written under
  * one version is read correctly only by libraries reporting the same version. */
-#define KVQ_CACHE_FORMAT_VERSION 1
+#define KVQ_CACHE_FORMAT_VERSION 2
 
 /* KVQ_CACHE_FORMAT_VERSION of the loaded library (no reference counterpart). */
 int kvq_cache_format_version(void);
@@ -103,7 +107,8 @@ typedef struct kvq_decode_args {
     int32_t k_group;          /* tokens per K scale group (quantized formats; 128) */
     const void* k_scale;      /* fp16 (scale, zero) pairs [num_blocks, kv_heads, head_dim, 2] */
     const void* k_zero;       /* = k_scale + 2 bytes */
-    const void* v_scale;      /* fp16 (scale, zero) pairs [num_blocks, kv_heads, block_size, 2] */
+    const void* v_scale;      /* fp16 (scale, zero) pairs [num_blocks, kv_heads, VG, 2], VG =
+                                 max(block_size, 32) */
     const void* v_zero;       /* = v_scale + 2 bytes */
     int32_t waves_per_group;  /* tuning: waves per (kv head, split) workgroup, one of
                                  1, 2, 4, 8, 16; 0 = the library's choice */
@@ -235,8 +240,9 @@ int kvq_decode_units_merge(const kvq_decode_args* args, int32_t units, const flo
  * block) and V scales/zeros per token. Slots past a sequence's length are not written;
  * seq_lens[b] is limited to the max_blocks * block_size slots its table row addresses.
  * A token whose block-table entry lies outside [0, num_blocks) is neither read nor
- * written (it does not enter its K group's min / max), and a K group whose first page
- * lies outside the pool (where its (scale, zero) pairs would go) writes nothing.
+ * written (it does not enter its K group's min / max), a K group whose first page lies
+ * outside the pool (where its (scale, zero) pairs would go) writes nothing, and a token
+ * whose V group's first page lies outside the pool gets no V codes or pair.
  * k_src/v_src: fp16 caches with the given element strides (args->k_cache / v_cache are
  * the destination code caches, args->kv_format the target format); 16-byte aligned, with
  * strides that are multiples of 8 elements (KVQ_ERR_ALIGNMENT otherwise): each lane
@@ -254,8 +260,8 @@ int kvq_quantize_cache(const kvq_decode_args* args, const void* k_src, const voi
  * args->seq_lens must already count the new token. A sequence whose seq_lens[b] is below
  * 1 or above max_blocks * block_size writes nothing (codes, pairs and residual), and a
  * row whose block-table entry lies outside [0, num_blocks) is not written (a K group
- * whose first page lies outside the pool writes nothing), as kvq_append_kv skips such
- * slots. k_new, v_new and k_resid are contiguous and 16-byte aligned (KVQ_ERR_ALIGNMENT
+ * whose first page lies outside the pool writes nothing, nor does a V row whose V group's
+ * first page does), as kvq_append_kv skips such slots. k_new, v_new and k_resid are contiguous and 16-byte aligned (KVQ_ERR_ALIGNMENT
  * otherwise). */
 int kvq_quantize_append(const kvq_decode_args* args, const void* k_new, const void* v_new,
                         void* k_resid, kvq_stream_t stream);

@@ -154,6 +154,7 @@ kvq::DecodeParams make_params(const kvq_decode_args* a) {
     p.max_blocks = a->max_blocks;
     p.num_blocks = a->num_blocks;
     p.cpp_shift = ilog2(a->block_size / 16);
+    p.vg_shift = ilog2(a->block_size) > 5 ? ilog2(a->block_size) : 5;
     p.k_group_chunks = a->kv_format == KVQ_KV_F16 ? 0 : a->k_group / 16;
     p.k_group_shift = a->kv_format == KVQ_KV_F16 ? 0 : ilog2(a->k_group / 16);
     p.k_group_pages = a->kv_format == KVQ_KV_F16 ? 0 : a->k_group / a->block_size;
@@ -262,6 +263,7 @@ kvq::QuantParams make_quant_params(const kvq_decode_args* a) {
     p.num_blocks = a->num_blocks;
     p.k_group = a->k_group;
     p.bs_shift = ilog2(a->block_size);
+    p.vg_shift = p.bs_shift > 5 ? p.bs_shift : 5;
     p.max_groups = cdiv(int64_t(a->max_blocks) * a->block_size, a->k_group);
     return p;
 }

@@ -248,8 +248,8 @@ __device__ __forceinline__ void f16_range(const DecodeParams& p, int kvh, int b,
         const F16LaneOff<D> lo = f16_lane_offsets<D>(p, i16, g, 15);
         const int last = r_hi - 1;
         ChunkF16<D> ring[P];
-        int pg_cur = chunk_pages<P>(p, b, w_lo, last, 0);
-        int pg_nxt = chunk_pages<P>(p, b, w_lo + P, last, 0);
+        int pg_cur = chunk_pages<P>(p, b, w_lo, last, 0, 0);
+        int pg_nxt = chunk_pages<P>(p, b, w_lo + P, last, 0, 0);
         // Issued slot by slot: a slot's loads moved behind a later slot's would make the
         // ring's waits (vmcnt counts the loads issued after the awaited one) drain it.
 #pragma unroll
@@ -260,7 +260,7 @@ __device__ __forceinline__ void f16_range(const DecodeParams& p, int kvh, int b,
         }
         for (int c0 = w_lo; c0 < r_hi; c0 += P) {
             pg_cur = pg_nxt;  // pages of chunks c0 + P .. c0 + 2P - 1
-            pg_nxt = chunk_pages<P>(p, b, c0 + 2 * P, last, 0);
+            pg_nxt = chunk_pages<P>(p, b, c0 + 2 * P, last, 0, 0);
 #pragma unroll
             for (int i = 0; i < P; ++i) {
                 if (c0 + i < r_hi) chunk_f16<D, false>(ring[i], qop, sl2, 16, g, kst, st);
@@ -272,7 +272,7 @@ __device__ __forceinline__ void f16_range(const DecodeParams& p, int kvh, int b,
     if (w_lo <= r_hi && r_hi < w_hi) {  // this wave owns the partial last chunk c_full
         const int c = r_hi;
         const int valid = seq_len - (c << 4);
-        const int pg = chunk_pages<1>(p, b, c, c, 0);
+        const int pg = chunk_pages<1>(p, b, c, c, 0, 0);
         ChunkF16<D> ch;
         load_chunk_f16<D>(p, kvc, c, f16_lane_offsets<D>(p, i16, g, valid - 1),
                           __builtin_amdgcn_readlane(pg, 0), ch);

@@ -52,16 +52,22 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // result is unchanged; the common chunk needs no cross-lane max and no rescale.
 constexpr float kLazyMax = 8.0f;
 
-// Physical blocks of the P chunks c .. c + P - 1 (lane j < P) and of the first pages of
-// their K groups (lane P + j), chunks clamped to `last` so the load is issued on every
-// path. Used one ring ahead: the compiler's wait for this register then counts the
-// chunk loads issued since, and never drains the loads in flight.
+// Physical blocks of the P chunks c .. c + P - 1 (lane j < P), of the first pages of
+// their K groups (lane P + j, groups of 2^gshift chunks) and of the first pages of their
+// V (scale, zero) groups (lane 2P + j, 2^vshift chunks), chunks clamped to `last` so the
+// load is issued on every path. Used one ring ahead: the compiler's wait for this
+// register then counts the chunk loads issued since, and never drains the loads in flight.
 template <int P>
 __device__ __forceinline__ int chunk_pages(const DecodeParams& p, int b, int c, int last,
-                                           int gshift) {
-    const int j = __lane_id() & (2 * P - 1);
+                                           int gshift, int vshift) {
+    static_assert(4 * P <= 64, "three lane regions of P chunks in one wave");
+    const int j = __lane_id() & (4 * P - 1);
     int cj = min(c + (j & (P - 1)), last);
-    if (j >= P) cj = (cj >> gshift) << gshift;
+    if (j >= 2 * P) {
+        cj = (cj >> vshift) << vshift;
+    } else if (j >= P) {
+        cj = (cj >> gshift) << gshift;
+    }
     const int phys = p.bt[(int64_t)b * p.bt_sb + (cj >> p.cpp_shift)];
     return min(max(phys, 0), p.num_blocks - 1);
 }

@@ -179,10 +179,11 @@ struct QFmt<KVQ_KV_INT4> {
     }
 };
 
-// Raw codes of one 16-token chunk as held by one lane, the (scale, zero) pair of token
+// Raw codes of one 16-token chunk as held by one lane, the V (scale, zero) pair of token
 // 4g + (l & 3) (vsz, scale in the low half; pv_weights gives every lane of the quad the
-// pairs of all 4 of its tokens 4g .. 4g + 3), and (lane l) the pairs of channels 2l, 2l+1 of
-// the chunk's K group (ksz). The group data is loaded with every chunk that
+// pairs of all 4 of its tokens 4g .. 4g + 3; for the first chunk of a chunk pair, of the
+// chunk the lane's column holds), and (lane l) the pairs of channels 2l, 2l+1 of the
+// chunk's K group (ksz). The group data is loaded with every chunk that
 // may start a group's use, not only with a group's first one: loads issued on every path
 // keep the compiler's wait counts exact, so no chunk waits for loads it does not use.
 template <int FMT>
@@ -203,10 +204,11 @@ struct ChunkQ {
 //   V, the same whole-row pattern: INT4 row min(l/4, last) bytes [16(l%4), +16); INT8 /
 //     FP8 load j row min(8j + l/8, last) bytes [16(l%8), +16) (regrouped by vstage_*);
 //   the V (scale, zero) pair of token 4g + (l & 3) (4 bytes: the 64 bytes of the chunk's
-//   16 pairs reach the wave once per row of 16 lanes, not once per lane), and the K group's
-//   pairs of channels 2l, 2l+1 (8 bytes).
+//   16 pairs reach the wave once per row of 16 lanes, not once per lane), vs2 the same
+//   token of the chunk pair's chunk (l >> 2) & 1, 64 bytes further for the second chunk,
+//   and the K group's pairs of channels 2l, 2l+1 (8 bytes).
 struct QLaneOff {
-    uint32_t k[2], v[2], vs, ks;
+    uint32_t k[2], v[2], vs, vs2, ks;
 };
 
 template <int FMT>
@@ -230,6 +232,7 @@ __device__ __forceinline__ QLaneOff lane_offsets(const DecodeParams& p, int i16,
             o.v[j] = (uint32_t)(min(8 * j + (lane >> 3), last) * (int)p.v_stok + 16 * (lane & 7));
     }
     o.vs = 16 * g + 4 * (lane & 3);
+    o.vs2 = o.vs + 64 * ((lane >> 2) & 1);
     o.ks = 8 * lane;
     return o;
 }
@@ -248,6 +251,7 @@ struct QBase {
     uint32_t k_sblk, v_sblk, k_stok, v_stok;
     uint32_t vs_blk, ks_blk;  // bytes per block of the V / K pair tensors
     uint32_t cmask;           // 16-token chunks per page - 1
+    uint32_t vmask;           // 16-token chunks per V (scale, zero) group - 1
 };
 
 // Buffer resource at a wave-uniform address: stride 0, the full 32-bit range (offsets from
@@ -264,15 +268,16 @@ __device__ __forceinline__ QBase q_base(const DecodeParams& p, int kvh) {
     QBase B;
     B.k = (const char*)p.k + (int64_t)kvh * p.k_sh;
     B.v = (const char*)p.v + (int64_t)kvh * p.v_sh;
-    B.vs = (const char*)p.v_scale + (int64_t)kvh * 4 * p.block_size;
+    B.vs = (const char*)p.v_scale + ((int64_t)kvh * 4 << p.vg_shift);
     B.ks = (const char*)p.k_scale + (int64_t)kvh * 4 * 128;
     B.k_sblk = (uint32_t)p.k_sblk;
     B.v_sblk = (uint32_t)p.v_sblk;
     B.k_stok = (uint32_t)p.k_stok;
     B.v_stok = (uint32_t)p.v_stok;
-    B.vs_blk = (uint32_t)(hkv * 4 * p.block_size);
+    B.vs_blk = (uint32_t)(hkv * 4) << p.vg_shift;
     B.ks_blk = (uint32_t)(hkv * 4 * 128);
     B.cmask = (1u << p.cpp_shift) - 1;
+    B.vmask = (1u << (p.vg_shift - 4)) - 1;
     return B;
 }
 
@@ -282,10 +287,13 @@ __device__ __forceinline__ QBase q_base(const DecodeParams& p, int kvh) {
 // policy.
 constexpr int kNT = 2;
 
-// WITH_K: also load the K group's (scale, zero) pairs (ch.ksz).
-template <int FMT, bool WITH_K = true>
+// WITH_K: also load the K group's (scale, zero) pairs (ch.ksz), stored with the group's
+// first page `lead`. VS: the V (scale, zero) pairs ch.vsz brings, from the chunk's V group
+// in its first page `vlead`: 1 the chunk's own; 2 those of the chunk pair c, c + 1 (c even,
+// both in one V group: lane l takes chunk c + ((l >> 2) & 1)); 0 none.
+template <int FMT, bool WITH_K = true, int VS = 1>
 __device__ __forceinline__ void load_chunk_q(const QBase& B, int c, const QLaneOff& lo, int phys,
-                                             int lead, ChunkQ<FMT>& ch) {
+                                             int lead, int vlead, ChunkQ<FMT>& ch) {
     typedef QFmt<FMT> Q;
     const uint32_t slot = ((uint32_t)c & B.cmask) << 4;
     const auto rk = block_rsrc(B.k, phys, B.k_sblk);
@@ -296,11 +304,14 @@ __device__ __forceinline__ void load_chunk_q(const QBase& B, int c, const QLaneO
 #pragma unroll
     for (int j = 0; j < Q::VLOADS; ++j)
         ch.vr[j] = __builtin_amdgcn_raw_buffer_load_b128(rv, lo.v[j], slot * B.v_stok, kNT);
-    // V (scale, zero) pair of token slot + 4g + (l & 3) (slots past the sequence hold
-    // garbage and are masked by selects, never multiplied)
-    ch.vsz = __builtin_amdgcn_raw_buffer_load_b32(block_rsrc(B.vs, phys, B.vs_blk), lo.vs,
-                                                  4 * slot, kNT);
-    // K group (scale, zero) pairs, stored with the group's first page `lead`
+    // V (scale, zero) pair of token 4g + (l & 3) of the chunk (slots past the sequence
+    // hold garbage and are masked by selects, never multiplied); the chunk's 16 pairs sit
+    // at 64 (c & vmask) bytes in its V group
+    if constexpr (VS != 0)
+        ch.vsz = __builtin_amdgcn_raw_buffer_load_b32(block_rsrc(B.vs, vlead, B.vs_blk),
+                                                      VS == 2 ? lo.vs2 : lo.vs,
+                                                      64 * ((uint32_t)c & B.vmask & ~(VS == 2 ? 1u : 0u)),
+                                                      kNT);
     if constexpr (WITH_K) {
         ch.ksz = __builtin_bit_cast(
             u2, __builtin_amdgcn_raw_buffer_load_b64(block_rsrc(B.ks, lead, B.ks_blk), lo.ks, 0, 0));
@@ -608,7 +619,7 @@ __device__ __forceinline__ void chunk_pair(const ChunkQ<FMT>& ca, const ChunkQ<F
     }
     float pr[4];
     softmax_step(s2, st, corr, pr);
-    const uint32_t vsz = slot ? cb.vsz : ca.vsz;  // slot is uniform over each quad
+    const uint32_t vsz = ca.vsz;  // the pairs of the lane's own chunk (load_chunk_q VS 2)
     h4 phi, plo;
     pv_weights<MASK>(pr, vsz, valid, g, phi, plo, corr);
     // B operand: k-slots 8g + r (chunk a's token 4g + r) and 8g + 4 + r (chunk b's); the
@@ -676,6 +687,7 @@ __device__ __forceinline__ void q_range(const DecodeParams& p, int kvh, int b, i
     const int G = p.group;
     const int c_full = seq_len >> 4;  // chunks below this index are fully valid
     const int kgs = p.k_group_shift;  // log2 of 16-token chunks per K group
+    const int vgs = p.vg_shift - 4;   // log2 of 16-token chunks per V (scale, zero) group
     const QBase base = q_base(p, cache_head(p, kvh));
 
     // LDS: [region 0][K-scale slots, 512 B per wave][q, 4 KB] (launch_q). Region 0 holds
@@ -725,20 +737,21 @@ __device__ __forceinline__ void q_range(const DecodeParams& p, int kvh, int b, i
         const QLaneOff lo = lane_offsets<FMT>(p, i16, g, 15);
         const int last = r_hi - 1;
         ChunkQ<FMT> ring[P];
-        int pg_cur = chunk_pages<P>(p, b, w_lo, last, kgs);
-        int pg_nxt = chunk_pages<P>(p, b, w_lo + P, last, kgs);
+        int pg_cur = chunk_pages<P>(p, b, w_lo, last, kgs, vgs);
+        int pg_nxt = chunk_pages<P>(p, b, w_lo + P, last, kgs, vgs);
         // Issued slot by slot: a slot's loads moved behind a later slot's would make the
         // ring's waits (vmcnt counts the loads issued after the awaited one) drain it.
 #pragma unroll
         for (int i = 0; i < P; ++i) {
             load_chunk_q<FMT>(base, min(w_lo + i, last), lo,
                               __builtin_amdgcn_readlane(pg_cur, i),
-                              __builtin_amdgcn_readlane(pg_cur, P + i), ring[i]);
+                              __builtin_amdgcn_readlane(pg_cur, P + i),
+                              __builtin_amdgcn_readlane(pg_cur, 2 * P + i), ring[i]);
             __builtin_amdgcn_sched_barrier(0);
         }
         for (int c0 = w_lo; c0 < r_hi; c0 += P) {
             pg_cur = pg_nxt;  // pages of chunks c0 + P .. c0 + 2P - 1
-            pg_nxt = chunk_pages<P>(p, b, c0 + 2 * P, last, kgs);
+            pg_nxt = chunk_pages<P>(p, b, c0 + 2 * P, last, kgs, vgs);
 #pragma unroll
             for (int i = 0; i < P; ++i) {
                 const int c = c0 + i;
@@ -748,17 +761,19 @@ __device__ __forceinline__ void q_range(const DecodeParams& p, int kvh, int b, i
                 }
                 load_chunk_q<FMT>(base, min(c + P, last), lo,
                                   __builtin_amdgcn_readlane(pg_cur, i),
-                                  __builtin_amdgcn_readlane(pg_cur, P + i), ring[i]);
+                                  __builtin_amdgcn_readlane(pg_cur, P + i),
+                                  __builtin_amdgcn_readlane(pg_cur, 2 * P + i), ring[i]);
             }
         }
     }
     if (w_lo <= r_hi && r_hi < w_hi) {  // this wave owns the partial last chunk c_full
         const int c = r_hi;
         const int valid = valid_of(c);
-        const int pg = chunk_pages<1>(p, b, c, c, kgs);
+        const int pg = chunk_pages<1>(p, b, c, c, kgs, vgs);
         ChunkQ<FMT> ch;
         load_chunk_q<FMT>(base, c, lane_offsets<FMT>(p, i16, g, valid - 1),
-                          __builtin_amdgcn_readlane(pg, 0), __builtin_amdgcn_readlane(pg, 1), ch);
+                          __builtin_amdgcn_readlane(pg, 0), __builtin_amdgcn_readlane(pg, 1),
+                          __builtin_amdgcn_readlane(pg, 2), ch);
         if (c == w_lo || (c & gmask) == 0) new_group(ch);
         chunk_q<FMT, true, SPLIT>(ch, qhi, qlo, csl, sl2f, valid, g, kst, st, corr);
     }
@@ -805,6 +820,7 @@ __device__ __forceinline__ void q2_range(const DecodeParams& p, int kvh, int b, 
     const bool lo_part = i16 >= 8;     // the column holds the lo parts
     const int c_full = seq_len >> 4;
     const int kgs = p.k_group_shift;
+    const int vgs = p.vg_shift - 4;
     const QBase base = q_base(p, cache_head(p, kvh));
 
     extern __shared__ float smem[];
@@ -834,10 +850,11 @@ __device__ __forceinline__ void q2_range(const DecodeParams& p, int kvh, int b, 
     };
     // chunk c alone (in the first chunk's columns), its first `valid` tokens
     auto single = [&](int c, int valid) {
-        const int pg = chunk_pages<1>(p, b, c, c, kgs);
+        const int pg = chunk_pages<1>(p, b, c, c, kgs, vgs);
         ChunkQ<FMT> ch;
         load_chunk_q<FMT>(base, c, lane_offsets<FMT>(p, i16, g, valid - 1),
-                          __builtin_amdgcn_readlane(pg, 0), __builtin_amdgcn_readlane(pg, 1), ch);
+                          __builtin_amdgcn_readlane(pg, 0), __builtin_amdgcn_readlane(pg, 1),
+                          __builtin_amdgcn_readlane(pg, 2), ch);
         group(ch, c >> kgs);
         chunk_pair<FMT, true>(ch, ch, qv, csl, sl2f, valid, 0, g, slot, lo_part, kst, st, corr);
     };
@@ -854,25 +871,26 @@ __device__ __forceinline__ void q2_range(const DecodeParams& p, int kvh, int b, 
         const QLaneOff lo = lane_offsets<FMT>(p, i16, g, 15);
         const int last = e_hi - 1;
         ChunkQ<FMT> ring[P];
-        int pg_cur = chunk_pages<P>(p, b, c_first, last, kgs);
-        int pg_nxt = chunk_pages<P>(p, b, c_first + P, last, kgs);
+        int pg_cur = chunk_pages<P>(p, b, c_first, last, kgs, vgs);
+        int pg_nxt = chunk_pages<P>(p, b, c_first + P, last, kgs, vgs);
         // Issued slot by slot: a slot's loads moved behind a later slot's would make the
         // ring's waits (vmcnt counts the loads issued after the awaited one) drain it.
         // a pair's K group is its first chunk's: odd slots skip the K pair load
 #pragma unroll
         for (int i = 0; i < P; ++i) {
             if (i % 2 == 0)
-                load_chunk_q<FMT, true>(base, min(c_first + i, last), lo,
-                                        __builtin_amdgcn_readlane(pg_cur, i),
-                                        __builtin_amdgcn_readlane(pg_cur, P + i), ring[i]);
+                load_chunk_q<FMT, true, 2>(base, min(c_first + i, last), lo,
+                                           __builtin_amdgcn_readlane(pg_cur, i),
+                                           __builtin_amdgcn_readlane(pg_cur, P + i),
+                                           __builtin_amdgcn_readlane(pg_cur, 2 * P + i), ring[i]);
             else
-                load_chunk_q<FMT, false>(base, min(c_first + i, last), lo,
-                                         __builtin_amdgcn_readlane(pg_cur, i), 0, ring[i]);
+                load_chunk_q<FMT, false, 0>(base, min(c_first + i, last), lo,
+                                            __builtin_amdgcn_readlane(pg_cur, i), 0, 0, ring[i]);
             __builtin_amdgcn_sched_barrier(0);
         }
         for (int c0 = c_first; c0 < e_hi; c0 += P) {
             pg_cur = pg_nxt;
-            pg_nxt = chunk_pages<P>(p, b, c0 + 2 * P, last, kgs);
+            pg_nxt = chunk_pages<P>(p, b, c0 + 2 * P, last, kgs, vgs);
 #pragma unroll
             for (int i = 0; i < P; i += 2) {
                 const int c = c0 + i;
@@ -881,11 +899,13 @@ __device__ __forceinline__ void q2_range(const DecodeParams& p, int kvh, int b, 
                     chunk_pair<FMT, false>(ring[i], ring[i + 1], qv, csl, sl2f, 16, 16, g, slot,
                                            lo_part, kst, st, corr);
                 }
-                load_chunk_q<FMT, true>(base, min(c0 + i + P, last), lo,
-                                        __builtin_amdgcn_readlane(pg_cur, i),
-                                        __builtin_amdgcn_readlane(pg_cur, P + i), ring[i]);
-                load_chunk_q<FMT, false>(base, min(c0 + i + 1 + P, last), lo,
-                                         __builtin_amdgcn_readlane(pg_cur, i + 1), 0, ring[i + 1]);
+                load_chunk_q<FMT, true, 2>(base, min(c0 + i + P, last), lo,
+                                           __builtin_amdgcn_readlane(pg_cur, i),
+                                           __builtin_amdgcn_readlane(pg_cur, P + i),
+                                           __builtin_amdgcn_readlane(pg_cur, 2 * P + i), ring[i]);
+                load_chunk_q<FMT, false, 0>(base, min(c0 + i + 1 + P, last), lo,
+                                            __builtin_amdgcn_readlane(pg_cur, i + 1), 0, 0,
+                                            ring[i + 1]);
             }
         }
     }

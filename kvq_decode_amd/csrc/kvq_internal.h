@@ -38,6 +38,7 @@ struct DecodeParams {
     float scale_log2;        // softmax scale * log2(e)
     int32_t xcd_group;       // workgroup order (decode_common.h wg_coord): 0 plain, 1 grouped
     int32_t units;           // work units per kv head (decode_common.h UnitSpace); 0 = splits
+    int32_t vg_shift;        // log2 of tokens per V (scale, zero) group, max(block_size, 32)
     int32_t kv_rep;          // q-head blocks per cache kv head (more than 16 q heads per kv
                              // head): the kernels' kv head v (kv_heads of them, `group` q
                              // heads each) reads the caches' kv head v / kv_rep; 1 otherwise
@@ -101,6 +102,7 @@ struct QuantParams {
     _Float16* k_resid;       // append only: [batch, kv_heads, k_group, head_dim]
     int32_t batch, kv_heads, head_dim, block_size, max_blocks, num_blocks, k_group;
     int32_t bs_shift;        // log2(block_size) (a power of two)
+    int32_t vg_shift;        // log2 of tokens per V (scale, zero) group, max(block_size, 32)
     int32_t max_groups;      // cdiv(max_blocks * block_size, k_group)
 };
 

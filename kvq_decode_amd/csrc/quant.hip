@@ -273,7 +273,9 @@ __device__ __forceinline__ void quant_k_group(const QuantParams& p, int kvh, int
 // V: one token row (D channels of one kv head) per D/8 lanes, each lane 8 channels (one
 // 16-byte load, one 4- or 8-byte code store). Bulk: workgroup = kVRows token rows of one
 // (kv head, sequence), 256 threads; append: the newest token, on the first D/8 lanes of
-// the append kernel's V workgroup.
+// the append kernel's V workgroup. The codes go to the token's page slot, its (scale,
+// zero) pair to index t % VG of its V group's first page (VG = 2^vg_shift tokens); a row
+// is written only when both pages lie in the pool.
 constexpr int kVRows = 64;
 
 template <int FMT, int D, bool APPEND>
@@ -284,7 +286,7 @@ __device__ __forceinline__ void quant_v_rows(const QuantParams& p, int kvh, int 
     const int n = APPEND ? append_len_of(p, b) : seq_len_of(p, b);
     // every pass's row is loaded first, so the workgroup waits on memory once. A row past
     // the sequence or in a page outside the pool is neither read nor written (tok = -1).
-    int tok[PASSES], phys[PASSES];
+    int tok[PASSES], phys[PASSES], vlead[PASSES];
     h8q row[PASSES];
 #pragma unroll
     for (int i = 0; i < PASSES; ++i) {
@@ -294,7 +296,8 @@ __device__ __forceinline__ void quant_v_rows(const QuantParams& p, int kvh, int 
             continue;
         }
         phys[i] = phys_of(p, b, tok[i] >> p.bs_shift);
-        if (phys[i] < 0) {
+        vlead[i] = phys_of(p, b, (tok[i] >> p.vg_shift) << (p.vg_shift - p.bs_shift));
+        if (phys[i] < 0 || vlead[i] < 0) {
             tok[i] = -1;
             continue;
         }
@@ -330,7 +333,8 @@ __device__ __forceinline__ void quant_v_rows(const QuantParams& p, int kvh, int 
                         (int64_t)kvh * p.v_sh,
                     c, code);
         if (c == 0) {
-            const int64_t sz = ((int64_t)phys[i] * p.kv_heads + kvh) * p.block_size + slot;
+            const int64_t sz = (((int64_t)vlead[i] * p.kv_heads + kvh) << p.vg_shift) +
+                               (tok[i] & ((1 << p.vg_shift) - 1));
             *(h2q*)(p.v_scale + 2 * sz) = h2q{(_Float16)q.s, (_Float16)q.z};
         }
     }

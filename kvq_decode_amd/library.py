@@ -8,7 +8,7 @@ them - append the new token, decode - can be captured in a HIP graph
 (`torch.cuda.CUDAGraph`) and replayed.
 
 Quantized caches pass their (scale, zero) storage as the interleaved pair tensors
-k_sz [num_blocks, Hkv, D, 2] and v_sz [num_blocks, Hkv, block_size, 2]
+k_sz [num_blocks, Hkv, D, 2] and v_sz [num_blocks, Hkv, max(block_size, 32), 2]
 (QuantizedKVCache.k_sz / .v_sz), one tensor each, so that every mutated buffer is a
 schema argument of its own.
 

@@ -32,6 +32,13 @@ MIN_TOKENS_PER_SPLIT = 512
 DEFAULT_K_GROUP = 128  # tokens per K scale group (reference roofline.py:50 group_size)
 
 
+def v_group_tokens(block_size: int) -> int:
+    """Tokens per V (scale, zero) group of a quantized cache, max(block_size, 32): the
+    pairs of a group live in its first page, so the 32 pairs of one kv head that a 128-byte
+    line holds belong to 32 consecutive tokens of one sequence (include/kvq.h)."""
+    return max(block_size, 32)
+
+
 class KvqArgumentError(AssertionError, ValueError):
     """A precondition the reference asserts (triton_fp16.py:195-201) does not hold.
     Subclasses AssertionError so callers written against the reference still catch it."""
@@ -258,7 +265,8 @@ def paged_decode_attention(
         _require(Dc == (D // 2 if kv_format == "int4" else D),
                  "code cache last dim must be head_dim (head_dim/2 for int4)")
         check_scale_pairs(k_scale, k_zero, (k_cache.shape[0], Hkv, D), "k")
-        check_scale_pairs(v_scale, v_zero, (k_cache.shape[0], Hkv, block_size), "v")
+        check_scale_pairs(v_scale, v_zero, (k_cache.shape[0], Hkv, v_group_tokens(block_size)),
+                          "v")
     else:
         _require(k_cache.dtype == v_cache.dtype == torch.float16,
                  "q, k_cache and v_cache must all be float16")

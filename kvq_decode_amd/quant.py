@@ -11,7 +11,9 @@ channel over groups of `k_group` tokens, values per token. Storage (include/kvq.
                       with 16-byte aligned rows are accepted
     k_scale, k_zero   fp16 [num_blocks, Hkv, D]  - group g of sequence b lives in block
                       block_table[b, g * k_group // block_size]
-    v_scale, v_zero   fp16 [num_blocks, Hkv, block_size]
+    v_scale, v_zero   fp16 [num_blocks, Hkv, VG], VG = max(block_size, 32) - the pairs of
+                      tokens [j * VG, (j + 1) * VG) of sequence b live in block
+                      block_table[b, j * VG // block_size], token t at index t % VG
                       both pairs are strided views of interleaved storage, one fp16
                       [..., 2] tensor of (scale, zero) per channel (K) / token (V): a
                       decode reads both of a token with one access
@@ -23,7 +25,8 @@ import torch
 
 from kvq_decode_amd import _lib
 from kvq_decode_amd._lib import KV_FORMATS, DecodeArgs
-from kvq_decode_amd.ops import DEFAULT_K_GROUP, KvqArgumentError, _require, check_scale_pairs
+from kvq_decode_amd.ops import (DEFAULT_K_GROUP, KvqArgumentError, _require, check_scale_pairs,
+                                v_group_tokens)
 
 QUANT_FORMATS = ("int8", "fp8_e4m3", "int4")
 
@@ -31,7 +34,7 @@ QUANT_FORMATS = ("int8", "fp8_e4m3", "int4")
 # The on-device format these caches follow (include/kvq.h KVQ_CACHE_FORMAT_VERSION); a
 # cache kept across processes should be stored with it and read back only by a library
 # reporting the same value (cache_format_version()).
-CACHE_FORMAT_VERSION = 1
+CACHE_FORMAT_VERSION = 2
 
 
 def cache_format_version() -> int:
@@ -61,7 +64,7 @@ class QuantizedKVCache(NamedTuple):
 
     @property
     def v_sz(self) -> torch.Tensor:
-        """The interleaved V (scale, zero) storage [num_blocks, Hkv, block_size, 2]."""
+        """The interleaved V (scale, zero) storage [num_blocks, Hkv, VG, 2]."""
         return _pairs(self.v_scale, self.v_zero, "v")
 
 
@@ -85,7 +88,8 @@ def allocate_quantized_cache(num_blocks: int, block_size: int, kv_heads: int, he
     kc = torch.empty(shape, dtype=torch.uint8, device=device).permute(0, 2, 1, 3)
     vc = torch.empty(shape, dtype=torch.uint8, device=device).permute(0, 2, 1, 3)
     ksz = torch.empty((num_blocks, kv_heads, head_dim, 2), dtype=torch.float16, device=device)
-    vsz = torch.empty((num_blocks, kv_heads, block_size, 2), dtype=torch.float16, device=device)
+    vsz = torch.empty((num_blocks, kv_heads, v_group_tokens(block_size), 2), dtype=torch.float16,
+                      device=device)
     return QuantizedKVCache(kc, vc, ksz[..., 0], ksz[..., 1], vsz[..., 0], vsz[..., 1],
                             kv_format, k_group)
 
@@ -129,7 +133,7 @@ def _check_cache(cache: QuantizedKVCache, block_table, seq_lens, head_dim):
     _require(dc == (head_dim // 2 if cache.kv_format == "int4" else head_dim),
              "code cache width does not match head_dim")
     check_scale_pairs(cache.k_scale, cache.k_zero, (nb, hkv, head_dim), "k")
-    check_scale_pairs(cache.v_scale, cache.v_zero, (nb, hkv, bs), "v")
+    check_scale_pairs(cache.v_scale, cache.v_zero, (nb, hkv, v_group_tokens(bs)), "v")
     _require(cache.k_group % bs == 0, "k_group must be a multiple of block_size")
     dev = cache.k_codes.device
     _require(dev.type == "cuda", "kvq runs on the GPU only (no CPU fallback)")

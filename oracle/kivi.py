@@ -28,7 +28,10 @@ Paged storage (this build's format, layout of the codes follows the fp16 cache):
   k_scale, k_zero  [num_blocks, Hkv, D] fp16: the scales of group g of sequence b are
             stored in physical block block_table[b, g * G // block_size] (the block that
             holds the group's first token); other blocks' entries are unused.
-  v_scale, v_zero  [num_blocks, Hkv, block_size] fp16, one pair per token slot.
+  v_scale, v_zero  [num_blocks, Hkv, VG] fp16, VG = max(block_size, 32) (v_group): the
+            pairs of tokens [j*VG, (j+1)*VG) of sequence b are stored in physical block
+            block_table[b, j*VG // block_size] (the block that holds the V group's first
+            token), token t at index t % VG; other blocks' entries are unused.
 """
 
 import numpy as np
@@ -39,6 +42,11 @@ F16 = np.float16
 FORMATS = ("int8", "fp8_e4m3", "int4")
 FP8_MAX = 448.0
 DEFAULT_GROUP = 128          # reference src/bpt/roofline.py:50 (group_size default)
+
+
+def v_group(block_size):
+    """Tokens per V (scale, zero) group: max(block_size, 32)."""
+    return max(block_size, 32)
 
 
 def _bits(fmt):
@@ -192,8 +200,9 @@ def quantize_paged_cache(k_cache, v_cache, block_table, seq_lens, fmt, group=DEF
     kc = rng.integers(0, 256, (nb, bs, hkv, dc), dtype=np.uint8)
     vc = rng.integers(0, 256, (nb, bs, hkv, dc), dtype=np.uint8)
     garbage = lambda shape: (rng.standard_normal(shape) * 100).astype(F16)  # noqa: E731
+    vg = v_group(bs)
     ks, kz = garbage((nb, hkv, d)), garbage((nb, hkv, d))
-    vs, vz = garbage((nb, hkv, bs)), garbage((nb, hkv, bs))
+    vs, vz = garbage((nb, hkv, vg)), garbage((nb, hkv, vg))
     for b in range(len(seq_lens)):
         n = int(seq_lens[b])
         npg = -(-n // bs)
@@ -209,8 +218,11 @@ def quantize_paged_cache(k_cache, v_cache, block_table, seq_lens, fmt, group=DEF
             phys = blocks[i]
             kc[phys, :hi - lo] = kq[lo:hi]
             vc[phys, :hi - lo] = vq[lo:hi]
-            vs[phys, :, :hi - lo] = vsc[lo:hi].T
-            vz[phys, :, :hi - lo] = vze[lo:hi].T
+        for j in range(-(-n // vg)):
+            lo, hi = j * vg, min((j + 1) * vg, n)
+            lead = blocks[lo // bs]
+            vs[lead, :, :hi - lo] = vsc[lo:hi].T
+            vz[lead, :, :hi - lo] = vze[lo:hi].T
         for g in range(ksc.shape[0]):
             phys = blocks[g * group // bs]
             ks[phys], kz[phys] = ksc[g], kze[g]
@@ -222,6 +234,7 @@ def dequantize_paged_cache(qc, block_table, seq_lens, fmt, group=DEFAULT_GROUP):
     kc, vc = qc["k_codes"], qc["v_codes"]
     nb, bs, hkv, dc = kc.shape
     d = dc * 2 if fmt == "int4" else dc
+    vg = v_group(bs)
     kd = np.zeros((nb, bs, hkv, d), F32)
     vd = np.zeros((nb, bs, hkv, d), F32)
     for b in range(len(seq_lens)):
@@ -234,7 +247,10 @@ def dequantize_paged_cache(qc, block_table, seq_lens, fmt, group=DEFAULT_GROUP):
             if fmt == "int4":
                 kcode, vcode = unpack_int4(kcode), unpack_int4(vcode)
             kd[phys, :cnt] = dequant(kcode, qc["k_scale"][gphys][None], qc["k_zero"][gphys][None], fmt)
-            vs = qc["v_scale"][phys, :, :cnt].T[..., None]
-            vz = qc["v_zero"][phys, :, :cnt].T[..., None]
+            t0 = i * bs  # the page's first token; its V group starts at a multiple of vg
+            vlead = int(block_table[b, (t0 // vg) * vg // bs])
+            off = t0 % vg
+            vs = qc["v_scale"][vlead, :, off:off + cnt].T[..., None]
+            vz = qc["v_zero"][vlead, :, off:off + cnt].T[..., None]
             vd[phys, :cnt] = dequant(vcode, vs, vz, fmt)
     return kd, vd

@@ -56,13 +56,14 @@ def test_bytes_per_token_head(fmt, want):
 @pytest.mark.parametrize("group", [16, 128, 256])
 def test_quantized_bytes_equal_cache_storage(fmt, group):
     """The model's bytes per token-head equal what the cache stores per token-head: code
-    bytes of both caches plus the V pairs of every slot plus the K pairs of the group-leading
-    blocks only (one group per group/block_size blocks), from the real tensors."""
+    bytes of both caches plus the V pairs of the V-group-leading blocks (one 32-token V
+    group per 32/block_size blocks) plus the K pairs of the K-group-leading blocks (one
+    group per group/block_size blocks), from the real tensors."""
     from kvq_decode_amd.quant import allocate_quantized_cache
     nb, bs, hkv, d = 64, 16, 2, 128
     qc = allocate_quantized_cache(nb, bs, hkv, d, fmt, "cpu", k_group=group)
     codes = (qc.k_codes.numel() + qc.v_codes.numel()) * qc.k_codes.element_size()
-    v_pairs = qc.v_sz.numel() * qc.v_sz.element_size()
+    v_pairs = qc.v_sz.numel() * qc.v_sz.element_size() * bs / max(bs, 32)  # leading blocks
     k_pairs = qc.k_sz.numel() * qc.k_sz.element_size() * bs / group  # leading blocks only
     token_heads = nb * bs * hkv
     assert (codes + v_pairs + k_pairs) / token_heads == roofline.bytes_per_token_head(d, fmt, group)

@@ -290,11 +290,15 @@ def test_op_requires_interleaved_scale_pairs():
     bt = torch.zeros(B, nb, dtype=torch.int32)
     sl = torch.ones(B, dtype=torch.int32)
     ksz = torch.zeros(nb, hkv, d, 2, dtype=torch.float16)
-    vsz = torch.zeros(nb, hkv, bs, 2, dtype=torch.float16)
+    vsz = torch.zeros(nb, hkv, 32, 2, dtype=torch.float16)  # V groups of max(bs, 32) tokens
     good = dict(kv_format="int4", k_scale=ksz[..., 0], k_zero=ksz[..., 1],
                 v_scale=vsz[..., 0], v_zero=vsz[..., 1])
     with pytest.raises(KvqArgumentError, match="GPU only"):  # the pair check passed
         paged_decode_attention(q, kc, kc, bt, sl, **good)
+    per_page = torch.zeros(nb, hkv, bs, 2, dtype=torch.float16)  # the version-1 V layout
+    with pytest.raises(KvqArgumentError, match="interleaved"):
+        paged_decode_attention(q, kc, kc, bt, sl,
+                               **dict(good, v_scale=per_page[..., 0], v_zero=per_page[..., 1]))
     bad = dict(good, k_scale=torch.zeros(nb, hkv, d, dtype=torch.float16),
                k_zero=torch.zeros(nb, hkv, d, dtype=torch.float16))
     with pytest.raises(KvqArgumentError, match="interleaved"):

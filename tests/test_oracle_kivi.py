@@ -109,10 +109,12 @@ def test_invariants_on_random_data(fmt):
 
 
 @pytest.mark.parametrize("fmt", kivi.FORMATS)
-@pytest.mark.parametrize("bs", [16, 32])
+@pytest.mark.parametrize("bs", [16, 32, 64])
 def test_paged_quantization_round_trip(fmt, bs):
     """quantize_paged_cache stores what the per-sequence quantizers compute, and
-    dequantize_paged_cache reads it back through the block table (group-leading block)."""
+    dequantize_paged_cache reads it back through the block table (group-leading block).
+    The V pairs sit where include/kvq.h puts them: token t at index t % VG of the block
+    holding its V group's first token, VG = max(block_size, 32)."""
     rng = np.random.default_rng(3)
     lens = [5, 128, 129, 300]
     k = rng.standard_normal((4, 300, 2, 128)).astype(np.float16)
@@ -126,6 +128,10 @@ def test_paged_quantization_round_trip(fmt, bs):
         vq, vs, vz = kivi.quantize_v_seq(v[b, :n], fmt)
         want_k = kivi.dequant(kq, np.repeat(ks, 128, axis=0)[:n], np.repeat(kz, 128, axis=0)[:n], fmt)
         want_v = kivi.dequant(vq, vs[..., None], vz[..., None], fmt)
+        vg = max(bs, 32)
         for t in range(n):
             np.testing.assert_array_equal(kd[bt[b, t // bs], t % bs], want_k[t])
             np.testing.assert_array_equal(vd[bt[b, t // bs], t % bs], want_v[t])
+            lead = bt[b, (t // vg) * vg // bs]
+            assert np.array_equal(qc["v_scale"][lead, :, t % vg].view(np.uint16), vs[t].view(np.uint16))
+            assert np.array_equal(qc["v_zero"][lead, :, t % vg].view(np.uint16), vz[t].view(np.uint16))

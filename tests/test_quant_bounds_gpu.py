@@ -94,10 +94,12 @@ def test_bulk_quantizer_skips_pages_outside_the_pool(fmt):
     after = storage(qc)
     for name, b_, a_ in zip(("k_codes", "v_codes", "k_sz", "v_sz"), before, after):
         assert np.array_equal(b_[20:], a_[20:]), f"{fmt} {name}: wrote outside the table"
-    # sequence 1's first group (pages 0-7) has no pair page: its valid pages 1-7 keep their
-    # K bytes; its V rows are per token and written
+    # sequence 1's first K group (pages 0-7) has no pair page: its valid pages 1-7 keep
+    # their K bytes. Its page 1 (block 11) shares its V (scale, zero) group with page 0,
+    # also outside the pool, and keeps its V bytes; the V rows of pages 2-7 are written
     assert np.array_equal(before[0][11:18], after[0][11:18])
-    assert not np.array_equal(before[1][11:18], after[1][11:18])
+    assert np.array_equal(before[1][11], after[1][11])
+    assert not np.array_equal(before[1][12:18], after[1][12:18])
     # sequence 0's page 3 is outside the pool; its other pages were written
     assert not np.array_equal(before[0][0:3], after[0][0:3])
 

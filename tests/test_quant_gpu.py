@@ -48,6 +48,17 @@ def valid_slots(bt, sl, bs):
     return np.array(out)
 
 
+def v_pair_slots(bt, sl, bs):
+    """(block, index) of every valid token's V (scale, zero) pair: index t % VG of its V
+    group's first page, VG = max(block_size, 32) (include/kvq.h)."""
+    vg = max(bs, 32)
+    out = []
+    for b, n in enumerate(sl):
+        for t in range(int(n)):
+            out.append((int(bt[b, (t // vg) * vg // bs]), t % vg))
+    return np.array(out)
+
+
 def lead_blocks(bt, sl, bs, group=128):
     return sorted({int(bt[b, (g * group) // bs]) for b, n in enumerate(sl)
                    for g in range(-(-int(n) // group))})
@@ -72,6 +83,7 @@ def test_bulk_quantizer_bit_exact(fmt, bs):
     got = quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt)
     torch.cuda.synchronize()
     slots = valid_slots(bt, sl, bs)
+    vsl = v_pair_slots(bt, sl, bs)
     for name in ("k_codes", "v_codes"):
         g = getattr(got, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
         w = want[name][slots[:, 0], slots[:, 1]]
@@ -81,8 +93,8 @@ def test_bulk_quantizer_bit_exact(fmt, bs):
         g = getattr(got, name).cpu().numpy()[lead].view(np.uint16)
         assert np.array_equal(g, want[name][lead].view(np.uint16)), name
     for name in ("v_scale", "v_zero"):
-        g = getattr(got, name).cpu().numpy()[slots[:, 0], :, slots[:, 1]].view(np.uint16)
-        w = want[name][slots[:, 0], :, slots[:, 1]].view(np.uint16)
+        g = getattr(got, name).cpu().numpy()[vsl[:, 0], :, vsl[:, 1]].view(np.uint16)
+        w = want[name][vsl[:, 0], :, vsl[:, 1]].view(np.uint16)
         assert np.array_equal(g, w), name
 
 
@@ -99,6 +111,7 @@ def test_bulk_quantizer_other_head_dims(fmt, D):
         got = quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt, k_group=k_group)
         torch.cuda.synchronize()
         slots = valid_slots(bt, sl, 16)
+        vsl = v_pair_slots(bt, sl, 16)
         for name in ("k_codes", "v_codes"):
             g = getattr(got, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
             w = want[name][slots[:, 0], slots[:, 1]]
@@ -108,8 +121,8 @@ def test_bulk_quantizer_other_head_dims(fmt, D):
             g = getattr(got, name).cpu().numpy()[lead].view(np.uint16)
             assert np.array_equal(g, want[name][lead].view(np.uint16)), name
         for name in ("v_scale", "v_zero"):
-            g = getattr(got, name).cpu().numpy()[slots[:, 0], :, slots[:, 1]].view(np.uint16)
-            w = want[name][slots[:, 0], :, slots[:, 1]].view(np.uint16)
+            g = getattr(got, name).cpu().numpy()[vsl[:, 0], :, vsl[:, 1]].view(np.uint16)
+            w = want[name][vsl[:, 0], :, vsl[:, 1]].view(np.uint16)
             assert np.array_equal(g, w), name
 
 
@@ -136,6 +149,7 @@ def test_append_equals_bulk_other_head_dims(fmt, D):
     want = quantize_paged_cache(kc_g, vc_g, bt_g, gpu(sl1), fmt)
     torch.cuda.synchronize()
     slots = valid_slots(bt, sl1, bs)
+    vsl = v_pair_slots(bt, sl1, bs)
     for name in ("k_codes", "v_codes"):
         g = getattr(qc, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
         w = getattr(want, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
@@ -145,8 +159,8 @@ def test_append_equals_bulk_other_head_dims(fmt, D):
         assert np.array_equal(getattr(qc, name).cpu().numpy()[lead],
                               getattr(want, name).cpu().numpy()[lead]), name
     for name in ("v_scale", "v_zero"):
-        g = getattr(qc, name).cpu().numpy()[slots[:, 0], :, slots[:, 1]]
-        w = getattr(want, name).cpu().numpy()[slots[:, 0], :, slots[:, 1]]
+        g = getattr(qc, name).cpu().numpy()[vsl[:, 0], :, vsl[:, 1]]
+        w = getattr(want, name).cpu().numpy()[vsl[:, 0], :, vsl[:, 1]]
         assert np.array_equal(g, w), name
 
 
@@ -174,6 +188,7 @@ def test_append_equals_bulk_other_k_groups(fmt, k_group):
     want = quantize_paged_cache(kc_g, vc_g, bt_g, gpu(sl1), fmt, k_group=k_group)
     torch.cuda.synchronize()
     slots = valid_slots(bt, sl1, bs)
+    vsl = v_pair_slots(bt, sl1, bs)
     for name in ("k_codes", "v_codes"):
         g = getattr(qc, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
         w = getattr(want, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
@@ -182,6 +197,9 @@ def test_append_equals_bulk_other_k_groups(fmt, k_group):
     for name in ("k_scale", "k_zero"):
         assert np.array_equal(getattr(qc, name).cpu().numpy()[lead],
                               getattr(want, name).cpu().numpy()[lead]), name
+    for name in ("v_scale", "v_zero"):
+        assert np.array_equal(getattr(qc, name).cpu().numpy()[vsl[:, 0], :, vsl[:, 1]],
+                              getattr(want, name).cpu().numpy()[vsl[:, 0], :, vsl[:, 1]]), name
 
 
 def _tie_rows(rng, n, width, fmt):
@@ -232,6 +250,7 @@ def test_quantizer_rounding_ties(fmt):
     got = quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt)
     torch.cuda.synchronize()
     slots = valid_slots(bt, sl, bs)
+    vsl = v_pair_slots(bt, sl, bs)
     for name in ("k_codes", "v_codes"):
         g = getattr(got, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
         w = want[name][slots[:, 0], slots[:, 1]]
@@ -241,8 +260,8 @@ def test_quantizer_rounding_ties(fmt):
         g = getattr(got, name).cpu().numpy()[lead].view(np.uint16)
         assert np.array_equal(g, want[name][lead].view(np.uint16)), name
     for name in ("v_scale", "v_zero"):
-        g = getattr(got, name).cpu().numpy()[slots[:, 0], :, slots[:, 1]].view(np.uint16)
-        w = want[name][slots[:, 0], :, slots[:, 1]].view(np.uint16)
+        g = getattr(got, name).cpu().numpy()[vsl[:, 0], :, vsl[:, 1]].view(np.uint16)
+        w = want[name][vsl[:, 0], :, vsl[:, 1]].view(np.uint16)
         assert np.array_equal(g, w), name
 
 
@@ -308,9 +327,14 @@ def test_code_layout_does_not_change_results(fmt):
         k_codes=torch.zeros_like(tm.k_codes), v_codes=torch.zeros_like(tm.v_codes))
     quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt, out=dst)
     slots = valid_slots(bt, sl, 16)
+    vsl = v_pair_slots(bt, sl, 16)
     for name in ("k_codes", "v_codes"):
         g = getattr(dst, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
         w = getattr(qc, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
+        assert np.array_equal(g, w), name
+    for name in ("v_scale", "v_zero"):
+        g = getattr(dst, name).cpu().numpy()[vsl[:, 0], :, vsl[:, 1]].view(np.uint16)
+        w = getattr(qc, name).cpu().numpy()[vsl[:, 0], :, vsl[:, 1]].view(np.uint16)
         assert np.array_equal(g, w), name
 
 
@@ -350,6 +374,7 @@ def test_other_k_group_sizes(fmt, k_group):
     qc = quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt, k_group=k_group)
     want = kivi.quantize_paged_cache(kc, vc, bt, sl, fmt, group=k_group)
     slots = valid_slots(bt, sl, 16)
+    vsl = v_pair_slots(bt, sl, 16)
     for name in ("k_codes", "v_codes"):
         g = getattr(qc, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
         assert np.array_equal(g, want[name][slots[:, 0], slots[:, 1]]), name
@@ -357,6 +382,9 @@ def test_other_k_group_sizes(fmt, k_group):
     for name in ("k_scale", "k_zero"):
         g = getattr(qc, name).cpu().numpy()[lead].view(np.uint16)
         assert np.array_equal(g, want[name][lead].view(np.uint16)), name
+    for name in ("v_scale", "v_zero"):
+        g = getattr(qc, name).cpu().numpy()[vsl[:, 0], :, vsl[:, 1]].view(np.uint16)
+        assert np.array_equal(g, want[name][vsl[:, 0], :, vsl[:, 1]].view(np.uint16)), name
     host = {n: getattr(qc, n).cpu().numpy() for n in
             ("k_codes", "v_codes", "k_scale", "k_zero", "v_scale", "v_zero")}
     kd, vd = kivi.dequantize_paged_cache(host, bt, sl, fmt, group=k_group)
@@ -401,6 +429,7 @@ def test_append_equals_bulk(fmt):
     want = quantize_paged_cache(kc_g, vc_g, bt_g, gpu(sl1), fmt)
     torch.cuda.synchronize()
     slots = valid_slots(bt, sl1, bs)
+    vsl = v_pair_slots(bt, sl1, bs)
     for name in ("k_codes", "v_codes"):
         g = getattr(qc, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
         w = getattr(want, name).cpu().numpy()[slots[:, 0], slots[:, 1]]
@@ -410,8 +439,8 @@ def test_append_equals_bulk(fmt):
         assert np.array_equal(getattr(qc, name).cpu().numpy()[lead],
                               getattr(want, name).cpu().numpy()[lead]), name
     for name in ("v_scale", "v_zero"):
-        g = getattr(qc, name).cpu().numpy()[slots[:, 0], :, slots[:, 1]]
-        w = getattr(want, name).cpu().numpy()[slots[:, 0], :, slots[:, 1]]
+        g = getattr(qc, name).cpu().numpy()[vsl[:, 0], :, vsl[:, 1]]
+        w = getattr(want, name).cpu().numpy()[vsl[:, 0], :, vsl[:, 1]]
         assert np.array_equal(g, w), name
 
 
@@ -475,7 +504,8 @@ def _full_size_case(fmt, lens, check_seqs):
 
 def _dequant_int4_torch(qc, bt, b, L, h, bs, group=128):
     """float32 K, V [L, D] of kv head h of sequence b from an INT4 cache (x = c s + z;
-    low nibble = even channel; K pairs in the group's first block, V pairs per token)."""
+    low nibble = even channel; K pairs in the K group's first block, V pairs at index
+    t % VG of the V group's first block, VG = max(bs, 32))."""
     pages = bt[b, :-(-L // bs)].long()
 
     def codes(c):
@@ -485,7 +515,9 @@ def _dequant_int4_torch(qc, bt, b, L, h, bs, group=128):
     lead = bt[b, (t // group) * group // bs].long()
     ksz = qc.k_sz[lead, h].float()                       # [L, D, 2]
     k = codes(qc.k_codes) * ksz[..., 0] + ksz[..., 1]
-    vsz = qc.v_sz[pages, h].reshape(-1, 2)[:L].float()   # [L, 2]
+    vg = max(bs, 32)
+    vlead = bt[b, (t // vg) * vg // bs].long()
+    vsz = qc.v_sz[vlead, h, t % vg].float()              # [L, 2]
     v = codes(qc.v_codes) * vsz[:, :1] + vsz[:, 1:]
     return k, v
 
@@ -557,12 +589,15 @@ def test_nan_garbage_in_unused_quantized_slots(fmt, kw):
     kd, vd = kivi.dequantize_paged_cache(host, bt, sl, fmt)
     ref = paged_decode_attention_ref(q.astype(np.float32), kd, vd, bt, sl, out_dtype=np.float32)
     nan16 = torch.tensor(float("nan"), dtype=torch.float16)
+    vg = 32  # tokens per V (scale, zero) group at block_size 16
     for b, n in enumerate(lens):
         if n % 16:
             blk = int(bt[b, (n - 1) // 16])
             qc.k_codes[blk, n % 16:] = 0xFF
             qc.v_codes[blk, n % 16:] = 0xFF
-            qc.v_sz[blk, :, n % 16:] = nan16
+        if n % vg:  # the pairs past the end of the sequence's last V group
+            vlead = int(bt[b, ((n - 1) // vg) * vg // 16])
+            qc.v_sz[vlead, :, n % vg:] = nan16
     out = paged_decode_attention(gpu(q), qc.k_codes, qc.v_codes, gpu(bt), gpu(sl), **kw,
                                  **qc.decode_kwargs())
     torch.cuda.synchronize()
@@ -593,6 +628,7 @@ def test_append_skips_empty_sequences(fmt):
     want = quantize_paged_cache(kc_g, vc_g, bt_g, gpu(sl1), fmt)
     torch.cuda.synchronize()
     slots = valid_slots(bt, sl1, bs)
+    vsl = v_pair_slots(bt, sl1, bs)
     for name in ("k_codes", "v_codes"):
         g = getattr(qc, name).cpu().numpy()
         assert np.array_equal(g[slots[:, 0], slots[:, 1]],
@@ -609,3 +645,10 @@ def test_append_skips_empty_sequences(fmt):
         mask = np.ones(g.shape[0], bool)
         mask[lead] = False
         assert np.array_equal(g[mask], bits(before[name])[mask]), name
+    for name in ("v_scale", "v_zero"):
+        g = bits(getattr(qc, name))
+        assert np.array_equal(g[vsl[:, 0], :, vsl[:, 1]],
+                              bits(getattr(want, name))[vsl[:, 0], :, vsl[:, 1]]), name
+        mask = np.ones((g.shape[0], g.shape[2]), bool)  # [block, index]
+        mask[vsl[:, 0], vsl[:, 1]] = False
+        assert np.array_equal(g.transpose(0, 2, 1)[mask], bits(before[name]).transpose(0, 2, 1)[mask]), name
