@@ -491,7 +491,7 @@ def stats_summary(config, kt_dir, steps=200, warmup=20):
     ]
     stage1_avg = None
     for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
-        name = r["Name"].split("(")[0].replace("void ", "")
+        name = r["Name"].replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")
         avg = float(r["AverageNs"]) / 1e3
         lines.append(f"{name[:60]:60s}{int(r['Calls']):>8d}{avg:>10.2f}"
                      f"{float(r['MinNs']) / 1e3:>10.2f}{float(r['MaxNs']) / 1e3:>10.2f}")
