@@ -168,8 +168,9 @@ int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t
 
 /* Work-unit plan, the library's default for batches of 2 to 1024 sequences (no reference
  * counterpart; it takes the place of the split heuristic, triton_fp16.py:175-180). For
- * 2 <= batch <= 1024 when kvq_plan_decode gives splits >= 2 or the longest context
- * (max_pages * block_size) is at least 4096 tokens:
+ * 2 <= batch <= 1024 with batch * cdiv(max_pages * block_size, 16) < 2^31, when
+ * kvq_plan_decode gives splits >= 2 or the longest context (max_pages * block_size) is at
+ * least 4096 tokens:
  *   units = T * cu_count / (waves * kv_heads) (at least 1), with T waves per CU and
  *           `waves` per unit workgroup: fp16 T = 2, waves = 2; INT8 / FP8 T = 4,
  *           waves = 4; INT4 T = 8, waves = 2,
@@ -215,7 +216,9 @@ int kvq_paged_decode(const kvq_decode_args* args, int32_t num_splits, float* o_p
                      float* lse, kvq_stream_t stream);
 
 /* Work-unit decode (no reference counterpart: another partition of the same two stages,
- * triton_fp16.py:83-163, for ragged and large batches; every kv_format, batch at most 1024).
+ * triton_fp16.py:83-163, for ragged and large batches; every kv_format, batch at most 1024,
+ * and batch * cdiv(max_blocks * block_size, 16) below 2^31 so that a kv head's chunk count
+ * over the batch fits the kernels' 32-bit arithmetic; KVQ_ERR_UNSUPPORTED otherwise).
  * Per kv head, the 16-token chunks of all sequences, concatenated in batch order
  * (sequence b has cdiv(seq_lens[b], 16) chunks, N in total), are cut into
  * NU = min(units, N) equal ranges; one workgroup of args->waves_per_group waves (0 = 2;

@@ -317,6 +317,13 @@ kvq::AppendParams make_append_params(const kvq_decode_args* a, const void* k_new
     return p;
 }
 
+// The work-unit kernels count a kv head's chunks over the whole batch in 32-bit integers:
+// every sequence contributes at most cdiv(max_blocks * block_size, 16) of them, and the
+// batch's total must stay below 2^31 (then the unit arithmetic's products stay below 2^62).
+bool units_fit(int64_t batch, int64_t max_blocks, int64_t block_size) {
+    return batch * ((max_blocks * block_size + 15) / 16) <= INT32_MAX;
+}
+
 // Checks of the work-unit entry points; fills the launch parameters. The units kernels
 // read every seq_len of the batch in one workgroup (batch <= kUnitMaxBatch).
 int units_params(const kvq_decode_args* args, int32_t units, float* o_part, float* lse,
@@ -325,6 +332,7 @@ int units_params(const kvq_decode_args* args, int32_t units, float* o_part, floa
     if (st != KVQ_OK) return st;
     if (!o_part || !lse) return KVQ_ERR_NULL_POINTER;
     if (args->batch > kvq::kUnitMaxBatch) return KVQ_ERR_UNSUPPORTED;
+    if (!units_fit(args->batch, args->max_blocks, args->block_size)) return KVQ_ERR_UNSUPPORTED;
     if (units < 1 || int64_t(units) * grid_heads(args) > INT32_MAX ||
         int64_t(units) + args->batch > INT32_MAX)
         return KVQ_ERR_SPLITS;
@@ -433,6 +441,7 @@ int kvq_plan_units(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t 
     // amortize (measured on MI355X: fp16 B64 at 1k tokens +17%, at 8k +3% uniform and
     // -26% ragged)
     if (batch < 2 || batch > kvq::kUnitMaxBatch) return KVQ_OK;
+    if (!units_fit(batch, max_pages, block_size)) return KVQ_OK;
     if (splits < 2 && int64_t(max_pages) * block_size < 4096) return KVQ_OK;
     // Waves per CU and per unit workgroup, measured on MI355X: fp16 2 in workgroups of 2;
     // INT8 / FP8 4 in workgroups of 4; INT4 (half the bytes of a chunk for about the

@@ -156,7 +156,7 @@ def test_plan_decode():
 
 
 def test_plan_units():
-    """The work-unit plan is chosen for batches of 2 to 256 whose split plan splits or
+    """The work-unit plan is chosen for batches of 2 to 1024 whose split plan splits or
     whose longest context is at least 4096 tokens:
     2 waves per CU in 2-wave unit workgroups (fp16), 4 in 4-wave workgroups (INT8, FP8),
     8 in 2-wave workgroups (INT4); else (0, 0)."""
@@ -348,6 +348,13 @@ def test_units_reject():
         assert fn(None, 8, op, lse, None) == _lib.KVQ_ERR_NULL_POINTER
     a.batch = 1025  # one workgroup reads every seq_len of the batch
     assert L.kvq_decode_units(ctypes.byref(a), 8, op, lse, None) == _lib.KVQ_ERR_UNSUPPORTED
+    # a kv head's chunks over the batch must stay below 2^31: 1024 x 2^21 chunks do not
+    a.batch, a.max_blocks, a.num_blocks = 1024, 2**21, 2**22
+    assert L.kvq_decode_units(ctypes.byref(a), 8, op, lse, None) == _lib.KVQ_ERR_UNSUPPORTED
+    from kvq_decode_amd.ops import plan_units
+    assert plan_units(1024, 8, 16, 2**21, 256, "fp16") == (0, 0)  # the split plan instead
+    assert plan_units(1024, 8, 16, 2**21 - 1, 256, "fp16") == (32, 2)
+    a.max_blocks, a.num_blocks = 64, 128
     a.batch = 2
     a.waves_per_group = 8  # unit workgroups: 1, 2 or 4 waves
     assert L.kvq_decode_units(ctypes.byref(a), 8, op, lse, None) == _lib.KVQ_ERR_UNSUPPORTED

@@ -87,8 +87,10 @@ def test_unit_partition_invariants():
 
 
 def test_unit_of_large_values_do_not_overflow_int64():
-    # B <= 256 sequences of at most 65535 chunks: (x + 1) * NU stays far below 2^63
-    N, NU = 256 * 65535, 2**31 - 1
+    # the host keeps a kv head's chunk count N below 2^31 (kvq_decode_units rejects larger
+    # batch * chunks-per-sequence bounds), and NU <= N: (x + 1) * NU < 2^62
+    N, NU = 2**31 - 1, 2**31 - 1
     NU = min(NU, N)
+    assert N * NU < 2**62 and (N - 1) * N < 2**62  # unit_of's and unit_lo's products
     assert unit_of(N - 1, N, NU) == NU - 1
     assert unit_of(0, N, NU) == 0
