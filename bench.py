@@ -219,7 +219,8 @@ def time_stage1(step, iters, blocks=5):
 
     import torch
     # spin the clock up first: at least SPIN_UP_S of back-to-back launches (MI355X takes
-    # tens of ms of sustained load to reach its steady clock after idle)
+    # tens of ms of sustained load to reach its steady clock after idle, and after the CPU
+    # work of building a quantized config's inputs 50 ms was not always enough)
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < SPIN_UP_S:
         for _ in range(10):
@@ -238,7 +239,7 @@ def time_stage1(step, iters, blocks=5):
 
 
 FLUSH_SAMPLES = 60
-SPIN_UP_S = 0.05
+SPIN_UP_S = 0.3
 
 
 def time_flushed(step, iters=FLUSH_SAMPLES):
