@@ -11,6 +11,7 @@
 //           two codes); F = 2^24, w = 1
 //     INT4  nibbles masked in place: low nibbles (even codes) c * 2^-24 (w = 1), high
 //           nibbles (odd codes) c * 2^-20 (w = 16); F = 2^24. Five VALU ops per 8 codes
+//           for K; V takes whole bytes and the high nibbles (QFmt<KVQ_KV_INT4>::vtiles)
 //     FP8   h = f(c) (v_cvt_scalef32_pk_f16_fp8, exact OCP e4m3fn); F = 1, w = 1
 //   MI355X's MFMAs take fp16 subnormal inputs exactly (measured: a 32-term product sum of
 //   subnormal A operands agrees with an exact sum to fp32 rounding).
@@ -150,7 +151,10 @@ struct QFmt<KVQ_KV_FP8_E4M3> {
 // k-step st uses dword st: halves in code order {0,4, 1,5, 2,6, 3,7} of channels 32g + 8st,
 // the odd codes at 2^-20 (w = 16). V: the lane needs 4 bytes (8 codes) of each of its 4
 // token rows; the rows are loaded whole (16 lanes per 1 KB instruction) and regrouped
-// through LDS (vstage_i4). Tile t = code t of the lane's 8, odd tiles at 2^-20.
+// through LDS (vstage_i4). Tiles 2k, 2k + 1 come from byte k of the lane's 4: tile 2k takes
+// the whole byte (code 2k + 16 code 2k+1, a subnormal below 2^-16 - no mask), tile 2k + 1
+// the odd code alone at 2^-20; tile_weights turns the sums back into codes 2k and 2k + 1.
+// One v_perm and one v_and per two tiles of a token pair.
 template <>
 struct QFmt<KVQ_KV_INT4> {
     static constexpr float F = 16777216.f;  // 2^24
@@ -171,9 +175,9 @@ struct QFmt<KVQ_KV_INT4> {
         for (int k = 0; k < 4; ++k) {
             const uint32_t x = pair_bytes(v[0][0], v[1][0], k);
             const uint32_t y = pair_bytes(v[2][0], v[3][0], k);
-            a01[2 * k] = x & 0x000F000Fu;
+            a01[2 * k] = x;
             a01[2 * k + 1] = x & 0x00F000F0u;
-            a23[2 * k] = y & 0x000F000Fu;
+            a23[2 * k] = y;
             a23[2 * k + 1] = y & 0x00F000F0u;
         }
     }
@@ -642,12 +646,18 @@ __device__ __forceinline__ void chunk_pair(const ChunkQ<FMT>& ca, const ChunkQ<F
     }
 }
 
-// INT4 V tiles hold odd codes at 2^-20 (w = 16): their accumulators carry F / 16.
+// INT4 V tiles: tile 2k sums p'' (c_2k + 16 c_2k+1), tile 2k + 1 sums p'' 16 c_2k+1 (both in
+// units of 2^-24). Code 2k's sum is their difference and code 2k + 1's a sixteenth of the
+// second. The difference cancels at most 255 / 15 of the magnitude: the fp32 accumulators'
+// rounding stays below 2^-24 * 255 * sum p'', about 1.5e-5 of the largest V value.
 template <int FMT>
 __device__ __forceinline__ void tile_weights(SoftmaxState<128>& st) {
     if constexpr (FMT == KVQ_KV_INT4) {
 #pragma unroll
-        for (int t = 1; t < 8; t += 2) st.acc[t] *= 0.0625f;
+        for (int t = 0; t < 8; t += 2) {
+            st.acc[t] -= st.acc[t + 1];
+            st.acc[t + 1] *= 0.0625f;
+        }
     }
 }
 
