@@ -22,9 +22,10 @@ Pinning status (what checks each function beyond re-typing its formula):
       in its own results files (A100 108 SMs, T4 40 SMs).
   roofline.*                             pinned: 128 KiB/token Llama-3-8B fp16, INT4 3.76x,
       kv_MB fields of the reference results files.
-  kivi.*                                 no reference code exists (quantized KV is "not
-      started" upstream): pinned by hand-computed vectors, invariants (code range,
-      extremes, error <= s/2, pack/unpack identity) and, for FP8, torch.float8_e4m3fn.
+  kivi.*                                 pinned by the spec's mathematics (the reference
+      has no quantizer code to compare with: quantized KV is "not started" upstream):
+      hand-computed vectors, invariants (code range, extremes, error <= s/2, pack/unpack
+      identity) and, for FP8, the library routine torch.float8_e4m3fn.
 """
 
 from oracle.attention import (  # noqa: F401

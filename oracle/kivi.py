@@ -3,9 +3,10 @@
 The reference plans quantized KV (README.md:7, :16 "not started") and fixes only its byte
 model (src/bpt/roofline.py:6-9, :22-31): asymmetric fp16 scale + zero, keys per channel
 over groups of `group_size` tokens, values per token. There is no reference code, so this
-module IS the spec the HIP kernels must match bit for bit. Parity with the reference is
-therefore "unpinned" for this module; it is pinned instead by hand-computed vectors and
-invariants in tests/test_oracle_kivi.py and, for FP8, by torch.float8_e4m3fn.
+module IS the spec the HIP kernels must match bit for bit. With no reference output to
+compare against, it is pinned by the mathematics of the spec: hand-computed vectors and
+invariants in tests/test_oracle_kivi.py and, for FP8, the library routine
+torch.float8_e4m3fn.
 
 Spec (all arithmetic IEEE float32, round-to-nearest-even, in this exact order):
   integer formats, b in {8, 4}, R = 2**b - 1, over a set X of fp16 values:
