@@ -66,6 +66,7 @@ typedef enum kvq_status {
  *                    block_table[b][j * VG / block_size], token t at index t % VG (with
  *                    16-token pages, a page pair's 32 pairs of one kv head fill one
  *                    128-byte line; other blocks' entries are unused)
+ * The quantized formats decode at head_dim D = 64, 128 or 256 (fp16: 32-256).
  * Scale and zero are stored interleaved: one fp16 [nb, Hkv, D, 2] (K) and one
  * [nb, Hkv, VG, 2] (V) tensor of (scale, zero) pairs, so that a decode loads both of a
  * token (V) or a channel (K) with one access. k_scale / v_scale point at element 0 of that
@@ -113,7 +114,7 @@ typedef struct kvq_decode_args {
     int32_t waves_per_group;  /* tuning: waves per (kv head, split) workgroup, one of
                                  1, 2, 4, 8, 16; 0 = the library's choice */
     int32_t pipeline;         /* tuning: depth of the load ring in 16-token chunks, 1, 2
-                                 or 4 (fp16 head_dim 256: 1 or 2); deeper rings keep more
+                                 or 4 (head_dim 256: 1 or 2); deeper rings keep more
                                  loads in flight with fewer waves per SIMD; 0 = the
                                  library's choice (2) */
 } kvq_decode_args;

@@ -20,8 +20,8 @@ LIB_PATH = os.path.join(PKG_DIR, "libkvq.so")
 OBJ_DIR = os.path.join(PKG_DIR, "_build")  # objects (not committed, not shipped)
 
 ARCH = "gfx950"
-SOURCES = ["capi.cpp", "decode.hip", "decode_q.hip", "quant.hip", "append.hip",
-           "static_workspace.hip"]
+SOURCES = ["capi.cpp", "decode.hip", "decode_q.hip", "decode_q_d64.hip", "decode_q_d256.hip",
+           "quant.hip", "append.hip", "static_workspace.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

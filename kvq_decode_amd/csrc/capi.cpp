@@ -80,7 +80,8 @@ int check_decode_args(const kvq_decode_args* a, bool need_out) {
     if (a->kv_format < KVQ_KV_F16 || a->kv_format > KVQ_KV_INT4) return KVQ_ERR_FORMAT;
     if (a->kv_format != KVQ_KV_F16) {
         if (!a->k_scale || !a->k_zero || !a->v_scale || !a->v_zero) return KVQ_ERR_FORMAT;
-        if (a->head_dim != 128) return KVQ_ERR_UNSUPPORTED;
+        if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
+            return KVQ_ERR_UNSUPPORTED;
         // a K group spans at most the decode kernel's 64-page block-table window
         if (a->k_group < a->block_size || a->k_group % a->block_size != 0 ||
             !is_pow2(a->k_group) || a->k_group / a->block_size > 64)
@@ -169,14 +170,15 @@ int64_t lds_bytes(const kvq_decode_args* a, int waves) {
     const int group = int(a->q_heads / grid_heads(a));  // q heads per kernel kv head
     const int64_t combine = int64_t(4) * (int64_t(waves) * group * a->head_dim + 32 * waves);
     // fp16: the waves' K staging tiles (16 rows of head_dim halves each), which the
-    // combine reuses; quantized: region 0 (combine or K tiles), a 512-byte K-scale slot
-    // per wave and 4 KB of q in k-operand order
+    // combine reuses; quantized: region 0 (combine or staging tiles), a K-scale slot of
+    // 4 head_dim bytes per wave and 32 head_dim bytes of q in k-operand order
     if (a->kv_format == KVQ_KV_F16) {
         const int64_t stage = int64_t(waves) * 32 * a->head_dim;
         return combine > stage ? combine : stage;
     }
-    return int64_t(4) * (kvq::quant_lds_region0(waves, group, a->kv_format) + 128 * int64_t(waves) +
-                         1024);
+    return int64_t(4) * (kvq::quant_lds_region0(waves, group, a->kv_format, a->head_dim) +
+                         int64_t(a->head_dim) * waves) +
+           32 * int64_t(a->head_dim);
 }
 
 // Waves per workgroup: the caller's choice if given, else as many as give each wave at
@@ -199,14 +201,14 @@ int pick_waves(const kvq_decode_args* a, int pages_per_split) {
 }
 
 // Loads in flight per wave, in 16-token chunks (the depth of the kernels' register
-// ring): the caller's 1, 2 or 4 (fp16 head_dim 256: 1 or 2), else 2 (measured best for
+// ring): the caller's 1, 2 or 4 (head_dim 256: 1 or 2), else 2 (measured best for
 // every format on MI355X; the chunk-pair kernel of the quantized formats keeps one pair
 // in flight at depths 1 and 2, three at 4). Returns 0 when invalid.
 int pick_pipeline(const kvq_decode_args* a) {
     const int r = a->pipeline;
     if (r == 0) return 2;
     if (r != 1 && r != 2 && r != 4) return 0;
-    if (r == 4 && a->kv_format == KVQ_KV_F16 && a->head_dim > 128) return 0;
+    if (r == 4 && a->head_dim > 128) return 0;
     return r;
 }
 

@@ -504,8 +504,7 @@ static hipError_t launch_units_d(const DecodeParams& p, int waves, int ring,
 hipError_t launch_decode_units(const DecodeParams& p, int kv_format, int head_dim, int waves,
                                int ring, hipStream_t stream) {
     if (kv_format != KVQ_KV_F16)
-        return head_dim == 128 ? launch_decode_q_units(p, kv_format, waves, ring, stream)
-                               : hipErrorInvalidValue;
+        return launch_decode_q_units(p, kv_format, head_dim, waves, ring, stream);
     switch (head_dim) {
         case 32: return launch_units_d<32>(p, waves, ring, stream);
         case 64: return launch_units_d<64>(p, waves, ring, stream);

@@ -1,1092 +1,34 @@
-// Paged-KV GQA decode attention over KIVI-quantized KV for gfx950: INT8, FP8-e4m3 (OCP
-// e4m3fn) and packed INT4 codes with fp16 scale and zero-point, K per channel over groups
-// of k_group tokens, V per token. The reference plans this (README.md:7, :16 "not
-// started"); its byte model (src/bpt/roofline.py:6-9, 22-31) fixes the format's costs.
-//
-// Same workgroup/wave decomposition and MFMA layouts as the fp16 kernel (decode.hip); the
-// dequantization is folded into the two products instead of being applied per element.
-//
-//   code c -> fp16 h, exactly and without a bias: h = c * w / F
-//     INT8  h = c * 2^-24: the code is the mantissa of an fp16 subnormal (one v_perm per
-//           two codes); F = 2^24, w = 1
-//     INT4  nibbles masked in place: low nibbles (even codes) c * 2^-24 (w = 1), high
-//           nibbles (odd codes) c * 2^-20 (w = 16); F = 2^24. Five VALU ops per 8 codes
-//           for K; V takes whole bytes and the high nibbles (QFmt<KVQ_KV_INT4>::vtiles)
-//     FP8   h = f(c) (v_cvt_scalef32_pk_f16_fp8, exact OCP e4m3fn); F = 1, w = 1
-//   MI355X's MFMAs take fp16 subnormal inputs exactly (measured: a 32-term product sum of
-//   subnormal A operands agrees with an exact sum to fp32 rounding).
-//   K (x = c * s_d + z_d, per channel d):
-//     q.k = sum_d q'_d c_d + C = F * sum_d (q'_d / w_d) h_d + C,   q' = q * s,
-//     C = sum_d q_d z_d.  q'' = q' / w is held as hi + lo fp16 parts (recomputed per K
-//     group); the MFMA chains give R = sum q'' h, and the log2-domain score is
-//     R * (F * scale * log2 e) + C * scale * log2 e.
-//   V (x = c * s_t + z_t, per token t):
-//     sum_t p_t x_td = (F / w_d) * sum_t p''_t h_td + sum_t p_t z_t,  p'' = p * s_t as
-//     hi + lo fp16 parts (the PV MFMA's B operand); the second sum is one fp32 scalar per
-//     head (`corr`), added once at the end.
-//
-// Two kernels:
-//   decode_q2_kernel (1 to 4 q heads per kv head): the 16 MFMA columns hold 2 chunks x
-//     4 heads x {hi, lo}. Column j: head j & 3, chunk (j >> 2) & 1 of the pair, part j >> 3.
-//     The QK product runs the 4 k-steps of both chunks into one accumulator against
-//     block-masked Q operands (zero in the other chunk's columns), so one softmax pass
-//     covers 32 tokens, and the PV product contracts both chunks in one 16x16x32 MFMA per
-//     tile: k-slots 8g + r hold the first chunk's token 4g + r, 8g + 4 + r the second's;
-//     each lane's p sits in the half of its own chunk, zeros in the other. The two chunks'
-//     softmax streams of a head (columns j, j ^ 4) are merged once at the end.
-//   decode_q_kernel (5 to 16 heads): one chunk per step; up to 8 heads the columns hold
-//     {hi, lo} x 8 heads (one QK chain), above that two chains.
-// Only head_dim 128 is built for the quantized formats.
-#include <hip/hip_runtime.h>
-#include <math.h>
-#include <stdint.h>
-
-#include "decode_common.h"
+// Quantized decode kernels (decode_q_impl.h) for head_dim 128.
+#include "decode_q_impl.h"
 
 namespace kvq {
 
-typedef uint32_t u2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u4v __attribute__((ext_vector_type(4)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-
-// v_perm_b32: byte k of the result is byte sel.k of {hi:lo} (0-3 = lo, 4-7 = hi, 12 = 0x00).
-__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
-    return __builtin_amdgcn_perm(hi, lo, sel);
+hipError_t launch_decode_q_hd128(const DecodeParams& p, int kv_format, bool final_out,
+                                int waves, int ring, hipStream_t stream) {
+    return launch_decode_q_for<128>(p, kv_format, final_out, waves, ring, stream);
 }
 
-// Byte e of a and byte e of b as the low bytes of two halves: [a.e, 0, b.e, 0].
-__device__ __forceinline__ uint32_t pair_bytes(uint32_t a, uint32_t b, int e) {
-    return perm(b, a, 0x0C040C00u + 0x00010001u * (uint32_t)e);
+hipError_t launch_decode_q_units_hd128(const DecodeParams& p, int kv_format, int waves,
+                                      int ring, hipStream_t stream) {
+    return launch_decode_q_units_for<128>(p, kv_format, waves, ring, stream);
 }
 
-// Initial reference max of an online-softmax stream: finite, so that a stream that has
-// seen no token yet (m = kM0, l = 0) rescales by exp2(kM0 - m') = 0 or 1 without NaN, and
-// masked scores (-inf) give p = 0.
-constexpr float kM0 = -1e30f;
-
-template <int FMT>
-struct QFmt;
-
-// Per format: KLOADS / VLOADS = 16-byte-per-lane K / V loads per 16-token chunk (whole
-// rows), VBYTES = bytes of each of its 4 token rows a lane needs for the PV operand, TILE =
-// bytes of the wave's LDS staging tiles (K rows for INT8 / FP8, then V rows).
-//
-// INT8 / FP8 share the byte layout: K rows of 128 bytes; after the LDS staging (kstage_q)
-// lane (token l%16, g) holds bytes [64j + 16g, +16) for j = 0, 1; k-step st = 2j + u uses
-// dwords 2u, 2u+1, i.e. channels 64*(st/2) + 16g + 8*(st%2) + e in order. V: 8 bytes of
-// each token row per lane (regrouped from whole rows by vstage_i8), tile t = byte t of the
-// lane's 8.
-template <>
-struct QFmt<KVQ_KV_INT8> {
-    static constexpr float F = 16777216.f;  // 2^24
-    static constexpr int KLOADS = 2, VBYTES = 8, VLOADS = 2, TILE = 4608;
-    __device__ static int chan_base(int st, int g) { return 64 * (st >> 1) + 16 * g + 8 * (st & 1); }
-    static constexpr bool permuted() { return false; }
-    __device__ static h8 kop(const u4v* kr, int st) {
-        const u4v x = kr[st >> 1];
-        const uint32_t d0 = x[2 * (st & 1)], d1 = x[2 * (st & 1) + 1];
-        u4v o;
-        o[0] = perm(0u, d0, 0x0C010C00u);
-        o[1] = perm(0u, d0, 0x0C030C02u);
-        o[2] = perm(0u, d1, 0x0C010C00u);
-        o[3] = perm(0u, d1, 0x0C030C02u);
-        return __builtin_bit_cast(h8, o);
-    }
-    // V^T operand dwords: tile t of token pairs (0, 1) and (2, 3) of the lane's 4 rows.
-    __device__ static void vtiles(const uint32_t (*v)[2], uint32_t* a01, uint32_t* a23) {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            a01[t] = pair_bytes(v[0][t >> 2], v[1][t >> 2], t & 3);
-            a23[t] = pair_bytes(v[2][t >> 2], v[3][t >> 2], t & 3);
-        }
-    }
-};
-
-// FP8: gfx950 converts OCP e4m3fn to fp16 exactly in hardware (two codes per
-// v_cvt_scalef32_pk_f16_fp8, scale 1.0), so h = f(c) with F = 1.
-__device__ __forceinline__ uint32_t f8_lo(uint32_t x) {
-    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 1.0f, false));
-}
-__device__ __forceinline__ uint32_t f8_hi(uint32_t x) {
-    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 1.0f, true));
-}
-
-template <>
-struct QFmt<KVQ_KV_FP8_E4M3> {
-    static constexpr float F = 1.f;
-    static constexpr int KLOADS = 2, VBYTES = 8, VLOADS = 2, TILE = 4608;
-    __device__ static int chan_base(int st, int g) { return 64 * (st >> 1) + 16 * g + 8 * (st & 1); }
-    static constexpr bool permuted() { return false; }
-    __device__ static h8 kop(const u4v* kr, int st) {
-        const u4v x = kr[st >> 1];
-        const uint32_t d0 = x[2 * (st & 1)], d1 = x[2 * (st & 1) + 1];
-        u4v o;
-        o[0] = f8_lo(d0);
-        o[1] = f8_hi(d0);
-        o[2] = f8_lo(d1);
-        o[3] = f8_hi(d1);
-        return __builtin_bit_cast(h8, o);
-    }
-    __device__ static void vtiles(const uint32_t (*v)[2], uint32_t* a01, uint32_t* a23) {
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            // bytes [a0, b0, a1, b1] and [a2, b2, a3, b3] of token pairs, two codes per cvt
-            const uint32_t x0 = perm(v[1][k], v[0][k], 0x05010400u);
-            const uint32_t x1 = perm(v[1][k], v[0][k], 0x07030602u);
-            const uint32_t y0 = perm(v[3][k], v[2][k], 0x05010400u);
-            const uint32_t y1 = perm(v[3][k], v[2][k], 0x07030602u);
-            a01[4 * k + 0] = f8_lo(x0);
-            a01[4 * k + 1] = f8_hi(x0);
-            a01[4 * k + 2] = f8_lo(x1);
-            a01[4 * k + 3] = f8_hi(x1);
-            a23[4 * k + 0] = f8_lo(y0);
-            a23[4 * k + 1] = f8_hi(y0);
-            a23[4 * k + 2] = f8_lo(y1);
-            a23[4 * k + 3] = f8_hi(y1);
-        }
-    }
-};
-
-// INT4: K rows of 64 bytes, lane (token, g) loads bytes [16g, +16) (channels [32g, +32));
-// k-step st uses dword st: halves in code order {0,4, 1,5, 2,6, 3,7} of channels 32g + 8st,
-// the odd codes at 2^-20 (w = 16). V: the lane needs 4 bytes (8 codes) of each of its 4
-// token rows; the rows are loaded whole (16 lanes per 1 KB instruction) and regrouped
-// through LDS (vstage_i4). Tiles 2k, 2k + 1 come from byte k of the lane's 4: tile 2k takes
-// the whole byte (code 2k + 16 code 2k+1, a subnormal below 2^-16 - no mask), tile 2k + 1
-// the odd code alone at 2^-20; tile_weights turns the sums back into codes 2k and 2k + 1.
-// One v_perm and one v_and per two tiles of a token pair.
-template <>
-struct QFmt<KVQ_KV_INT4> {
-    static constexpr float F = 16777216.f;  // 2^24
-    static constexpr int KLOADS = 1, VBYTES = 4, VLOADS = 1, TILE = 2048;
-    __device__ static int chan_base(int st, int g) { return 32 * g + 8 * st; }
-    static constexpr bool permuted() { return true; }
-    __device__ static h8 kop(const u4v* kr, int st) {
-        const uint32_t x = kr[0][st], y = x >> 8;
-        u4v o;
-        o[0] = x & 0x000F000Fu;
-        o[1] = x & 0x00F000F0u;
-        o[2] = y & 0x000F000Fu;
-        o[3] = y & 0x00F000F0u;
-        return __builtin_bit_cast(h8, o);
-    }
-    __device__ static void vtiles(const uint32_t (*v)[1], uint32_t* a01, uint32_t* a23) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t x = pair_bytes(v[0][0], v[1][0], k);
-            const uint32_t y = pair_bytes(v[2][0], v[3][0], k);
-            a01[2 * k] = x;
-            a01[2 * k + 1] = x & 0x00F000F0u;
-            a23[2 * k] = y;
-            a23[2 * k + 1] = y & 0x00F000F0u;
-        }
-    }
-};
-
-// Raw codes of one 16-token chunk as held by one lane, the V (scale, zero) pair of token
-// 4g + (l & 3) (vsz, scale in the low half; pv_weights gives every lane of the quad the
-// pairs of all 4 of its tokens 4g .. 4g + 3; for the first chunk of a chunk pair, of the
-// chunk the lane's column holds), and (lane l) the pairs of channels 2l, 2l+1 of the
-// chunk's K group (ksz). The group data is loaded with every chunk that
-// may start a group's use, not only with a group's first one: loads issued on every path
-// keep the compiler's wait counts exact, so no chunk waits for loads it does not use.
-template <int FMT>
-struct ChunkQ {
-    u4v k[QFmt<FMT>::KLOADS];
-    u4v vr[QFmt<FMT>::VLOADS];  // V whole rows (vstage_i4 / vstage_i8 give the layouts)
-    uint32_t vsz;
-    u2 ksz;
-};
-
-// Per-lane byte offsets of a chunk's loads inside its page (the page base and the slot
-// are wave-uniform), `last` = valid tokens - 1 of the chunk:
-//   K, INT4 (64-byte rows): row min(l%16, last) bytes [16g, +16) - one load instruction
-//     covers all 16 rows;
-//   K, INT8 / FP8 (128-byte rows): load j row min(8j + l/8, last), bytes [16(l%8), +16) -
-//     each instruction covers 8 whole rows (every 128-byte line in one instruction); the
-//     rows reach the k-operand layout through the wave's LDS tile (kstage_q);
-//   V, the same whole-row pattern: INT4 row min(l/4, last) bytes [16(l%4), +16); INT8 /
-//     FP8 load j row min(8j + l/8, last) bytes [16(l%8), +16) (regrouped by vstage_*);
-//   the V (scale, zero) pair of token 4g + (l & 3) (4 bytes: the 64 bytes of the chunk's
-//   16 pairs reach the wave once per row of 16 lanes, not once per lane), vs2 the same
-//   token of the chunk pair's chunk (l >> 2) & 1, 64 bytes further for the second chunk,
-//   and the K group's pairs of channels 2l, 2l+1 (8 bytes).
-struct QLaneOff {
-    uint32_t k[2], v[2], vs, vs2, ks;
-};
-
-template <int FMT>
-__device__ __forceinline__ QLaneOff lane_offsets(const DecodeParams& p, int i16, int g,
-                                                 int last) {
-    typedef QFmt<FMT> Q;
-    const int lane = __lane_id();
-    QLaneOff o;
-    if constexpr (Q::KLOADS == 1) {
-        o.k[0] = o.k[1] = (uint32_t)(min(i16, last) * (int)p.k_stok + 16 * g);
-    } else {
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-            o.k[j] = (uint32_t)(min(8 * j + (lane >> 3), last) * (int)p.k_stok + 16 * (lane & 7));
-    }
-    if constexpr (Q::VLOADS == 1) {  // 64-byte rows: 16 per instruction
-        o.v[0] = (uint32_t)(min(lane >> 2, last) * (int)p.v_stok + 16 * (lane & 3));
-    } else {  // 128-byte rows: 8 per instruction
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-            o.v[j] = (uint32_t)(min(8 * j + (lane >> 3), last) * (int)p.v_stok + 16 * (lane & 7));
-    }
-    o.vs = 16 * g + 4 * (lane & 3);
-    o.vs2 = o.vs + 64 * ((lane >> 2) & 1);
-    o.ks = 8 * lane;
-    return o;
-}
-
-// Addressing of one kv head's data, made once per wave: the head's base in each tensor
-// (64-bit) and the strides a chunk's address needs. A chunk's loads go through buffer
-// resources based at its block - base + block * block stride, a 64-bit scalar product, so
-// pools of any size work - with the token slot as one 32-bit scalar offset (soffset) and
-// the lane's 32-bit offset (voffset): a few scalar operations per chunk and no vector
-// address arithmetic. Offsets inside a block are below 2^31 bytes (checked on the host).
-struct QBase {
-    const char* k;   // codes of kv head kvh in block 0
-    const char* v;
-    const char* vs;  // V (scale, zero) pairs of kv head kvh in block 0
-    const char* ks;  // K (scale, zero) pairs of kv head kvh in block 0
-    uint32_t k_sblk, v_sblk, k_stok, v_stok;
-    uint32_t vs_blk, ks_blk;  // bytes per block of the V / K pair tensors
-    uint32_t cmask;           // 16-token chunks per page - 1
-    uint32_t vmask;           // 16-token chunks per V (scale, zero) group - 1
-};
-
-// Buffer resource at a wave-uniform address: stride 0, the full 32-bit range (offsets from
-// it stay below 2^31), dword data format.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const char* base, int phys,
-                                                             uint32_t blk_bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<char*>(base + (uint64_t)(uint32_t)phys * blk_bytes), (short)0, -1, 0x00020000);
-}
-
-// kvh: the caches' kv head (cache_head).
-__device__ __forceinline__ QBase q_base(const DecodeParams& p, int kvh) {
-    const int hkv = p.kv_heads / p.kv_rep;  // the caches' kv heads
-    QBase B;
-    B.k = (const char*)p.k + (int64_t)kvh * p.k_sh;
-    B.v = (const char*)p.v + (int64_t)kvh * p.v_sh;
-    B.vs = (const char*)p.v_scale + ((int64_t)kvh * 4 << p.vg_shift);
-    B.ks = (const char*)p.k_scale + (int64_t)kvh * 4 * 128;
-    B.k_sblk = (uint32_t)p.k_sblk;
-    B.v_sblk = (uint32_t)p.v_sblk;
-    B.k_stok = (uint32_t)p.k_stok;
-    B.v_stok = (uint32_t)p.v_stok;
-    B.vs_blk = (uint32_t)(hkv * 4) << p.vg_shift;
-    B.ks_blk = (uint32_t)(hkv * 4 * 128);
-    B.cmask = (1u << p.cpp_shift) - 1;
-    B.vmask = (1u << (p.vg_shift - 4)) - 1;
-    return B;
-}
-
-// Cache policy of the loads that stream the cache once (codes, V scale/zero): nt, the
-// streaming hint; measured on MI355X it lifts a plain streaming read from about 6.3 to
-// 7.0 TB/s. The K group scales, which every chunk of the group reloads, keep the default
-// policy.
-constexpr int kNT = 2;
-
-// WITH_K: also load the K group's (scale, zero) pairs (ch.ksz), stored with the group's
-// first page `lead`. VS: the V (scale, zero) pairs ch.vsz brings, from the chunk's V group
-// in its first page `vlead`: 1 the chunk's own; 2 those of the chunk pair c, c + 1 (c even,
-// both in one V group: lane l takes chunk c + ((l >> 2) & 1)); 0 none.
-template <int FMT, bool WITH_K = true, int VS = 1>
-__device__ __forceinline__ void load_chunk_q(const QBase& B, int c, const QLaneOff& lo, int phys,
-                                             int lead, int vlead, ChunkQ<FMT>& ch) {
-    typedef QFmt<FMT> Q;
-    const uint32_t slot = ((uint32_t)c & B.cmask) << 4;
-    const auto rk = block_rsrc(B.k, phys, B.k_sblk);
-    const auto rv = block_rsrc(B.v, phys, B.v_sblk);
-#pragma unroll
-    for (int j = 0; j < Q::KLOADS; ++j)
-        ch.k[j] = __builtin_amdgcn_raw_buffer_load_b128(rk, lo.k[j], slot * B.k_stok, kNT);
-#pragma unroll
-    for (int j = 0; j < Q::VLOADS; ++j)
-        ch.vr[j] = __builtin_amdgcn_raw_buffer_load_b128(rv, lo.v[j], slot * B.v_stok, kNT);
-    // V (scale, zero) pair of token 4g + (l & 3) of the chunk (slots past the sequence
-    // hold garbage and are masked by selects, never multiplied); the chunk's 16 pairs sit
-    // at 64 (c & vmask) bytes in its V group
-    if constexpr (VS != 0)
-        ch.vsz = __builtin_amdgcn_raw_buffer_load_b32(block_rsrc(B.vs, vlead, B.vs_blk),
-                                                      VS == 2 ? lo.vs2 : lo.vs,
-                                                      64 * ((uint32_t)c & B.vmask & ~(VS == 2 ? 1u : 0u)),
-                                                      kNT);
-    if constexpr (WITH_K) {
-        ch.ksz = __builtin_bit_cast(
-            u2, __builtin_amdgcn_raw_buffer_load_b64(block_rsrc(B.ks, lead, B.ks_blk), lo.ks, 0, 0));
-    }
-}
-
-// Half-row rotation: lane l reads lane (l & ~15) | ((l + 8) & 15), i.e. column n of a
-// 16-lane row meets column n ^ 8 (DPP row_ror:8).
-__device__ __forceinline__ float ror8(float x) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf,
-                                                      false));
-}
-
-// INT8 / FP8 K rows (16 rows of 128 bytes, loaded 8 whole rows per instruction) to the
-// k-operand layout (lane (tok = l%16, g) holds bytes [64j + 16g, +16) of row tok) through
-// the wave's 2 KB LDS tile. 16-byte piece j of row r sits at slot j ^ (r >> 1): the row
-// writes (16 lanes = 2 rows x 8 pieces) and the operand reads (16 lanes = 16 rows, one
-// piece) each touch 16 distinct 16-byte slots modulo 256 bytes - no bank conflicts.
-__device__ __forceinline__ void kstage_q(const u4v* rows, char* kst, int g, u4v* kr) {
-    const int lane = __lane_id();
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int row = 8 * j + (lane >> 3);
-        *(u4v*)(kst + row * 128 + 16 * ((lane & 7) ^ (row >> 1))) = rows[j];
-    }
-    const int tok = lane & 15;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) kr[j] = *(const u4v*)(kst + tok * 128 + 16 * ((4 * j + g) ^ (tok >> 1)));
-}
-
-// The chunk's K codes in k-operand order.
-template <int FMT>
-__device__ __forceinline__ void k_operand(const ChunkQ<FMT>& ch, char* kst, int g,
-                                          u4v* kr) {
-    if constexpr (QFmt<FMT>::KLOADS == 2) {
-        kstage_q(ch.k, kst, g, kr);
-    } else {
-        kr[0] = ch.k[0];
-    }
-}
-
-// INT4 V rows (16 rows of 64 bytes, lane l holding row l/4, dwords [4(l%4), +4)) to the
-// PV operand's grouping (lane (i16, g) needs dword i16 of rows 4g .. 4g + 3) through the
-// wave's LDS tile. Dword c of row R sits at 80 (R / 4) + 16 (R % 4) + c: the 16-byte row
-// writes and the 4-byte reads (rows 4g + r, column i16: 80g + 16r + i16) each hit distinct
-// banks, so neither conflicts.
-__device__ __forceinline__ void vstage_i4(const u4v* vr, char* vst, int i16, int g,
-                                          uint32_t (*v)[1]) {
-    const int lane = __lane_id();
-    const int row = lane >> 2;
-    uint32_t* t = (uint32_t*)vst;
-    *(u4v*)(t + 80 * (row >> 2) + 16 * (row & 3) + 4 * (lane & 3)) = vr[0];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) v[r][0] = t[80 * g + 16 * r + i16];
-}
-
-// INT8 / FP8 V rows (16 rows of 128 bytes; load j: lane l holds row 8j + l/8, dwords
-// [4(l%8), +4)) to the PV grouping (lane (i16, g) needs dwords 2 i16, 2 i16 + 1 of rows
-// 4g .. 4g + 3) through the wave's 2.5 KB V tile. Dword c of row R sits at
-// 160 (R / 4) + 32 (R % 4) + c: the 8-byte reads of lanes with g and g + 1 fall in opposite
-// halves of 64 banks, the 16-byte writes of 8 lanes cover 32 distinct banks.
-__device__ __forceinline__ void vstage_i8(const u4v* vr, char* vst, int i16, int g,
-                                          uint32_t (*v)[2]) {
-    const int lane = __lane_id();
-    uint32_t* t = (uint32_t*)vst;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int row = 8 * j + (lane >> 3);
-        *(u4v*)(t + 160 * (row >> 2) + 32 * (row & 3) + 4 * (lane & 7)) = vr[j];
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const u2 x = *(const u2*)(t + 160 * g + 32 * r + 2 * i16);
-        v[r][0] = x[0];
-        v[r][1] = x[1];
-    }
-}
-
-// The chunk's V codes grouped by token row as vtiles takes them. The V tile follows the
-// wave's 2 KB K tile for INT8 / FP8 and takes its place for INT4 (no K staging).
-template <int FMT>
-__device__ __forceinline__ void v_rows(const ChunkQ<FMT>& ch, char* kst, int i16, int g,
-                                       uint32_t (*v)[QFmt<FMT>::VBYTES / 4]) {
-    if constexpr (QFmt<FMT>::VLOADS == 1) {
-        vstage_i4(ch.vr, kst, i16, g, v);
-    } else {
-        vstage_i8(ch.vr, kst + 2048, i16, g, v);
-    }
-}
-
-// q'' = q * s / w of the K group whose scales lane l holds for channels 2l, 2l+1 (s2, z2),
-// as hi + lo fp16 parts: hi = fp16(q s') (v_pk_mul_f16), lo = fma(q, s', -hi) rounded once
-// (v_pk_fma_f16: q s' - hi is exact), s' = s / w. For INT4 the odd channels' s / 16 is
-// exact unless it falls below the fp16 normal range, where its error stays under 2^-25 -
-// at most 16 * 15 * 2^-25 |q| (about 7e-6 |q|) in the score. One fp16 rounding of q s
-// alone would move logits by ~1e-3 on outlier channels. The lane keeps the part `lo_part`
-// selects for the head whose q `qsh` points at (q in k-operand order in LDS, 64 h8 apart
-// per k-step). The scales pass through the wave's 512-byte LDS slot `stage` to reach every
-// lane in k-operand order (INT4: written there in the permuted order, two halves per
-// lane). Returns C = sum_d q_d z_d of that head (all 128 channels).
-template <int FMT>
-__device__ __forceinline__ float make_qprime(u2 ksz, uint32_t* stage, int g, const h8* qsh,
-                                             bool lo_part, h8* val) {
-    typedef QFmt<FMT> Q;
-    const int lane = __lane_id();
-    // (s, z) pairs of channels 2l, 2l+1 -> the two scales and the two zeros
-    const uint32_t s2 = perm(ksz[1], ksz[0], 0x05040100u);
-    const uint32_t z2 = perm(ksz[1], ksz[0], 0x07060302u);
-    _Float16* ss = (_Float16*)stage;
-    _Float16* zz = (_Float16*)(stage + 64);
-    if constexpr (Q::permuted()) {
-        // channels 2l (even: w = 1) and 2l + 1 (odd: w = 16) of block l / 4 sit at k-order
-        // positions {0, 4, 1, 5}[l % 4] and {2, 6, 3, 7}[l % 4] of that block
-        h2 sv2 = __builtin_bit_cast(h2, s2);
-        sv2[1] *= (_Float16)0.0625f;
-        const h2 zv2 = __builtin_bit_cast(h2, z2);
-        const int j = lane & 3, blk = 8 * (lane >> 2);
-        const int p0 = blk + ((j & 2) ? 1 : 0) + 4 * (j & 1);
-        const int p1 = p0 + 2;
-        ss[p0] = sv2[0];
-        ss[p1] = sv2[1];
-        zz[p0] = zv2[0];
-        zz[p1] = zv2[1];
-    } else {
-        stage[lane] = s2;
-        stage[64 + lane] = z2;
-    }
-    float qz = 0.f;
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-        const h8 sv = *(const h8*)(ss + Q::chan_base(st, g));
-        const h8 zv = *(const h8*)(zz + Q::chan_base(st, g));
-        const h8 qv = qsh[64 * st];
-        const h8 hi = qv * sv;
-        const h8 lo = __builtin_elementwise_fma(qv, sv, -hi);
-        val[st] = lo_part ? lo : hi;
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-            const h2 qa = {qv[e], qv[e + 1]};
-            const h2 za = {zv[e], zv[e + 1]};
-            qz = __builtin_amdgcn_fdot2(qa, za, qz, false);
-        }
-    }
-    return rows_sum(qz);
-}
-
-// Online-softmax update of one lane for scores s2 (log2 domain, masked scores -inf):
-// rescales the state when a score passes the lazy reference max, returns p = 2^(s2 - m).
-__device__ __forceinline__ void softmax_step(float* s2, SoftmaxState<128>& st, float& corr,
-                                             float* pr) {
-    const float lm = fmaxf(fmaxf(s2[0], s2[1]), fmaxf(s2[2], s2[3]));
-    if (__builtin_amdgcn_ballot_w64(lm > st.m + kLazyMax) != 0) {  // rare: the max moved
-        const float mn = fmaxf(st.m, rows_max(lm));
-        const float alpha = fast_exp2(st.m - mn);
-        st.m = mn;
-        st.l *= alpha;
-        corr *= alpha;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) st.acc[t] *= alpha;
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(s2[r] - st.m);
-    st.l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-}
-
-// p s_t as hi + lo fp16 parts, hi = fp16(p s_t) (fma with +0 is the product: p, s >= 0;
-// v_fma_mix on the fp16 scale) and lo = fp16(p s_t - hi): one fp16 rounding of p s_t
-// would be an error of up to 2^-11 (V - z) when one token dominates. corr accumulates
-// p z_t in fp32. Rows r with !ok (past the sequence: garbage scales) give 0.
-// vsz: lane r of each quad holds the pair of token 4g + r (ChunkQ::vsz); a DPP quad
-// broadcast (quad_perm [r, r, r, r]) hands it to the quad's other lanes. The quad's lanes
-// must all pass the same chunk's vsz.
-template <int R>
-__device__ __forceinline__ uint32_t quad_bcast(uint32_t x) {
-    return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x55 * R, 0xf, 0xf, false);
-}
-
-template <bool MASK>
-__device__ __forceinline__ void pv_weights(const float* pr, uint32_t vsz, int valid, int g,
-                                           h4& phi, h4& plo, float& corr) {
-    const uint32_t pairs[4] = {quad_bcast<0>(vsz), quad_bcast<1>(vsz), quad_bcast<2>(vsz),
-                               quad_bcast<3>(vsz)};
-    float cadd = 0.f;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const bool ok = !MASK || 4 * g + r < valid;
-        const uint32_t pair = pairs[r];
-        const h2 sz = __builtin_bit_cast(h2, pair);
-        const float sv = (float)sz[0];
-        const _Float16 hi = (_Float16)__builtin_fmaf(pr[r], sv, 0.f);
-        phi[r] = ok ? hi : (_Float16)0.f;
-        plo[r] = ok ? (_Float16)__builtin_fmaf(pr[r], sv, -(float)hi) : (_Float16)0.f;
-        cadd = __builtin_fmaf(pr[r], ok ? (float)sz[1] : 0.f, cadd);
-    }
-    corr += cadd;
-}
-
-// One chunk, 5 to 16 q heads per kv head (decode_q_kernel). SPLIT (at most 8 heads): the
-// MFMA's 16 columns hold hi in column h and lo in column h + 8, so one QK^T chain gives
-// both parts (summed across the half rows after the MFMAs) and one PV chain takes p''
-// hi / lo the same way. Otherwise hi and lo run in two chains over columns [0, G).
-template <int FMT, bool MASK, bool SPLIT>
-__device__ __forceinline__ void chunk_q(const ChunkQ<FMT>& ch, const h8* qhi, const h8* qlo,
-                                        float csl, float sl2f, int valid, int g, char* kst,
-                                        SoftmaxState<128>& st, float& corr) {
-    typedef QFmt<FMT> Q;
-    // V regrouped first (INT4: through LDS), so that its latency overlaps the QK product
-    uint32_t vrows[4][Q::VBYTES / 4];
-    v_rows<FMT>(ch, kst, __lane_id() & 15, g, vrows);
-    u4v kr[Q::KLOADS];
-    k_operand<FMT>(ch, kst, g, kr);
-    float s2[4];
-    if constexpr (SPLIT) {
-        f4 sc = (f4)0.f;
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(Q::kop(kr, k), qhi[k], sc, 0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s2[r] = __builtin_fmaf(sc[r] + ror8(sc[r]), sl2f, csl);
-    } else {
-        // hi and lo parts in two independent MFMA chains (half the dependent-chain latency)
-        f4 sh = (f4)0.f, sl = (f4)0.f;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const h8 kh = Q::kop(kr, k);
-            sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qhi[k], sh, 0, 0, 0);
-            sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qlo[k], sl, 0, 0, 0);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s2[r] = __builtin_fmaf(sh[r] + sl[r], sl2f, csl);
-    }
-    if (MASK) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s2[r] = 4 * g + r < valid ? s2[r] : -INFINITY;
-    }
-    float pr[4];
-    softmax_step(s2, st, corr, pr);
-    h4 phi, plo;
-    pv_weights<MASK>(pr, ch.vsz, valid, g, phi, plo, corr);
-    uint32_t a01[8], a23[8];
-    Q::vtiles(vrows, a01, a23);
-    if constexpr (SPLIT) {
-        // column h takes p hi, column h + 8 p lo (the lanes of a pair hold the same p)
-        const h4 pop = (__lane_id() & 8) ? plo : phi;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            u2 w = {a01[t], a23[t]};
-            st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, w), pop,
-                                                               st.acc[t], 0, 0, 0);
-        }
-    } else {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            u2 w = {a01[t], a23[t]};
-            st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, w), phi,
-                                                               st.acc[t], 0, 0, 0);
-        }
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            u2 w = {a01[t], a23[t]};
-            st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, w), plo,
-                                                               st.acc[t], 0, 0, 0);
-        }
-    }
-}
-
-// A chunk pair (chunks a, b) of one K group, 1 to 4 q heads per kv head
-// (decode_q2_kernel). `slot` = the lane column's chunk (0: a, 1: b). Both chunks' QK
-// products run against the same q'' operand (column j: head j & 3, part j >> 3) into two
-// accumulators; each column keeps its own chunk's. csl = C * scale * log2 e of the group.
-// MASK: tokens at or past valid_a / valid_b of their chunk are masked (valid_b = 0: no
-// second chunk).
-template <int FMT, bool MASK>
-__device__ __forceinline__ void chunk_pair(const ChunkQ<FMT>& ca, const ChunkQ<FMT>& cb,
-                                           const h8* qv, float csl, float sl2f, int valid_a,
-                                           int valid_b, int g, int slot, bool lo_part,
-                                           char* kst, SoftmaxState<128>& st, float& corr) {
-    typedef QFmt<FMT> Q;
-    // V regrouped first (INT4: through LDS), so that its latency overlaps the QK products
-    uint32_t va[4][Q::VBYTES / 4], vb[4][Q::VBYTES / 4];
-    v_rows<FMT>(ca, kst, __lane_id() & 15, g, va);
-    v_rows<FMT>(cb, kst, __lane_id() & 15, g, vb);
-    f4 sa = (f4)0.f, sb = (f4)0.f;
-    {
-        u4v kr[Q::KLOADS];
-        k_operand<FMT>(ca, kst, g, kr);
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(Q::kop(kr, k), qv[k], sa, 0, 0, 0);
-        k_operand<FMT>(cb, kst, g, kr);
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(Q::kop(kr, k), qv[k], sb, 0, 0, 0);
-    }
-    float s2[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const float x = slot ? sb[r] : sa[r];
-        s2[r] = __builtin_fmaf(x + ror8(x), sl2f, csl);
-    }
-    const int valid = slot ? valid_b : valid_a;
-    if (MASK) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s2[r] = 4 * g + r < valid ? s2[r] : -INFINITY;
-    }
-    float pr[4];
-    softmax_step(s2, st, corr, pr);
-    const uint32_t vsz = ca.vsz;  // the pairs of the lane's own chunk (load_chunk_q VS 2)
-    h4 phi, plo;
-    pv_weights<MASK>(pr, vsz, valid, g, phi, plo, corr);
-    // B operand: k-slots 8g + r (chunk a's token 4g + r) and 8g + 4 + r (chunk b's); the
-    // lane's p in its chunk's half, zeros in the other
-    const u2 pw = __builtin_bit_cast(u2, lo_part ? plo : phi);
-    u4v pbw;
-    pbw[0] = slot ? 0u : pw[0];
-    pbw[1] = slot ? 0u : pw[1];
-    pbw[2] = slot ? pw[0] : 0u;
-    pbw[3] = slot ? pw[1] : 0u;
-    const h8 pb = __builtin_bit_cast(h8, pbw);
-    uint32_t a01[8], a23[8], b01[8], b23[8];
-    Q::vtiles(va, a01, a23);
-    Q::vtiles(vb, b01, b23);
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        const u4v w = {a01[t], a23[t], b01[t], b23[t]};
-        st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, w), pb,
-                                                           st.acc[t], 0, 0, 0);
-    }
-}
-
-// INT4 V tiles: tile 2k sums p'' (c_2k + 16 c_2k+1), tile 2k + 1 sums p'' 16 c_2k+1 (both in
-// units of 2^-24). Code 2k's sum is their difference and code 2k + 1's a sixteenth of the
-// second. The difference cancels at most 255 / 15 of the magnitude: the fp32 accumulators'
-// rounding stays below 2^-24 * 255 * sum p'', about 1.5e-5 of the largest V value.
-template <int FMT>
-__device__ __forceinline__ void tile_weights(SoftmaxState<128>& st) {
-    if constexpr (FMT == KVQ_KV_INT4) {
-#pragma unroll
-        for (int t = 0; t < 8; t += 2) {
-            st.acc[t] -= st.acc[t + 1];
-            st.acc[t + 1] *= 0.0625f;
-        }
-    }
-}
-
-// Writes q in this format's k-operand order (zero for heads >= G) to LDS for the
-// once-per-K-group q'' products: [4 k-steps][64 lanes] h8, lane (g, head i16).
-template <int FMT>
-__device__ __forceinline__ void stage_q(const DecodeParams& p, int b, int kvh, int i16, int g,
-                                        h8* qsh) {
-    typedef QFmt<FMT> Q;
-    const int G = p.group;
-    const bool head_ok = i16 < G;
-    const _Float16* qrow = (const _Float16*)p.q + (int64_t)b * p.q_sb +
-                           (int64_t)(kvh * G + (head_ok ? i16 : 0)) * p.q_sh;
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-        h8 x = *(const h8*)(qrow + Q::chan_base(st, g));
-        if constexpr (Q::permuted()) x = __builtin_shufflevector(x, x, 0, 4, 1, 5, 2, 6, 3, 7);
-        qsh[64 * st + __lane_id()] = head_ok ? x : (h8)(_Float16)0;
-    }
-}
-
-// P-deep register ring: chunk c + P is loaded while chunk c computes, the block-table
-// entries of chunks c + 2P .. c + 3P - 1 meanwhile. Every chunk carries its own K group's
-// scales, so any group size works with any P. 5 to 16 q heads per kv head.
-//
-// q_range runs one wave's chunk range [w_lo, w_hi) of sequence b (of length seq_len) for
-// kv head kvh and stores the workgroup's result (partial rows part_base + h * part_stride,
-// or the output row for FINAL).
-template <int FMT, int W, bool FINAL, int P, bool SPLIT>
-__device__ __forceinline__ void q_range(const DecodeParams& p, int kvh, int b, int seq_len,
-                                        int w_lo, int w_hi, int wave, int64_t part_base,
-                                        int64_t part_stride) {
-    typedef QFmt<FMT> Q;
-    constexpr int D = 128, DV = 8;
-    const int lane = threadIdx.x & 63;
-    const int i16 = lane & 15, g = lane >> 4;
-    const int G = p.group;
-    const int c_full = seq_len >> 4;  // chunks below this index are fully valid
-    const int kgs = p.k_group_shift;  // log2 of 16-token chunks per K group
-    const int vgs = p.vg_shift - 4;   // log2 of 16-token chunks per V (scale, zero) group
-    const QBase base = q_base(p, cache_head(p, kvh));
-
-    // LDS: [region 0][K-scale slots, 512 B per wave][q, 4 KB] (launch_q). Region 0 holds
-    // the cross-wave combine after the chunk loop and, before it, the waves' staging tiles
-    // (Q::TILE bytes each: INT8 / FP8 K and V rows, INT4 V rows).
-    extern __shared__ float smem[];
-    const int r0 = quant_lds_region0(W, G, FMT);
-    char* kst = (char*)smem + wave * Q::TILE;
-    h8* qsh = (h8*)(smem + r0 + W * 128);
-    if (wave == 0) stage_q<FMT>(p, b, kvh, i16, g, qsh);
-    __syncthreads();
-    qsh += SPLIT ? (lane & ~8) : lane;  // SPLIT: columns h and h + 8 read head h
-
-    SoftmaxState<D> st;
-#pragma unroll
-    for (int t = 0; t < DV; ++t) st.acc[t] = (f4)0.f;
-    st.m = kM0;
-    st.l = 0.f;
-    float corr = 0.f, csl = 0.f;
-    const float sl2 = p.scale_log2, sl2f = sl2 * Q::F;
-    h8 qhi[4], qlo[4];
-    const bool upper = SPLIT && (lane & 8);
-
-    uint32_t* stage = (uint32_t*)(smem + r0) + wave * 128;
-    auto valid_of = [&](int c) { return min(seq_len - (c << 4), 16); };
-    // q'' of chunk ch's K group into the operands (hi / lo by column in SPLIT; both chains
-    // otherwise) and C * scale * log2 e into csl
-    auto new_group = [&](const ChunkQ<FMT>& ch) {
-        h8 v[4];
-        if constexpr (SPLIT) {
-            csl = make_qprime<FMT>(ch.ksz, stage, g, qsh, upper, v) * sl2;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) qhi[k] = v[k];
-        } else {
-            csl = make_qprime<FMT>(ch.ksz, stage, g, qsh, false, qhi) * sl2;
-            make_qprime<FMT>(ch.ksz, stage, g, qsh, true, qlo);
-        }
-    };
-
-    // The ring covers the wave's fully valid chunks [w_lo, r_hi); the sequence's partial
-    // last chunk (at most one per sequence) is handled once after it. Every load in the
-    // ring is issued on every path (chunks past r_hi - 1 re-read chunk r_hi - 1 and are
-    // never used), so each wait counts exactly the loads still in flight behind it.
-    const int r_hi = min(w_hi, c_full);
-    const int gmask = (1 << kgs) - 1;
-    if (w_lo < r_hi) {
-        const QLaneOff lo = lane_offsets<FMT>(p, i16, g, 15);
-        const int last = r_hi - 1;
-        ChunkQ<FMT> ring[P];
-        int pg_cur = chunk_pages<P>(p, b, w_lo, last, kgs, vgs);
-        int pg_nxt = chunk_pages<P>(p, b, w_lo + P, last, kgs, vgs);
-        // Issued slot by slot: a slot's loads moved behind a later slot's would make the
-        // ring's waits (vmcnt counts the loads issued after the awaited one) drain it.
-#pragma unroll
-        for (int i = 0; i < P; ++i) {
-            load_chunk_q<FMT>(base, min(w_lo + i, last), lo,
-                              __builtin_amdgcn_readlane(pg_cur, i),
-                              __builtin_amdgcn_readlane(pg_cur, P + i),
-                              __builtin_amdgcn_readlane(pg_cur, 2 * P + i), ring[i]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        for (int c0 = w_lo; c0 < r_hi; c0 += P) {
-            pg_cur = pg_nxt;  // pages of chunks c0 + P .. c0 + 2P - 1
-            pg_nxt = chunk_pages<P>(p, b, c0 + 2 * P, last, kgs, vgs);
-#pragma unroll
-            for (int i = 0; i < P; ++i) {
-                const int c = c0 + i;
-                if (c < r_hi) {
-                    if (c == w_lo || (c & gmask) == 0) new_group(ring[i]);
-                    chunk_q<FMT, false, SPLIT>(ring[i], qhi, qlo, csl, sl2f, 16, g, kst, st, corr);
-                }
-                load_chunk_q<FMT>(base, min(c + P, last), lo,
-                                  __builtin_amdgcn_readlane(pg_cur, i),
-                                  __builtin_amdgcn_readlane(pg_cur, P + i),
-                                  __builtin_amdgcn_readlane(pg_cur, 2 * P + i), ring[i]);
-            }
-        }
-    }
-    if (w_lo <= r_hi && r_hi < w_hi) {  // this wave owns the partial last chunk c_full
-        const int c = r_hi;
-        const int valid = valid_of(c);
-        const int pg = chunk_pages<1>(p, b, c, c, kgs, vgs);
-        ChunkQ<FMT> ch;
-        load_chunk_q<FMT>(base, c, lane_offsets<FMT>(p, i16, g, valid - 1),
-                          __builtin_amdgcn_readlane(pg, 0), __builtin_amdgcn_readlane(pg, 1),
-                          __builtin_amdgcn_readlane(pg, 2), ch);
-        if (c == w_lo || (c & gmask) == 0) new_group(ch);
-        chunk_q<FMT, true, SPLIT>(ch, qhi, qlo, csl, sl2f, valid, g, kst, st, corr);
-    }
-
-    if constexpr (SPLIT) {  // add the lo columns into the hi columns
-#pragma unroll
-        for (int t = 0; t < DV; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) st.acc[t][r] += ror8(st.acc[t][r]);
-    }
-    tile_weights<FMT>(st);
-    __syncthreads();  // every wave is done with its LDS staging tile
-    combine_store<D, W, FINAL>(p, st.acc, Q::F, rows_sum(corr), st.m, rows_sum(st.l), wave, i16,
-                               g, kvh, b, part_base, part_stride);
-}
-
-// Split-KV stage 1 / single pass: workgroup = (kv head, split, sequence), W waves.
-template <int FMT, int W, bool FINAL, int P, bool SPLIT>
-__global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) {
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const WgCoord wc = wg_coord(p, FINAL ? 1 : p.num_splits);
-    if (!wc.live) return;
-    const WaveRange wr = wave_range<W>(p, wc.b, wc.split, wave);
-    q_range<FMT, W, FINAL, P, SPLIT>(p, wc.kvh, wc.b, wr.seq_len, wr.w_lo, wr.w_hi, wave,
-                                     split_part_base(p, wc.b, wc.split), p.num_splits);
-}
-
-// Chunk pairs, 1 to 4 q heads per kv head, K groups of at least 2 chunks. Pairs are
-// (2i, 2i + 1) in absolute chunk index, so both chunks of a pair share their K group; a
-// wave's odd leading chunk, odd trailing full chunk and the sequence's partial last chunk
-// run as single-chunk steps. P-deep ring over the pairs (P = 4 or 8 chunks: while a pair
-// computes, P - 2 chunks are in flight); the ring depth never changes the arithmetic.
-template <int FMT, int W, bool FINAL, int P>
-__device__ __forceinline__ void q2_range(const DecodeParams& p, int kvh, int b, int seq_len,
-                                         int w_lo, int w_hi, int wave, int64_t part_base,
-                                         int64_t part_stride) {
-    static_assert(P == 4 || P == 8, "a pair computes while P - 2 chunks are in flight");
-    typedef QFmt<FMT> Q;
-    constexpr int D = 128, DV = 8;
-    const int lane = threadIdx.x & 63;
-    const int i16 = lane & 15, g = lane >> 4;
-    const int G = p.group;
-    const int slot = (i16 >> 2) & 1;   // the column's chunk of the pair
-    const bool lo_part = i16 >= 8;     // the column holds the lo parts
-    const int c_full = seq_len >> 4;
-    const int kgs = p.k_group_shift;
-    const int vgs = p.vg_shift - 4;
-    const QBase base = q_base(p, cache_head(p, kvh));
-
-    extern __shared__ float smem[];
-    const int r0 = quant_lds_region0(W, G, FMT);
-    char* kst = (char*)smem + wave * Q::TILE;
-    h8* qsh = (h8*)(smem + r0 + W * 128);
-    if (wave == 0) stage_q<FMT>(p, b, kvh, i16, g, qsh);
-    __syncthreads();
-    qsh += (lane & 48) | (lane & 3);  // column j reads head j & 3
-    uint32_t* stage = (uint32_t*)(smem + r0) + wave * 128;
-
-    SoftmaxState<D> st;
-#pragma unroll
-    for (int t = 0; t < DV; ++t) st.acc[t] = (f4)0.f;
-    st.m = kM0;
-    st.l = 0.f;
-    float corr = 0.f, csl = 0.f;
-    const float sl2 = p.scale_log2, sl2f = sl2 * Q::F;
-    h8 qv[4];
-    int gq = -1;  // the K group whose q'' qv holds
-
-    auto group = [&](const ChunkQ<FMT>& ch, int gi) {
-        if (gi != gq) {
-            csl = make_qprime<FMT>(ch.ksz, stage, g, qsh, lo_part, qv) * sl2;
-            gq = gi;
-        }
-    };
-    // chunk c alone (in the first chunk's columns), its first `valid` tokens
-    auto single = [&](int c, int valid) {
-        const int pg = chunk_pages<1>(p, b, c, c, kgs, vgs);
-        ChunkQ<FMT> ch;
-        load_chunk_q<FMT>(base, c, lane_offsets<FMT>(p, i16, g, valid - 1),
-                          __builtin_amdgcn_readlane(pg, 0), __builtin_amdgcn_readlane(pg, 1),
-                          __builtin_amdgcn_readlane(pg, 2), ch);
-        group(ch, c >> kgs);
-        chunk_pair<FMT, true>(ch, ch, qv, csl, sl2f, valid, 0, g, slot, lo_part, kst, st, corr);
-    };
-
-    const int r_hi = min(w_hi, c_full);  // fully valid chunks [w_lo, r_hi)
-    int c_first = w_lo;
-    if ((w_lo & 1) && w_lo < r_hi) {
-        single(w_lo, 16);
-        c_first = w_lo + 1;
-    }
-    // pairs [c_first, e_hi); an empty wave or split has r_hi < w_lo and runs nothing
-    const int e_hi = c_first + (max(r_hi - c_first, 0) & ~1);
-    if (c_first < e_hi) {
-        const QLaneOff lo = lane_offsets<FMT>(p, i16, g, 15);
-        const int last = e_hi - 1;
-        ChunkQ<FMT> ring[P];
-        int pg_cur = chunk_pages<P>(p, b, c_first, last, kgs, vgs);
-        int pg_nxt = chunk_pages<P>(p, b, c_first + P, last, kgs, vgs);
-        // Issued slot by slot: a slot's loads moved behind a later slot's would make the
-        // ring's waits (vmcnt counts the loads issued after the awaited one) drain it.
-        // a pair's K group is its first chunk's: odd slots skip the K pair load
-#pragma unroll
-        for (int i = 0; i < P; ++i) {
-            if (i % 2 == 0)
-                load_chunk_q<FMT, true, 2>(base, min(c_first + i, last), lo,
-                                           __builtin_amdgcn_readlane(pg_cur, i),
-                                           __builtin_amdgcn_readlane(pg_cur, P + i),
-                                           __builtin_amdgcn_readlane(pg_cur, 2 * P + i), ring[i]);
-            else
-                load_chunk_q<FMT, false, 0>(base, min(c_first + i, last), lo,
-                                            __builtin_amdgcn_readlane(pg_cur, i), 0, 0, ring[i]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        for (int c0 = c_first; c0 < e_hi; c0 += P) {
-            pg_cur = pg_nxt;
-            pg_nxt = chunk_pages<P>(p, b, c0 + 2 * P, last, kgs, vgs);
-#pragma unroll
-            for (int i = 0; i < P; i += 2) {
-                const int c = c0 + i;
-                if (c < e_hi) {
-                    group(ring[i], c >> kgs);
-                    chunk_pair<FMT, false>(ring[i], ring[i + 1], qv, csl, sl2f, 16, 16, g, slot,
-                                           lo_part, kst, st, corr);
-                }
-                load_chunk_q<FMT, true, 2>(base, min(c0 + i + P, last), lo,
-                                           __builtin_amdgcn_readlane(pg_cur, i),
-                                           __builtin_amdgcn_readlane(pg_cur, P + i),
-                                           __builtin_amdgcn_readlane(pg_cur, 2 * P + i), ring[i]);
-                load_chunk_q<FMT, false, 0>(base, min(c0 + i + 1 + P, last), lo,
-                                            __builtin_amdgcn_readlane(pg_cur, i + 1), 0, 0,
-                                            ring[i + 1]);
-            }
-        }
-    }
-    if (e_hi < r_hi) single(e_hi, 16);
-    if (w_lo <= r_hi && r_hi < w_hi)  // this wave owns the partial last chunk c_full
-        single(r_hi, min(seq_len - (r_hi << 4), 16));
-
-    // hi + lo columns, then the two chunk streams of each head (columns j, j ^ 4)
-#pragma unroll
-    for (int t = 0; t < DV; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) st.acc[t][r] += ror8(st.acc[t][r]);
-    {
-        const float m_o = __shfl_xor(st.m, 4), l_o = __shfl_xor(st.l, 4);
-        const float c_o = __shfl_xor(corr, 4);
-        const float M = fmaxf(st.m, m_o);
-        const float wa = fast_exp2(st.m - M), wb = fast_exp2(m_o - M);
-        st.l = wa * st.l + wb * l_o;
-        corr = wa * corr + wb * c_o;
-#pragma unroll
-        for (int t = 0; t < DV; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                st.acc[t][r] = wa * st.acc[t][r] + wb * __shfl_xor(st.acc[t][r], 4);
-        st.m = M;
-    }
-    tile_weights<FMT>(st);
-    __syncthreads();  // every wave is done with its LDS staging tile
-    combine_store<D, W, FINAL>(p, st.acc, Q::F, rows_sum(corr), st.m, rows_sum(st.l), wave, i16,
-                               g, kvh, b, part_base, part_stride);
-}
-
-template <int FMT, int W, bool FINAL, int P>
-__global__ __launch_bounds__(W * 64) void decode_q2_kernel(const DecodeParams p) {
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const WgCoord wc = wg_coord(p, FINAL ? 1 : p.num_splits);
-    if (!wc.live) return;
-    const WaveRange wr = wave_range<W>(p, wc.b, wc.split, wave);
-    q2_range<FMT, W, FINAL, P>(p, wc.kvh, wc.b, wr.seq_len, wr.w_lo, wr.w_hi, wave,
-                               split_part_base(p, wc.b, wc.split), p.num_splits);
-}
-
-// Work units (decode_common.h UnitSpace): workgroup = (kv head, unit), W waves running
-// one segment per sequence the unit's chunk range overlaps, each wave a contiguous share
-// of it; PAIRS selects the chunk-pair kernel.
-template <int FMT, int W, int P, bool PAIRS, bool SPLIT>
-__global__ __launch_bounds__(W * 64) void decode_q_units_kernel(const DecodeParams p) {
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    for_unit_segments<W>(p, [&](int kvh, int b, int seq_len, int w_lo, int w_hi, int64_t base,
-                                int64_t stride) {
-        if constexpr (PAIRS)
-            q2_range<FMT, W, false, P>(p, kvh, b, seq_len, w_lo, w_hi, wave, base, stride);
-        else
-            q_range<FMT, W, false, P, SPLIT>(p, kvh, b, seq_len, w_lo, w_hi, wave, base,
-                                             stride);
-    });
-}
-
-// LDS: region 0 (the cross-wave combine, or the waves' 2 KB staging tiles), one 512-byte K-scale
-// slot per wave, then q in k-operand order (4 KB)
-template <int W>
-static size_t q_shmem(const DecodeParams& p, int fmt) {
-    return sizeof(float) * (quant_lds_region0(W, p.group, fmt) + W * 128) + 4096;
-}
-
-template <int FMT, int W, bool FINAL, int P, bool SPLIT>
-static hipError_t launch_q(const DecodeParams& p, hipStream_t stream) {
-    const dim3 grid(decode_grid(p.xcd_group, p.kv_heads, FINAL ? 1 : p.num_splits, p.batch));
-    hipLaunchKernelGGL((decode_q_kernel<FMT, W, FINAL, P, SPLIT>), grid, dim3(W * 64),
-                       q_shmem<W>(p, FMT), stream, p);
-    return hipGetLastError();
-}
-
-template <int FMT, int W, bool FINAL, int P>
-static hipError_t launch_q2(const DecodeParams& p, hipStream_t stream) {
-    const dim3 grid(decode_grid(p.xcd_group, p.kv_heads, FINAL ? 1 : p.num_splits, p.batch));
-    hipLaunchKernelGGL((decode_q2_kernel<FMT, W, FINAL, P>), grid, dim3(W * 64),
-                       q_shmem<W>(p, FMT), stream, p);
-    return hipGetLastError();
-}
-
-// 1 to 4 heads per kv head and K groups of at least 2 chunks: chunk pairs, ring 1 or 2 ->
-// 4 chunks, 4 -> 8. Up to 8 heads otherwise: hi / lo parts in the two column halves of
-// one MFMA chain, any ring depth. 9 to 16 heads: two chains, ring depth 4.
-template <int FMT, bool FINAL, int W>
-static hipError_t launch_q_g(const DecodeParams& p, int ring, hipStream_t stream) {
-    // pair kernel: ring 4 -> 8 chunks in flight, else 4 (a pair computes while P - 2 load);
-    // single-chunk kernel: the ring depth as given (two chains above 8 heads: 4)
-    if (p.group <= 4 && p.k_group_chunks >= 2)
-        return ring == 4 ? launch_q2<FMT, W, FINAL, 8>(p, stream)
-                         : launch_q2<FMT, W, FINAL, 4>(p, stream);
-    if (p.group > 8) return launch_q<FMT, W, FINAL, 4, false>(p, stream);
-    switch (ring) {
-        case 1: return launch_q<FMT, W, FINAL, 1, true>(p, stream);
-        case 2: return launch_q<FMT, W, FINAL, 2, true>(p, stream);
-        case 4: return launch_q<FMT, W, FINAL, 4, true>(p, stream);
+hipError_t launch_decode_q_units(const DecodeParams& p, int kv_format, int head_dim, int waves,
+                                 int ring, hipStream_t stream) {
+    switch (head_dim) {
+        case 64: return launch_decode_q_units_hd64(p, kv_format, waves, ring, stream);
+        case 128: return launch_decode_q_units_hd128(p, kv_format, waves, ring, stream);
+        case 256: return launch_decode_q_units_hd256(p, kv_format, waves, ring, stream);
         default: return hipErrorInvalidValue;
     }
-}
-
-template <int FMT, bool FINAL>
-static hipError_t launch_q_w(const DecodeParams& p, int waves, int ring, hipStream_t stream) {
-    if (ring != 1 && ring != 2 && ring != 4) return hipErrorInvalidValue;
-    switch (waves) {
-        case 1: return launch_q_g<FMT, FINAL, 1>(p, ring, stream);
-        case 2: return launch_q_g<FMT, FINAL, 2>(p, ring, stream);
-        case 4: return launch_q_g<FMT, FINAL, 4>(p, ring, stream);
-        case 8: return launch_q_g<FMT, FINAL, 8>(p, ring, stream);
-        default: return hipErrorInvalidValue;
-    }
-}
-
-// Work units: the kernel variant launch_q_g picks, for W-wave workgroups.
-template <int FMT, int W, int P, bool PAIRS, bool SPLIT>
-static hipError_t launch_qu(const DecodeParams& p, hipStream_t stream) {
-    hipLaunchKernelGGL((decode_q_units_kernel<FMT, W, P, PAIRS, SPLIT>),
-                       dim3((unsigned)(p.kv_heads * p.units)), dim3(W * 64), q_shmem<W>(p, FMT),
-                       stream, p);
-    return hipGetLastError();
-}
-
-template <int FMT, int W>
-static hipError_t launch_q_units_w(const DecodeParams& p, int ring, hipStream_t stream) {
-    if (p.group <= 4 && p.k_group_chunks >= 2)
-        return ring == 4 ? launch_qu<FMT, W, 8, true, false>(p, stream)
-                         : launch_qu<FMT, W, 4, true, false>(p, stream);
-    if (p.group > 8) return launch_qu<FMT, W, 4, false, false>(p, stream);
-    switch (ring) {
-        case 1: return launch_qu<FMT, W, 1, false, true>(p, stream);
-        case 2: return launch_qu<FMT, W, 2, false, true>(p, stream);
-        case 4: return launch_qu<FMT, W, 4, false, true>(p, stream);
-        default: return hipErrorInvalidValue;
-    }
-}
-
-template <int FMT>
-static hipError_t launch_q_units(const DecodeParams& p, int waves, int ring,
-                                 hipStream_t stream) {
-    switch (waves) {
-        case 1: return launch_q_units_w<FMT, 1>(p, ring, stream);
-        case 2: return launch_q_units_w<FMT, 2>(p, ring, stream);
-        case 4: return launch_q_units_w<FMT, 4>(p, ring, stream);
-        default: return hipErrorInvalidValue;
-    }
-}
-
-hipError_t launch_decode_q_units(const DecodeParams& p, int kv_format, int waves, int ring,
-                                 hipStream_t stream) {
-    switch (kv_format) {
-        case KVQ_KV_INT8: return launch_q_units<KVQ_KV_INT8>(p, waves, ring, stream);
-        case KVQ_KV_FP8_E4M3: return launch_q_units<KVQ_KV_FP8_E4M3>(p, waves, ring, stream);
-        case KVQ_KV_INT4: return launch_q_units<KVQ_KV_INT4>(p, waves, ring, stream);
-        default: return hipErrorInvalidValue;
-    }
-}
-
-template <int FMT>
-static hipError_t launch_q_f(const DecodeParams& p, bool final_out, int waves, int ring,
-                             hipStream_t stream) {
-    return final_out ? launch_q_w<FMT, true>(p, waves, ring, stream)
-                     : launch_q_w<FMT, false>(p, waves, ring, stream);
 }
 
 hipError_t launch_decode_q(const DecodeParams& p, int kv_format, int head_dim, bool final_out,
                            int waves, int ring, hipStream_t stream) {
-    if (head_dim != 128) return hipErrorInvalidValue;
-    switch (kv_format) {
-        case KVQ_KV_INT8: return launch_q_f<KVQ_KV_INT8>(p, final_out, waves, ring, stream);
-        case KVQ_KV_FP8_E4M3:
-            return launch_q_f<KVQ_KV_FP8_E4M3>(p, final_out, waves, ring, stream);
-        case KVQ_KV_INT4: return launch_q_f<KVQ_KV_INT4>(p, final_out, waves, ring, stream);
+    switch (head_dim) {
+        case 64: return launch_decode_q_hd64(p, kv_format, final_out, waves, ring, stream);
+        case 128: return launch_decode_q_hd128(p, kv_format, final_out, waves, ring, stream);
+        case 256: return launch_decode_q_hd256(p, kv_format, final_out, waves, ring, stream);
         default: return hipErrorInvalidValue;
     }
 }

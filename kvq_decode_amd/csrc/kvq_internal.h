@@ -49,29 +49,39 @@ struct DecodeParams {
 hipError_t launch_decode(const DecodeParams& p, int kv_format, int head_dim, bool final_out,
                          int waves_per_group, int pipeline, hipStream_t stream);
 
-// Floats of LDS region 0 of the quantized decode kernel (decode_q.hip) with `waves` waves
-// per workgroup: the cross-wave combine ([waves][group][128] accumulators + [waves][16] m
-// and l), or the waves' staging tiles if larger (INT8 / FP8: a 2 KB K tile and a 2.5 KB V
-// tile, 4608 bytes per wave; INT4: a V tile in 2 KB per wave; the tiles are used before
-// the combine).
-__host__ __device__ inline int quant_lds_region0(int waves, int group, int kv_format) {
-    const int combine = waves * group * 128 + 2 * waves * 16;
-    const int tiles = waves * (kv_format == KVQ_KV_INT4 ? 512 : 1152);
+// Floats of LDS region 0 of the quantized decode kernels (decode_q_impl.h) with `waves`
+// waves per workgroup and head dim `head_dim`: the cross-wave combine ([waves][group]
+// [head_dim] accumulators + [waves][16] m and l), or the waves' staging tiles if larger
+// (INT8 / FP8: a 16 head_dim-byte K tile and a 20 head_dim-byte V tile per wave; INT4: a V
+// tile in 16 head_dim bytes per wave; the tiles are used before the combine).
+__host__ __device__ inline int quant_lds_region0(int waves, int group, int kv_format,
+                                                 int head_dim) {
+    const int combine = waves * group * head_dim + 2 * waves * 16;
+    const int tiles = waves * head_dim * (kv_format == KVQ_KV_INT4 ? 4 : 9);
     return combine > tiles ? combine : tiles;
 }
 
-// Stage 1 of the work units for the quantized formats (decode_q.hip); head_dim 128.
-hipError_t launch_decode_q_units(const DecodeParams& p, int kv_format, int waves, int ring,
-                                 hipStream_t stream);
-
-// Quantized formats (decode_q.hip); head_dim 128 only.
-// `ring` = chunks of loads in flight per wave: 1, 2 or 4.
+// Quantized formats (decode_q_impl.h), head_dim 64, 128 or 256: stage 1 of the work units
+// and the split / single-pass kernels. `ring` = chunks of loads in flight per wave: 1, 2 or
+// 4 (head_dim 256: 1 or 2). Each head dim's kernels sit in a translation unit of their own
+// (decode_q_d64.hip, decode_q.hip, decode_q_d256.hip).
+hipError_t launch_decode_q_units(const DecodeParams& p, int kv_format, int head_dim, int waves,
+                                 int ring, hipStream_t stream);
 hipError_t launch_decode_q(const DecodeParams& p, int kv_format, int head_dim, bool final_out,
                            int waves_per_group, int ring, hipStream_t stream);
+#define KVQ_DECL_QHD(D)                                                                       \
+    hipError_t launch_decode_q_hd##D(const DecodeParams& p, int kv_format, bool final_out,    \
+                                     int waves, int ring, hipStream_t stream);               \
+    hipError_t launch_decode_q_units_hd##D(const DecodeParams& p, int kv_format, int waves,  \
+                                           int ring, hipStream_t stream);
+KVQ_DECL_QHD(64)
+KVQ_DECL_QHD(128)
+KVQ_DECL_QHD(256)
+#undef KVQ_DECL_QHD
 
 // Work units (decode_common.h UnitSpace): stage 1 over p.units units per kv head of
 // `waves`-wave workgroups, and the merge of each sequence's partial rows into p.out.
-// Batch at most kUnitMaxBatch; quantized formats head_dim 128.
+// Batch at most kUnitMaxBatch.
 constexpr int kUnitMaxBatch = 1024;  // a multiple of 64
 hipError_t launch_decode_units(const DecodeParams& p, int kv_format, int head_dim, int waves,
                                int ring, hipStream_t stream);

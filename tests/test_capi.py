@@ -319,6 +319,26 @@ def test_quantized_tuning_limits():
         assert L.kvq_decode_single(ctypes.byref(a), None) == _lib.KVQ_ERR_UNSUPPORTED, field
 
 
+def test_quantized_head_dims():
+    """Quantized caches: head_dim 64, 128 or 256 (fp16 takes 32-256); head_dim 256 takes
+    rings of 1 or 2 chunks. A call whose arguments pass the checks reaches the split-count
+    check (KVQ_ERR_SPLITS for num_splits 0)."""
+    L = _lib.lib()
+    op, lse = 1 << 41, 1 << 42
+    for fmt in (1, 2, 3):
+        for D, want in ((32, _lib.KVQ_ERR_UNSUPPORTED), (64, _lib.KVQ_ERR_SPLITS),
+                        (128, _lib.KVQ_ERR_SPLITS), (256, _lib.KVQ_ERR_SPLITS)):
+            a = good_args()
+            a.kv_format = fmt
+            set_scale_pairs(a)
+            a.head_dim, a.q_stride_b, a.q_stride_h = D, 32 * D, D
+            a.o_stride_b, a.o_stride_h = 32 * D, D
+            assert L.kvq_decode_split(ctypes.byref(a), 0, 4, op, lse, None) == want, (fmt, D)
+        a.pipeline = 4  # head_dim 256
+        assert L.kvq_decode_split(ctypes.byref(a), 4, 16, op, lse, None) == \
+            _lib.KVQ_ERR_UNSUPPORTED, fmt
+
+
 def test_fp16_ring_depth_limits():
     """fp16: ring depth 1, 2 or 4 up to head_dim 128; head_dim 256 takes 1 or 2."""
     L = _lib.lib()
