@@ -28,10 +28,10 @@
 // Two kernels:
 //   decode_q2_kernel (1 to 4 q heads per kv head): the 16 MFMA columns hold 2 chunks x
 //     4 heads x {hi, lo}. Column j: head j & 3, chunk (j >> 2) & 1 of the pair, part j >> 3.
-//     The QK product runs the 4 k-steps of both chunks into one accumulator against
-//     block-masked Q operands (zero in the other chunk's columns), so one softmax pass
-//     covers 32 tokens, and the PV product contracts both chunks in one 16x16x32 MFMA per
-//     tile: k-slots 8g + r hold the first chunk's token 4g + r, 8g + 4 + r the second's;
+//     The QK product runs the D/32 k-steps of each chunk against the same q'' operand into
+//     two accumulators, and each column keeps its own chunk's, so one softmax pass covers
+//     32 tokens; the PV product contracts both chunks in one 16x16x32 MFMA per tile:
+//     k-slots 8g + r hold the first chunk's token 4g + r, 8g + 4 + r the second's;
 //     each lane's p sits in the half of its own chunk, zeros in the other. The two chunks'
 //     softmax streams of a head (columns j, j ^ 4) are merged once at the end.
 //   decode_q_kernel (5 to 16 heads): one chunk per step; up to 8 heads the columns hold
