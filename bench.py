@@ -604,7 +604,7 @@ def counter_summary(config, pmc_dir):
     log(f"wrote {path}")
 
 
-def default_plan(config, B, max_pages, cu_count=None, hkv=HKV, fmt_name=None):
+def default_plan(config, B, max_pages, cu_count=None, hkv=HKV, fmt_name=None, head_dim=D):
     """(splits, waves, units) the op would use with num_splits=None: the work-unit plan
     (units > 0) where the library prefers it, else the split plan (C1: no split,
     configs[0]). `fmt_name` defaults to the config's format."""
@@ -614,10 +614,10 @@ def default_plan(config, B, max_pages, cu_count=None, hkv=HKV, fmt_name=None):
         return 1, 0, 0
     cus = cu_count or _sm_count(0)
     fmt_name = fmt_name or CONFIGS[config][3]
-    units, waves = plan_units(B, hkv, BS, max_pages, cus, fmt_name)
+    units, waves = plan_units(B, hkv, BS, max_pages, cus, fmt_name, head_dim)
     if units:
         return 0, waves, units
-    return (*plan_decode(B, hkv, BS, max_pages, cus, fmt_name), 0)
+    return (*plan_decode(B, hkv, BS, max_pages, cus, fmt_name, head_dim), 0)
 
 
 def run_config(config, steps, warmup, splits=None, waves=0, pipeline=0, flushed=True,
@@ -676,7 +676,7 @@ def build_layers(B, ctx, pool, fmt_name, layers, shape=(HQ, HKV, D), config=None
                                            shape=shape)
         lens = lens or [int(x) for x in sl.tolist()]
         splits, waves, units = default_plan(config, B, bt.shape[1], hkv=shape[1],
-                                            fmt_name=fmt_name)
+                                            fmt_name=fmt_name, head_dim=shape[2])
         step_list.append(Step(q, k, v, bt, sl, splits, waves, 0, fmt, units))
         del q, k, v, bt, sl, fmt
     return step_list, lens

@@ -148,23 +148,26 @@ int kvq_head_blocks(int32_t q_heads, int32_t kv_heads);
 /* MI355X work plan used when the caller gives no split count; takes the place of the
  * heuristic above (triton_fp16.py:175-180) on this hardware. It sizes the decomposition
  * in waves, because a workgroup here holds several waves that combine through LDS:
- *   per_pair = pow2_floor(T * cu_count / (batch * kv_heads)), T = 2 waves per CU (fp16),
- *              4 (INT8, FP8) or 8 (INT4), raised to pow2_floor(cdiv(chunks, C)) (C = 512 chunks per
- *              wave for fp16; quantized 256, or 64 when batch * kv_heads > cu_count, so that
- *              uneven sequence lengths still balance), capped at pow2_floor(chunks / 4);
+ *   per_pair = pow2_floor(T * cu_count / (batch * kv_heads)), T = 2 s waves per CU (fp16,
+ *              s = max(1, 128 / head_dim)), 4 (INT8, FP8) or 8 (INT4), raised to
+ *              pow2_floor(cdiv(chunks, C)) (C = 512 chunks per wave for fp16; quantized
+ *              256, or 64 when batch * kv_heads > cu_count, so that uneven sequence
+ *              lengths still balance), capped at pow2_floor(chunks / 4);
  *              chunks = max_pages * block_size / 16
- *   waves = min(2, per_pair) for fp16; clamp(per_pair / 8, 1, Wq) for quantized (Wq = 4;
- *           INT4 8),
+ *   waves = min(min(2 s, 4), per_pair) for fp16; clamp(per_pair / 8, 1, Wq) for quantized
+ *           (Wq = 4; INT4 8),
  *   splits = per_pair / waves
  * fp16 streams fastest with about 2 waves per CU, each 2 chunks (16 KB) ahead, spread
  * over at least one workgroup per CU; more waves in flight lower the achieved bandwidth.
  * The quantized kernels run best with about 4 (INT4: 8) waves per CU, at most 8 splits per
  * (sequence, kv head) and, for large ragged batches, several waves per workgroup on small
- * partitions (all measured on MI355X for batch 1..64 and 32k..128k contexts). Writes
- * both outputs (splits before
- * kvq_normalize_splits); returns KVQ_OK or an error. */
+ * partitions (all measured on MI355X for batch 1..64 and 32k..128k contexts). fp16 head
+ * dims below 128 move fewer bytes per chunk through about the same per-chunk work and
+ * need s times the waves (the quantized split plans measured slower with them).
+ * head_dim is a power of two >= 16 (KVQ_ERR_SHAPE otherwise). Writes
+ * both outputs (splits before kvq_normalize_splits); returns KVQ_OK or an error. */
 int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t max_pages,
-                    int32_t kv_format, int32_t cu_count, int32_t* splits_out,
+                    int32_t kv_format, int32_t head_dim, int32_t cu_count, int32_t* splits_out,
                     int32_t* waves_out);
 
 /* Work-unit plan, the library's default for batches of 2 to 1024 sequences (no reference
@@ -173,14 +176,16 @@ int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t
  * kvq_plan_decode gives splits >= 2 or the longest context (max_pages * block_size) is at
  * least 4096 tokens:
  *   units = T * cu_count / (waves * kv_heads) (at least 1), with T waves per CU and
- *           `waves` per unit workgroup: fp16 T = 2, waves = 2; INT8 / FP8 T = 4,
- *           waves = 4; INT4 T = 8, waves = 2,
+ *           `waves` per unit workgroup: fp16 T = 2 s, waves = min(2 s, 4); INT8 / FP8
+ *           T = 4 s, waves = 4; INT4 T = 8 s, waves = min(2 s, 4)
+ *           (s = max(1, 128 / head_dim)),
  * for kvq_decode_units; otherwise units = waves = 0 (use kvq_plan_decode's split plan).
  * Units balance ragged batches (a static split count sizes every sequence's splits by
  * the longest one); on uniform batches the two plans run within a few percent of each
  * other on MI355X. Returns KVQ_OK or an error. */
 int kvq_plan_units(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t max_pages,
-                   int32_t kv_format, int32_t cu_count, int32_t* units_out, int32_t* waves_out);
+                   int32_t kv_format, int32_t head_dim, int32_t cu_count, int32_t* units_out,
+                   int32_t* waves_out);
 
 /* Split normalization, triton_fp16.py:211-217: clamps num_splits to [1, max_pages], then
  * pages_per_split = cdiv(max_pages, S) and S = cdiv(max_pages, pages_per_split).

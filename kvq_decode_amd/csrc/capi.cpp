@@ -393,19 +393,29 @@ int kvq_choose_num_splits(int32_t batch, int32_t kv_heads, int32_t block_size,
     return int(s < 1 ? 1 : s);
 }
 
+// Head dims below 128 move fewer bytes per 16-token chunk through about the same per-chunk
+// work, so they need proportionally more waves in flight. Measured on MI355X (32 q / 8 kv
+// heads, full steps): fp16 at head_dim 64 0.43 -> 0.72 of peak at batch 8 x 32k and 0.37
+// -> 0.57 at batch 1 x 64k, at head_dim 32 0.14 -> 0.27; quantized work units +1-19% at
+// head_dim 64. The quantized split plan (single sequences) measured 2-9% slower with the
+// extra waves and keeps the 128 plan, and so does head_dim 256 everywhere.
+int64_t head_dim_scale(int32_t head_dim) { return head_dim < 128 ? 128 / head_dim : 1; }
+
 int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t max_pages,
-                    int32_t kv_format, int32_t cu_count, int32_t* splits_out,
+                    int32_t kv_format, int32_t head_dim, int32_t cu_count, int32_t* splits_out,
                     int32_t* waves_out) {
     if (!splits_out || !waves_out) return KVQ_ERR_NULL_POINTER;
     if (batch < 1 || kv_heads < 1 || max_pages < 1 || cu_count < 1) return KVQ_ERR_SHAPE;
     if (!is_pow2(block_size) || block_size < 16) return KVQ_ERR_SHAPE;
+    if (!is_pow2(head_dim) || head_dim < 16) return KVQ_ERR_SHAPE;
     if (kv_format < KVQ_KV_F16 || kv_format > KVQ_KV_INT4) return KVQ_ERR_FORMAT;
     const bool quant = kv_format != KVQ_KV_F16;
     const int64_t chunks = int64_t(max_pages) * (block_size / 16);
     const int64_t pairs = int64_t(batch) * kv_heads;
     // INT4 moves half the bytes per token of INT8 / FP8 through the same per-chunk work,
     // so it needs twice the waves in flight to keep HBM busy
-    const int64_t waves_per_cu = kv_format == KVQ_KV_INT4 ? 8 : quant ? 4 : 2;
+    const int64_t waves_per_cu =
+        kv_format == KVQ_KV_INT4 ? 8 : quant ? 4 : 2 * head_dim_scale(head_dim);
     // quantized: 256-chunk partitions while (sequence, kv head) pairs alone do not fill
     // the CUs, 64-chunk partitions beyond (large batches, where ragged lengths need small
     // work items to balance)
@@ -415,10 +425,12 @@ int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t
     if (per_pair < balance) per_pair = balance;
     const int64_t cap = pow2_floor(chunks / 4);
     if (per_pair > cap) per_pair = cap;
-    // fp16: up to 2 waves per workgroup. Quantized: one wave per 8 units of per_pair, up
-    // to 4 (INT4: 8), so that long or many sequences get fewer, larger splits (less
-    // partial traffic)
-    int64_t waves = per_pair < 2 ? per_pair : 2;
+    // fp16: up to 2 waves per workgroup (head_dim 64: 4). Quantized: one wave per 8 units
+    // of per_pair, up to 4 (INT4: 8), so that long or many sequences get fewer, larger
+    // splits (less partial traffic)
+    int64_t wf = 2 * head_dim_scale(head_dim);
+    if (wf > 4) wf = 4;
+    int64_t waves = per_pair < wf ? per_pair : wf;
     if (quant) {
         const int64_t wmax = kv_format == KVQ_KV_INT4 ? 8 : 4;
         waves = per_pair / 8;
@@ -430,11 +442,12 @@ int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t
 }
 
 int kvq_plan_units(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t max_pages,
-                   int32_t kv_format, int32_t cu_count, int32_t* units_out, int32_t* waves_out) {
+                   int32_t kv_format, int32_t head_dim, int32_t cu_count, int32_t* units_out,
+                   int32_t* waves_out) {
     if (!units_out || !waves_out) return KVQ_ERR_NULL_POINTER;
     int32_t splits = 0, split_waves = 0;
-    const int st = kvq_plan_decode(batch, kv_heads, block_size, max_pages, kv_format, cu_count,
-                                   &splits, &split_waves);
+    const int st = kvq_plan_decode(batch, kv_heads, block_size, max_pages, kv_format, head_dim,
+                                   cu_count, &splits, &split_waves);
     if (st != KVQ_OK) return st;
     *units_out = 0;
     *waves_out = 0;
@@ -447,10 +460,14 @@ int kvq_plan_units(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t 
     if (splits < 2 && int64_t(max_pages) * block_size < 4096) return KVQ_OK;
     // Waves per CU and per unit workgroup, measured on MI355X: fp16 2 in workgroups of 2;
     // INT8 / FP8 4 in workgroups of 4; INT4 (half the bytes of a chunk for about the
-    // same per-chunk work) 8 in workgroups of 2
+    // same per-chunk work) 8 in workgroups of 2. Below head_dim 128 the waves per CU grow
+    // by 128 / head_dim and the fp16 / INT4 workgroups to up to 4 waves (head_dim 64: fp16
+    // 4 per CU in workgroups of 4, INT4 16 in workgroups of 4)
     const bool int4 = kv_format == KVQ_KV_INT4;
-    const int64_t waves_per_cu = kv_format == KVQ_KV_F16 ? 2 : int4 ? 8 : 4;
-    const int64_t waves = kv_format == KVQ_KV_F16 || int4 ? 2 : 4;
+    const int64_t scale = head_dim_scale(head_dim);
+    const int64_t waves_per_cu = (kv_format == KVQ_KV_F16 ? 2 : int4 ? 8 : 4) * scale;
+    int64_t waves = kv_format == KVQ_KV_F16 || int4 ? 2 * scale : 4;
+    if (waves > 4) waves = 4;
     const int64_t units = waves_per_cu * cu_count / (waves * int64_t(kv_heads));
     *units_out = int32_t(units < 1 ? 1 : units);
     *waves_out = int32_t(waves);

@@ -145,14 +145,46 @@ def test_plan_decode():
     assert plan_decode(1, 8, 32, 4096, 256, "fp16") == (32, 2)  # 2 chunks per page
     L = _lib.lib()
     s, w = ctypes.c_int32(), ctypes.c_int32()
-    assert L.kvq_plan_decode(0, 8, 16, 64, 0, 256, ctypes.byref(s), ctypes.byref(w)) == \
+    assert L.kvq_plan_decode(0, 8, 16, 64, 0, 128, 256, ctypes.byref(s), ctypes.byref(w)) == \
         _lib.KVQ_ERR_SHAPE
-    assert L.kvq_plan_decode(1, 8, 16, 64, 7, 256, ctypes.byref(s), ctypes.byref(w)) == \
+    assert L.kvq_plan_decode(1, 8, 16, 64, 7, 128, 256, ctypes.byref(s), ctypes.byref(w)) == \
         _lib.KVQ_ERR_FORMAT
-    assert L.kvq_plan_decode(1, 8, 24, 64, 0, 256, ctypes.byref(s), ctypes.byref(w)) == \
+    assert L.kvq_plan_decode(1, 8, 24, 64, 0, 128, 256, ctypes.byref(s), ctypes.byref(w)) == \
         _lib.KVQ_ERR_SHAPE
-    assert L.kvq_plan_decode(1, 8, 16, 64, 0, 256, None, ctypes.byref(w)) == \
+    assert L.kvq_plan_decode(1, 8, 16, 64, 0, 128, 256, None, ctypes.byref(w)) == \
         _lib.KVQ_ERR_NULL_POINTER
+    for hd in (0, 24, -64):  # head_dim: a power of two >= 16
+        assert L.kvq_plan_decode(1, 8, 16, 64, 0, hd, 256, ctypes.byref(s),
+                                 ctypes.byref(w)) == _lib.KVQ_ERR_SHAPE, hd
+
+
+def test_plan_head_dims():
+    """Head dims below 128 get 128 / head_dim times the waves per CU in the work-unit plan
+    (fp16 and INT4 unit workgroups of up to 4 waves) and, for fp16 only, in the split plan
+    (workgroups of up to 4); 256 keeps the 128 plan."""
+    from kvq_decode_amd.ops import plan_decode, plan_units
+    decode_cases = [  # batch, max_pages, format, head_dim -> (splits, waves)
+        (8, 2048, "fp16", 64, (4, 4)),    # 4 waves per CU: 16 per pair
+        (8, 2048, "fp16", 32, (8, 4)),    # 8 waves per CU: 32 per pair
+        (8, 2048, "fp16", 256, (4, 2)),   # as at 128
+        (16, 2048, "int8", 64, (8, 1)),   # quantized split plans: as at 128
+        (16, 2048, "int4", 64, (8, 2)),
+        (16, 2048, "int4", 256, (8, 2)),
+    ]
+    for batch, pages, fmt, hd, want in decode_cases:
+        assert plan_decode(batch, 8, 16, pages, 256, fmt, hd) == want, (batch, fmt, hd)
+    units_cases = [  # batch, max_pages, format, head_dim -> (units, waves)
+        (8, 2048, "fp16", 64, (32, 4)),    # 4 waves per CU in 4-wave workgroups
+        (8, 2048, "fp16", 32, (64, 4)),    # 8 waves per CU
+        (8, 2048, "fp16", 256, (32, 2)),   # as at 128
+        (64, 2048, "int4", 64, (128, 4)),  # 16 waves per CU
+        (16, 2048, "int8", 64, (64, 4)),   # 8 waves per CU
+        (16, 2048, "fp8_e4m3", 256, (32, 4)),
+    ]
+    for batch, pages, fmt, hd, want in units_cases:
+        assert plan_units(batch, 8, 16, pages, 256, fmt, hd) == want, (batch, fmt, hd)
+    # the default argument is head_dim 128
+    assert plan_units(8, 8, 16, 2048, 256, "fp16") == plan_units(8, 8, 16, 2048, 256, "fp16", 128)
 
 
 def test_plan_units():
@@ -180,11 +212,11 @@ def test_plan_units():
     assert plan_units(8, 1, 16, 2048, 256, "fp16") == (256, 2)  # MQA
     L = _lib.lib()
     u, w = ctypes.c_int32(), ctypes.c_int32()
-    assert L.kvq_plan_units(0, 8, 16, 64, 0, 256, ctypes.byref(u), ctypes.byref(w)) == \
+    assert L.kvq_plan_units(0, 8, 16, 64, 0, 128, 256, ctypes.byref(u), ctypes.byref(w)) == \
         _lib.KVQ_ERR_SHAPE
-    assert L.kvq_plan_units(2, 8, 16, 64, 7, 256, ctypes.byref(u), ctypes.byref(w)) == \
+    assert L.kvq_plan_units(2, 8, 16, 64, 7, 128, 256, ctypes.byref(u), ctypes.byref(w)) == \
         _lib.KVQ_ERR_FORMAT
-    assert L.kvq_plan_units(2, 8, 16, 64, 0, 256, None, ctypes.byref(w)) == \
+    assert L.kvq_plan_units(2, 8, 16, 64, 0, 128, 256, None, ctypes.byref(w)) == \
         _lib.KVQ_ERR_NULL_POINTER
 
 
@@ -197,6 +229,8 @@ def test_plan_workspace_shapes():
     assert plan_workspace_shapes(1, 32, 8, 128, 16, 4096, 256) == ((1, 32, 32, 128), (1, 32, 32))
     # a single pass over short contexts needs none
     assert plan_workspace_shapes(64, 32, 8, 128, 16, 64, 256) is None
+    # head_dim 32: 8 waves per CU in 4-wave unit workgroups, 64 units per kv head
+    assert plan_workspace_shapes(8, 32, 8, 32, 16, 2048, 256) == ((32, 72, 32), (32, 72))
 
 
 def test_normalize_splits():
