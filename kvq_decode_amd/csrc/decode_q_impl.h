@@ -25,7 +25,7 @@
 //     hi + lo fp16 parts (the PV MFMA's B operand); the second sum is one fp32 scalar per
 //     head (`corr`), added once at the end.
 //
-// Two kernels:
+// Kernels:
 //   decode_q2_kernel (1 to 4 q heads per kv head): the 16 MFMA columns hold 2 chunks x
 //     4 heads x {hi, lo}. Column j: head j & 3, chunk (j >> 2) & 1 of the pair, part j >> 3.
 //     The QK product runs the D/32 k-steps of each chunk against the same q'' operand into
@@ -34,8 +34,12 @@
 //     k-slots 8g + r hold the first chunk's token 4g + r, 8g + 4 + r the second's;
 //     each lane's p sits in the half of its own chunk, zeros in the other. The two chunks'
 //     softmax streams of a head (columns j, j ^ 4) are merged once at the end.
-//   decode_q_kernel (5 to 16 heads): one chunk per step; up to 8 heads the columns hold
-//     {hi, lo} x 8 heads (one QK chain), above that two chains.
+//   decode_q2_kernel with SPLIT (5 to 8 heads): the columns hold {hi, lo} x 8 heads and
+//     both chunks of the pair (chunk_pair_wide); the hi lane of a head weights one chunk,
+//     its lo lane the other, and they swap the parts each column needs.
+//   decode_q_kernel (5 to 16 heads; with pairs only where they do not apply: K groups of
+//     one chunk, head dim 256, more than 8 heads): one chunk per step; up to 8 heads the
+//     columns hold {hi, lo} x 8 heads (one QK chain), above that two chains.
 // Head dims 64, 128 and 256 (decode_q.hip, decode_q_d64.hip and decode_q_d256.hip each
 // instantiate one); 256 runs the single-chunk kernel with at most 2 chunks in flight.
 #pragma once
@@ -241,9 +245,9 @@ struct ChunkQ {
 //   the V (scale, zero) pair of token 4g + (l & 3) (4 bytes: the 64 bytes of the chunk's
 //   16 pairs reach the wave once per row of 16 lanes, not once per lane), vs2 the same
 //   token of the chunk pair's chunk (l >> 2) & 1, 64 bytes further for the second chunk,
-//   and the K group's pairs of channels CPL l .. CPL l + CPL - 1 (4 CPL bytes).
+//   vs3 that of chunk (l >> 3) & 1, and the K group's pairs of channels CPL l .. CPL l + CPL - 1 (4 CPL bytes).
 struct QLaneOff {
-    uint32_t k[4], v[4], vs, vs2, ks;
+    uint32_t k[4], v[4], vs, vs2, vs3, ks;
 };
 
 template <int FMT, int D>
@@ -276,6 +280,7 @@ __device__ __forceinline__ QLaneOff lane_offsets(const DecodeParams& p, int i16,
     }
     o.vs = 16 * g + 4 * (lane & 3);
     o.vs2 = o.vs + 64 * ((lane >> 2) & 1);
+    o.vs3 = o.vs + 64 * ((lane >> 3) & 1);
     o.ks = 4 * Q::CPL * lane;
     return o;
 }
@@ -346,7 +351,8 @@ __device__ __forceinline__ u4v load_codes(__amdgpu_buffer_rsrc_t r, uint32_t vof
 // WITH_K: also load the K group's (scale, zero) pairs (ch.ksz), stored with the group's
 // first page `lead`. VS: the V (scale, zero) pairs ch.vsz brings, from the chunk's V group
 // in its first page `vlead`: 1 the chunk's own; 2 those of the chunk pair c, c + 1 (c even,
-// both in one V group: lane l takes chunk c + ((l >> 2) & 1)); 0 none.
+// both in one V group: lane l takes chunk c + ((l >> 2) & 1)); 3 the same with chunk
+// c + ((l >> 3) & 1); 0 none.
 template <int FMT, int D, bool WITH_K = true, int VS = 1>
 __device__ __forceinline__ void load_chunk_q(const QBase& B, int c, const QLaneOff& lo, int phys,
                                              int lead, int vlead, ChunkQ<FMT, D>& ch) {
@@ -364,8 +370,8 @@ __device__ __forceinline__ void load_chunk_q(const QBase& B, int c, const QLaneO
     // at 64 (c & vmask) bytes in its V group
     if constexpr (VS != 0)
         ch.vsz = __builtin_amdgcn_raw_buffer_load_b32(block_rsrc(B.vs, vlead, B.vs_blk),
-                                                      VS == 2 ? lo.vs2 : lo.vs,
-                                                      64 * ((uint32_t)c & B.vmask & ~(VS == 2 ? 1u : 0u)),
+                                                      VS == 2 ? lo.vs2 : VS == 3 ? lo.vs3 : lo.vs,
+                                                      64 * ((uint32_t)c & B.vmask & ~(VS >= 2 ? 1u : 0u)),
                                                       kNT);
     if constexpr (WITH_K) {
         const auto rs = block_rsrc(B.ks, lead, B.ks_blk);
@@ -566,12 +572,18 @@ __device__ __forceinline__ float make_qprime(const uint32_t* ksz, uint32_t* stag
     return rows_sum(qz);
 }
 
-// Online-softmax update of one lane for scores s2 (log2 domain, masked scores -inf):
-// rescales the state when a score passes the lazy reference max, returns p = 2^(s2 - m).
-template <int D>
+// Online-softmax update of one lane for its N = 4 or 8 scores s2 (log2 domain, masked
+// scores -inf): rescales the state when a score passes the lazy reference max, returns
+// p = 2^(s2 - m).
+// PAIRED: lanes l and l ^ 8 hold different scores of one stream and keep one reference
+// max (their maxima are combined through DPP row_ror:8).
+template <int D, int N = 4, bool PAIRED = false>
 __device__ __forceinline__ void softmax_step(float* s2, SoftmaxState<D>& st, float& corr,
                                              float* pr) {
-    const float lm = fmaxf(fmaxf(s2[0], s2[1]), fmaxf(s2[2], s2[3]));
+    static_assert(N == 4 || N == 8, "4 or 8 scores per lane");
+    float lm = fmaxf(fmaxf(s2[0], s2[1]), fmaxf(s2[2], s2[3]));
+    if constexpr (N == 8) lm = fmaxf(lm, fmaxf(fmaxf(s2[4], s2[5]), fmaxf(s2[6], s2[7])));
+    if constexpr (PAIRED) lm = fmaxf(lm, ror8(lm));
     if (__builtin_amdgcn_ballot_w64(lm > st.m + kLazyMax) != 0) {  // rare: the max moved
         const float mn = fmaxf(st.m, rows_max(lm));
         const float alpha = fast_exp2(st.m - mn);
@@ -582,8 +594,11 @@ __device__ __forceinline__ void softmax_step(float* s2, SoftmaxState<D>& st, flo
         for (int t = 0; t < D / 16; ++t) st.acc[t] *= alpha;
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(s2[r] - st.m);
-    st.l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+    for (int r = 0; r < N; ++r) pr[r] = fast_exp2(s2[r] - st.m);
+    if constexpr (N == 4)
+        st.l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+    else
+        st.l += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
 }
 
 // p s_t as hi + lo fp16 parts, hi = fp16(p s_t) (fma with +0 is the product: p, s >= 0;
@@ -739,6 +754,81 @@ __device__ __forceinline__ void chunk_pair(const ChunkQ<FMT, D>& ca, const Chunk
     pbw[1] = slot ? 0u : pw[1];
     pbw[2] = slot ? pw[0] : 0u;
     pbw[3] = slot ? pw[1] : 0u;
+    const h8 pb = __builtin_bit_cast(h8, pbw);
+    uint32_t a01[Q::DV], a23[Q::DV], b01[Q::DV], b23[Q::DV];
+    Q::vtiles(va, a01, a23);
+    Q::vtiles(vb, b01, b23);
+#pragma unroll
+    for (int t = 0; t < Q::DV; ++t) {
+        const u4v w = {a01[t], a23[t], b01[t], b23[t]};
+        st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, w), pb,
+                                                           st.acc[t], 0, 0, 0);
+    }
+}
+
+// A chunk pair (chunks a, b) of one K group, 5 to 8 q heads per kv head (decode_q2_kernel
+// with SPLIT): the 16 columns hold {hi, lo} x 8 heads (column j: head j & 7, part j >> 3),
+// as in chunk_q, and every column takes both chunks. Two QK accumulators (one per chunk)
+// against the same q''. The hi lane (column j < 8) of a head runs the softmax and the PV
+// weights of chunk a's rows, its lo lane (j + 8) those of chunk b: the two share one
+// reference max (softmax_step PAIRED) and swap the parts the other column needs through
+// DPP row_ror:8, so no lane repeats its partner's work; their l and corr are summed at the
+// end. The PV product contracts both chunks in one 16x16x32 MFMA per tile (k-slots 8g + r:
+// chunk a's token 4g + r, 8g + 4 + r: chunk b's). The V pairs come as load_chunk_q's VS 3
+// (lane l: chunk (l >> 3) & 1, the lane's own); a single chunk loaded with VS 1 passes
+// itself as b with valid_b = 0.
+template <int FMT, int D, bool MASK>
+__device__ __forceinline__ void chunk_pair_wide(const ChunkQ<FMT, D>& ca,
+                                                const ChunkQ<FMT, D>& cb, const h8* qv,
+                                                float csl, float sl2f, int valid_a, int valid_b,
+                                                int g, bool lo_part, char* kst,
+                                                SoftmaxState<D>& st, float& corr) {
+    typedef QFmt<FMT, D> Q;
+    const int lane = __lane_id();
+    uint32_t va[4][vrow_dwords<FMT, D>()], vb[4][vrow_dwords<FMT, D>()];
+    v_rows<FMT, D>(ca, kst, lane & 15, g, va);
+    v_rows<FMT, D>(cb, kst, lane & 15, g, vb);
+    f4 sa = (f4)0.f, sb = (f4)0.f;
+    {
+        u4v kr[Q::KLOADS];
+        k_operand<FMT, D>(ca, kst, g, kr);
+#pragma unroll
+        for (int k = 0; k < Q::NST; ++k)
+            sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(Q::kop(kr, k), qv[k], sa, 0, 0, 0);
+        k_operand<FMT, D>(cb, kst, g, kr);
+#pragma unroll
+        for (int k = 0; k < Q::NST; ++k)
+            sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(Q::kop(kr, k), qv[k], sb, 0, 0, 0);
+    }
+    // the lane's own chunk's scores, hi + lo: the hi lane sums chunk a's columns j and
+    // j + 8, the lo lane chunk b's
+    const int valid = lo_part ? valid_b : valid_a;
+    float s2[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float x = lo_part ? sb[r] : sa[r], y = lo_part ? sa[r] : sb[r];
+        s2[r] = __builtin_fmaf(x + ror8(y), sl2f, csl);
+    }
+    if (MASK) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s2[r] = 4 * g + r < valid ? s2[r] : -INFINITY;
+    }
+    float pr[4];
+    softmax_step<D, 4, true>(s2, st, corr, pr);
+    h4 ph, pl;
+    pv_weights<MASK>(pr, ca.vsz, valid, g, ph, pl, corr);
+    // hi lane: chunk a's hi parts and (from the lo lane) chunk b's; lo lane: chunk a's lo
+    // parts (from the hi lane) and chunk b's
+    const u2 keep = __builtin_bit_cast(u2, lo_part ? pl : ph);
+    const u2 send = __builtin_bit_cast(u2, lo_part ? ph : pl);
+    u2 recv;
+    recv[0] = (uint32_t)__float_as_int(ror8(__int_as_float((int)send[0])));
+    recv[1] = (uint32_t)__float_as_int(ror8(__int_as_float((int)send[1])));
+    u4v pbw;
+    pbw[0] = lo_part ? recv[0] : keep[0];
+    pbw[1] = lo_part ? recv[1] : keep[1];
+    pbw[2] = lo_part ? keep[0] : recv[0];
+    pbw[3] = lo_part ? keep[1] : recv[1];
     const h8 pb = __builtin_bit_cast(h8, pbw);
     uint32_t a01[Q::DV], a23[Q::DV], b01[Q::DV], b23[Q::DV];
     Q::vtiles(va, a01, a23);
@@ -922,7 +1012,7 @@ __global__ __launch_bounds__(W * 64) void decode_q_kernel(const DecodeParams p) 
 // wave's odd leading chunk, odd trailing full chunk and the sequence's partial last chunk
 // run as single-chunk steps. P-deep ring over the pairs (P = 4 or 8 chunks: while a pair
 // computes, P - 2 chunks are in flight); the ring depth never changes the arithmetic.
-template <int FMT, int D, int W, bool FINAL, int P>
+template <int FMT, int D, int W, bool FINAL, int P, bool WIDE>
 __device__ __forceinline__ void q2_range(const DecodeParams& p, int kvh, int b, int seq_len,
                                          int w_lo, int w_hi, int wave, int64_t part_base,
                                          int64_t part_stride) {
@@ -945,7 +1035,7 @@ __device__ __forceinline__ void q2_range(const DecodeParams& p, int kvh, int b, 
     h8* qsh = (h8*)(smem + r0 + W * D);
     if (wave == 0) stage_q<FMT, D>(p, b, kvh, i16, g, qsh);
     __syncthreads();
-    qsh += (lane & 48) | (lane & 3);  // column j reads head j & 3
+    qsh += WIDE ? (lane & ~8) : ((lane & 48) | (lane & 3));  // column j reads head j & 7 / 3
     uint32_t* stage = (uint32_t*)(smem + r0) + wave * D;
 
     SoftmaxState<D> st;
@@ -972,8 +1062,12 @@ __device__ __forceinline__ void q2_range(const DecodeParams& p, int kvh, int b, 
                              __builtin_amdgcn_readlane(pg, 0), __builtin_amdgcn_readlane(pg, 1),
                              __builtin_amdgcn_readlane(pg, 2), ch);
         group(ch, c >> kgs);
-        chunk_pair<FMT, D, true>(ch, ch, qv, csl, sl2f, valid, 0, g, slot, lo_part, kst, st,
-                                 corr);
+        if constexpr (WIDE)
+            chunk_pair_wide<FMT, D, true>(ch, ch, qv, csl, sl2f, valid, 0, g, lo_part, kst, st,
+                                          corr);
+        else
+            chunk_pair<FMT, D, true>(ch, ch, qv, csl, sl2f, valid, 0, g, slot, lo_part, kst, st,
+                                     corr);
     };
 
     const int r_hi = min(w_hi, c_full);  // fully valid chunks [w_lo, r_hi)
@@ -996,11 +1090,10 @@ __device__ __forceinline__ void q2_range(const DecodeParams& p, int kvh, int b, 
 #pragma unroll
         for (int i = 0; i < P; ++i) {
             if (i % 2 == 0)
-                load_chunk_q<FMT, D, true, 2>(base, min(c_first + i, last), lo,
-                                              __builtin_amdgcn_readlane(pg_cur, i),
-                                              __builtin_amdgcn_readlane(pg_cur, P + i),
-                                              __builtin_amdgcn_readlane(pg_cur, 2 * P + i),
-                                              ring[i]);
+                load_chunk_q<FMT, D, true, WIDE ? 3 : 2>(
+                    base, min(c_first + i, last), lo, __builtin_amdgcn_readlane(pg_cur, i),
+                    __builtin_amdgcn_readlane(pg_cur, P + i),
+                    __builtin_amdgcn_readlane(pg_cur, 2 * P + i), ring[i]);
             else
                 load_chunk_q<FMT, D, false, 0>(base, min(c_first + i, last), lo,
                                                __builtin_amdgcn_readlane(pg_cur, i), 0, 0,
@@ -1015,14 +1108,17 @@ __device__ __forceinline__ void q2_range(const DecodeParams& p, int kvh, int b, 
                 const int c = c0 + i;
                 if (c < e_hi) {
                     group(ring[i], c >> kgs);
-                    chunk_pair<FMT, D, false>(ring[i], ring[i + 1], qv, csl, sl2f, 16, 16, g,
-                                              slot, lo_part, kst, st, corr);
+                    if constexpr (WIDE)
+                        chunk_pair_wide<FMT, D, false>(ring[i], ring[i + 1], qv, csl, sl2f, 16,
+                                                       16, g, lo_part, kst, st, corr);
+                    else
+                        chunk_pair<FMT, D, false>(ring[i], ring[i + 1], qv, csl, sl2f, 16, 16,
+                                                  g, slot, lo_part, kst, st, corr);
                 }
-                load_chunk_q<FMT, D, true, 2>(base, min(c0 + i + P, last), lo,
-                                              __builtin_amdgcn_readlane(pg_cur, i),
-                                              __builtin_amdgcn_readlane(pg_cur, P + i),
-                                              __builtin_amdgcn_readlane(pg_cur, 2 * P + i),
-                                              ring[i]);
+                load_chunk_q<FMT, D, true, WIDE ? 3 : 2>(
+                    base, min(c0 + i + P, last), lo, __builtin_amdgcn_readlane(pg_cur, i),
+                    __builtin_amdgcn_readlane(pg_cur, P + i),
+                    __builtin_amdgcn_readlane(pg_cur, 2 * P + i), ring[i]);
                 load_chunk_q<FMT, D, false, 0>(base, min(c0 + i + 1 + P, last), lo,
                                                __builtin_amdgcn_readlane(pg_cur, i + 1), 0, 0,
                                                ring[i + 1]);
@@ -1033,12 +1129,13 @@ __device__ __forceinline__ void q2_range(const DecodeParams& p, int kvh, int b, 
     if (w_lo <= r_hi && r_hi < w_hi)  // this wave owns the partial last chunk c_full
         single(r_hi, min(seq_len - (r_hi << 4), 16));
 
-    // hi + lo columns, then the two chunk streams of each head (columns j, j ^ 4)
+    // hi + lo columns, then (up to 4 heads) the two chunk streams of each head (columns j,
+    // j ^ 4)
 #pragma unroll
     for (int t = 0; t < DV; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) st.acc[t][r] += ror8(st.acc[t][r]);
-    {
+    if constexpr (!WIDE) {
         const float m_o = __shfl_xor(st.m, 4), l_o = __shfl_xor(st.l, 4);
         const float c_o = __shfl_xor(corr, 4);
         const float M = fmaxf(st.m, m_o);
@@ -1051,6 +1148,9 @@ __device__ __forceinline__ void q2_range(const DecodeParams& p, int kvh, int b, 
             for (int r = 0; r < 4; ++r)
                 st.acc[t][r] = wa * st.acc[t][r] + wb * __shfl_xor(st.acc[t][r], 4);
         st.m = M;
+    } else {  // the hi and lo lanes of a head summed different chunks' l and corr
+        st.l += ror8(st.l);
+        corr += ror8(corr);
     }
     tile_weights<FMT, D>(st);
     __syncthreads();  // every wave is done with its LDS staging tile
@@ -1058,26 +1158,27 @@ __device__ __forceinline__ void q2_range(const DecodeParams& p, int kvh, int b, 
                                g, kvh, b, part_base, part_stride);
 }
 
-template <int FMT, int D, int W, bool FINAL, int P>
+template <int FMT, int D, int W, bool FINAL, int P, bool WIDE>
 __global__ __launch_bounds__(W * 64) void decode_q2_kernel(const DecodeParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const WgCoord wc = wg_coord(p, FINAL ? 1 : p.num_splits);
     if (!wc.live) return;
     const WaveRange wr = wave_range<W>(p, wc.b, wc.split, wave);
-    q2_range<FMT, D, W, FINAL, P>(p, wc.kvh, wc.b, wr.seq_len, wr.w_lo, wr.w_hi, wave,
-                                  split_part_base(p, wc.b, wc.split), p.num_splits);
+    q2_range<FMT, D, W, FINAL, P, WIDE>(p, wc.kvh, wc.b, wr.seq_len, wr.w_lo, wr.w_hi, wave,
+                                        split_part_base(p, wc.b, wc.split), p.num_splits);
 }
 
 // Work units (decode_common.h UnitSpace): workgroup = (kv head, unit), W waves running
 // one segment per sequence the unit's chunk range overlaps, each wave a contiguous share
-// of it; PAIRS selects the chunk-pair kernel.
+// of it; PAIRS selects the chunk-pair kernel (with SPLIT: 5 to 8 heads, chunk_pair_wide).
 template <int FMT, int D, int W, int P, bool PAIRS, bool SPLIT>
 __global__ __launch_bounds__(W * 64) void decode_q_units_kernel(const DecodeParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     for_unit_segments<W>(p, [&](int kvh, int b, int seq_len, int w_lo, int w_hi, int64_t base,
                                 int64_t stride) {
         if constexpr (PAIRS)
-            q2_range<FMT, D, W, false, P>(p, kvh, b, seq_len, w_lo, w_hi, wave, base, stride);
+            q2_range<FMT, D, W, false, P, SPLIT>(p, kvh, b, seq_len, w_lo, w_hi, wave, base,
+                                                 stride);
         else
             q_range<FMT, D, W, false, P, SPLIT>(p, kvh, b, seq_len, w_lo, w_hi, wave, base,
                                                 stride);
@@ -1099,17 +1200,29 @@ static hipError_t launch_q(const DecodeParams& p, hipStream_t stream) {
     return hipGetLastError();
 }
 
-template <int FMT, int D, int W, bool FINAL, int P>
+template <int FMT, int D, int W, bool FINAL, int P, bool WIDE>
 static hipError_t launch_q2(const DecodeParams& p, hipStream_t stream) {
     const dim3 grid(decode_grid(p.xcd_group, p.kv_heads, FINAL ? 1 : p.num_splits, p.batch));
-    hipLaunchKernelGGL((decode_q2_kernel<FMT, D, W, FINAL, P>), grid, dim3(W * 64),
+    hipLaunchKernelGGL((decode_q2_kernel<FMT, D, W, FINAL, P, WIDE>), grid, dim3(W * 64),
                        (q_shmem<FMT, D, W>(p)), stream, p);
     return hipGetLastError();
 }
 
-// 1 to 4 heads per kv head and K groups of at least 2 chunks: chunk pairs, ring 1 or 2 ->
-// 4 chunks, 4 -> 8. Up to 8 heads otherwise: hi / lo parts in the two column halves of
-// one MFMA chain, any ring depth. 9 to 16 heads: two chains, ring depth 4. Head dim 256:
+// The pair kernel for up to 4 heads (chunk_pair) or 5 to 8 (chunk_pair_wide); ring 4 -> 8
+// chunks in flight, else 4.
+template <int FMT, int D, int W, bool FINAL>
+static hipError_t launch_q2_g(const DecodeParams& p, int ring, hipStream_t stream) {
+    if (p.group <= 4)
+        return ring == 4 ? launch_q2<FMT, D, W, FINAL, 8, false>(p, stream)
+                         : launch_q2<FMT, D, W, FINAL, 4, false>(p, stream);
+    return ring == 4 ? launch_q2<FMT, D, W, FINAL, 8, true>(p, stream)
+                     : launch_q2<FMT, D, W, FINAL, 4, true>(p, stream);
+}
+
+// 1 to 8 heads per kv head and K groups of at least 2 chunks: chunk pairs, ring 1 or 2 ->
+// 4 chunks, 4 -> 8. Up to 8 heads otherwise (K groups of one chunk): hi / lo parts in the
+// two column halves of one MFMA chain, any ring depth. 9 to 16 heads: two chains, ring
+// depth 4. Head dim 256:
 // the single-chunk kernel only, ring depth 1 or 2 (9 to 16 heads: 2), which keeps its
 // twice-as-large chunks and tiles in registers.
 template <int FMT, int D, bool FINAL, int W>
@@ -1124,9 +1237,8 @@ static hipError_t launch_q_g(const DecodeParams& p, int ring, hipStream_t stream
     } else {
         // pair kernel: ring 4 -> 8 chunks in flight, else 4 (a pair computes while P - 2
         // load); single-chunk kernel: the ring depth as given (two chains above 8 heads: 4)
-        if (p.group <= 4 && p.k_group_chunks >= 2)
-            return ring == 4 ? launch_q2<FMT, D, W, FINAL, 8>(p, stream)
-                             : launch_q2<FMT, D, W, FINAL, 4>(p, stream);
+        if (p.group <= 8 && p.k_group_chunks >= 2)
+            return launch_q2_g<FMT, D, W, FINAL>(p, ring, stream);
         if (p.group > 8) return launch_q<FMT, D, W, FINAL, 4, false>(p, stream);
         switch (ring) {
             case 1: return launch_q<FMT, D, W, FINAL, 1, true>(p, stream);
@@ -1171,6 +1283,9 @@ static hipError_t launch_q_units_w(const DecodeParams& p, int ring, hipStream_t 
         if (p.group <= 4 && p.k_group_chunks >= 2)
             return ring == 4 ? launch_qu<FMT, D, W, 8, true, false>(p, stream)
                              : launch_qu<FMT, D, W, 4, true, false>(p, stream);
+        if (p.group <= 8 && p.k_group_chunks >= 2)
+            return ring == 4 ? launch_qu<FMT, D, W, 8, true, true>(p, stream)
+                             : launch_qu<FMT, D, W, 4, true, true>(p, stream);
         if (p.group > 8) return launch_qu<FMT, D, W, 4, false, false>(p, stream);
         switch (ring) {
             case 1: return launch_qu<FMT, D, W, 1, false, true>(p, stream);

@@ -286,8 +286,8 @@ def test_decode_matches_fp32_attention_over_dequantized_cache(fmt, bs, num_split
 @pytest.mark.parametrize("fmt", FORMATS)
 def test_decode_group8_and_mqa_heads(fmt):
     """Other GQA groups over a quantized cache: 1, 2 and 3 q heads per kv head (the
-    chunk-pair kernel with padded head columns), 5, 7 (Qwen2.5-7B's 28 / 4) and 8 (one QK
-    chain with hi / lo columns), MQA, and 16 (two chains)."""
+    chunk-pair kernel with padded head columns), 5, 7 (Qwen2.5-7B's 28 / 4) and 8 (chunk
+    pairs with hi / lo columns), MQA, and 16 (two chains)."""
     from kvq_decode_amd import paged_decode_attention
     from kvq_decode_amd.quant import quantize_paged_cache
     for Hq, Hkv in ((8, 8), (4, 2), (6, 2), (10, 2), (28, 4), (16, 2), (8, 1), (32, 2)):
@@ -301,6 +301,36 @@ def test_decode_group8_and_mqa_heads(fmt):
         out = paged_decode_attention(gpu(q), qc.k_codes, qc.v_codes, gpu(bt), gpu(sl),
                                      num_splits=2, **qc.decode_kwargs())
         check_close(out, ref, f"{fmt} Hq={Hq} Hkv={Hkv}")
+
+
+@pytest.mark.parametrize("G", [5, 6, 7, 8])
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_chunk_pairs_five_to_eight_heads(fmt, G):
+    """5 to 8 q heads per kv head run chunk pairs with every column holding both chunks
+    (the hi and lo lanes of a head each weight one chunk): a one-token sequence, partial
+    last chunks and odd chunk counts (single-chunk steps at both ends of a wave), single
+    pass, splits, work units and the default plan; every ring depth and workgroup shape
+    within tolerance, and the ring depth never changes a result bit."""
+    from kvq_decode_amd import paged_decode_attention
+    from kvq_decode_amd.quant import quantize_paged_cache
+    Hkv = 2
+    q, kc, vc, bt, sl = make([1, 17, 33, 300, 2049], 16, Hq=G * Hkv, Hkv=Hkv, seed=30 + G)
+    qc = quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt)
+    host = {n: getattr(qc, n).cpu().numpy() for n in
+            ("k_codes", "v_codes", "k_scale", "k_zero", "v_scale", "v_zero")}
+    kd, vd = kivi.dequantize_paged_cache(host, bt, sl, fmt)
+    ref = paged_decode_attention_ref(q.astype(np.float32), kd, vd, bt, sl, out_dtype=np.float32)
+    args = (gpu(q), qc.k_codes, qc.v_codes, gpu(bt), gpu(sl))
+    for extra in ({"num_splits": 1}, {"num_splits": 3}, {"units": 5}, {"units": 7}, {}):
+        out = paged_decode_attention(*args, **extra, **qc.decode_kwargs())
+        check_close(out, ref, f"{fmt} G={G} {extra}")
+    for splits in (1, 5):
+        for waves in (1, 2, 4, 8):
+            outs = [paged_decode_attention(*args, num_splits=splits, waves_per_group=waves,
+                                           pipeline=ring, **qc.decode_kwargs())
+                    for ring in (1, 2, 4)]
+            check_close(outs[0], ref, f"{fmt} G={G} splits={splits} waves={waves}")
+            assert all(torch.equal(outs[0], o) for o in outs[1:]), (fmt, G, splits, waves)
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
