@@ -240,7 +240,7 @@ __device__ __forceinline__ void f16_range(const DecodeParams& p, int kvh, int b,
 
     // this wave's K staging tile (the LDS of the cross-wave combine is reused after the
     // barrier below)
-    extern __shared__ float smem[];
+    extern __shared__ __attribute__((aligned(16))) float smem[];
     char* kst = (char*)smem + wave * 32 * D;
 
     const int r_hi = min(w_hi, c_full);

@@ -169,7 +169,7 @@ __device__ __forceinline__ void combine_store(const DecodeParams& p, const f4* a
                                               int64_t part_base, int64_t part_stride) {
     constexpr int DV = D / 16;
     const int G = p.group;
-    extern __shared__ float smem[];
+    extern __shared__ __attribute__((aligned(16))) float smem[];
     float* sm_acc = smem;
     float* sm_m = smem + W * G * D;
     float* sm_l = sm_m + W * 16;

@@ -898,7 +898,7 @@ __device__ __forceinline__ void q_range(const DecodeParams& p, int kvh, int b, i
     // LDS: [region 0][K-scale slots, 4 D bytes per wave][q, 32 D bytes] (launch_q). Region 0 holds
     // the cross-wave combine after the chunk loop and, before it, the waves' staging tiles
     // (Q::TILE bytes each: INT8 / FP8 K and V rows, INT4 V rows).
-    extern __shared__ float smem[];
+    extern __shared__ __attribute__((aligned(16))) float smem[];
     const int r0 = quant_lds_region0(W, G, FMT, D);
     char* kst = (char*)smem + wave * Q::TILE;
     h8* qsh = (h8*)(smem + r0 + W * D);
@@ -1029,7 +1029,7 @@ __device__ __forceinline__ void q2_range(const DecodeParams& p, int kvh, int b, 
     const int vgs = p.vg_shift - 4;
     const QBase base = q_base<D>(p, cache_head(p, kvh));
 
-    extern __shared__ float smem[];
+    extern __shared__ __attribute__((aligned(16))) float smem[];
     const int r0 = quant_lds_region0(W, G, FMT, D);
     char* kst = (char*)smem + wave * Q::TILE;
     h8* qsh = (h8*)(smem + r0 + W * D);
