@@ -219,6 +219,34 @@ def test_plan_workspace_shapes_fit_the_default_plan(lens):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("D", [32, 64])
+@pytest.mark.parametrize("lens", [[3000, 17, 900, 64], [5000]])
+def test_head_dim_plans_default_path(D, lens):
+    """Below head_dim 128 the default plan runs more waves (fp16: work units in 4-wave
+    workgroups; one sequence: splits in 4-wave workgroups): against the oracle, and a
+    workspace preallocated from plan_workspace_shapes(head_dim=D) serves it bit for bit."""
+    from kvq_decode_amd import _sm_count, paged_decode_attention, plan_workspace_shapes
+    from kvq_decode_amd.ops import plan_decode, plan_units
+    q, kc, vc, bt, sl = make(32, 8, D, 16, lens, seed=19)
+    cus = _sm_count(0)
+    B, pages = len(lens), bt.shape[1]
+    units, waves = plan_units(B, 8, 16, pages, cus, "fp16", D)
+    if units:
+        assert waves == 4, (units, waves)
+    else:
+        assert plan_decode(B, 8, 16, pages, cus, "fp16", D)[1] == 4
+    ref = paged_decode_attention_ref(q, kc, vc, bt, sl, out_dtype=np.float32)
+    args = to_gpu(q, kc, vc, bt, sl)
+    out = paged_decode_attention(*args)
+    shapes = plan_workspace_shapes(B, 32, 8, D, 16, pages, cus)
+    ws = None if shapes is None else tuple(
+        torch.empty(sh, dtype=torch.float32, device="cuda") for sh in shapes)
+    out_ws = paged_decode_attention(*args, workspace=ws)
+    torch.cuda.synchronize()
+    check_close(out, ref, f"default plan D={D} lens={lens}")
+    assert torch.equal(out, out_ws)
+
+
 @pytest.mark.parametrize("fmt", ["fp16"] + QFORMATS)
 @pytest.mark.parametrize("Hq,Hkv", [(16, 2), (32, 2), (8, 1), (4, 2)])
 def test_units_head_groups(fmt, Hq, Hkv):
