@@ -4,7 +4,7 @@ test_quant_gpu.py and test_units_gpu.py). Needs a GPU.
 Every case decodes INT8 / FP8-e4m3 / INT4 caches written by the library's bulk quantizer and
 compares with float32 attention over the cache dequantized by the numpy spec, at the north
 star's bar for quantized KV (|out - ref| <= 2e-3 + 1e-2 |ref|). Head dim 64 runs the same
-kernel variants as 128 (chunk pairs for 1-4 q heads per kv head); 256 runs the single-chunk
+kernel variants as 128 (chunk pairs for 1-8 q heads per kv head); 256 runs the single-chunk
 kernel with at most 2 chunks in flight.
 """
 import numpy as np
@@ -52,8 +52,9 @@ def test_decode_other_head_dims(D, fmt, bs):
 @pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("D", HEAD_DIMS)
 def test_head_groups_other_head_dims(D, fmt):
-    """1, 2 and 4 q heads per kv head (chunk pairs at D = 64), 5 and 8 (one chain), 16 (two
-    chains) and 20 (two head blocks of 10), split and work-unit paths."""
+    """1, 2 and 4 q heads per kv head (chunk pairs at D = 64), 5 and 8 (chunk pairs with hi /
+    lo columns at D = 64, one chain at 256), 16 (two chains) and 20 (two head blocks of 10),
+    split and work-unit paths."""
     from kvq_decode_amd import paged_decode_attention
     for Hq, Hkv in ((8, 8), (4, 2), (8, 2), (10, 2), (16, 2), (32, 2), (40, 2)):
         args, kw, ref = case(fmt, D, [700, 3], Hq=Hq, Hkv=Hkv, seed=2)
