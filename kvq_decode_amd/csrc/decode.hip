@@ -196,6 +196,71 @@ __device__ __forceinline__ void chunk_f16(const ChunkF16<D>& ch, const h8* qop, 
     }
 }
 
+// Two chunks a, b at once, for head dims up to 64, whose chunks carry few bytes for the
+// same softmax work: each chunk's QK^T into its own accumulator (the two K tiles staged in
+// turn through the wave's tile: its LDS operations run in order), one softmax update over
+// the lane's 8 scores, and one 16x16x32 PV product per tile over both chunks' 32 tokens
+// (k-slots 8g + r: chunk a's token 4g + r, 8g + 4 + r: chunk b's; the lane's P values
+// are already in that order). Both chunks are fully valid.
+template <int D>
+__device__ __forceinline__ void chunk_pair_f16(const ChunkF16<D>& ca, const ChunkF16<D>& cb,
+                                               const h8* qop, float sl2, int g, char* kst,
+                                               SoftmaxState<D>& st) {
+    typedef ChunkF16<D> C;
+    constexpr int NST = C::NST;
+    constexpr int DV = C::DV;
+    const int lane = __lane_id();
+    f4 s[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const ChunkF16<D>& ch = j ? cb : ca;
+#pragma unroll
+        for (int i = 0; i < NST; ++i)
+            *(h8*)(kst + kstage_off<D>(C::RPL * i + lane / C::PC, lane % C::PC)) = ch.k[i];
+        h8 kop[NST];
+#pragma unroll
+        for (int k = 0; k < NST; ++k)
+            kop[k] = *(const h8*)(kst + kstage_off<D>(lane & 15, 4 * k + g));
+        s[j] = (f4)0.f;
+#pragma unroll
+        for (int k = 0; k < NST; ++k)
+            s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[k], qop[k], s[j], 0, 0, 0);
+    }
+    float s2[8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        s2[r] = s[0][r] * sl2;
+        s2[4 + r] = s[1][r] * sl2;
+    }
+    float lm = fmaxf(fmaxf(s2[0], s2[1]), fmaxf(s2[2], s2[3]));
+    lm = fmaxf(lm, fmaxf(fmaxf(s2[4], s2[5]), fmaxf(s2[6], s2[7])));
+    float alpha = 1.f;
+    if (__builtin_amdgcn_ballot_w64(lm > st.m + kLazyMax) != 0) {
+        const float mn = fmaxf(st.m, rows_max(lm));
+        alpha = fast_exp2(st.m - mn);
+        st.m = mn;
+    }
+    st.l *= alpha;
+    float pr[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) pr[r] = fast_exp2(s2[r] - st.m);
+    st.l += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+    h8 pop;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) pop[r] = (_Float16)pr[r];
+#pragma unroll
+    for (int t = 0; t < DV; ++t) {
+        h8 a;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            a[r] = ca.v[r][t];
+            a[4 + r] = cb.v[r][t];
+        }
+        st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pop, st.acc[t] * alpha, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 // P-deep register ring: chunk c + P is loaded while chunk c computes, the block-table
 // entries of chunks c + 2P .. c + 3P - 1 meanwhile. Every load is issued on every path
 // (chunks past the wave's last fully valid chunk re-read that chunk and are not used), so
@@ -243,29 +308,49 @@ __device__ __forceinline__ void f16_range(const DecodeParams& p, int kvh, int b,
     extern __shared__ __attribute__((aligned(16))) float smem[];
     char* kst = (char*)smem + wave * 32 * D;
 
+    // Head dims up to 64 run chunk pairs (w_lo + 2k, w_lo + 2k + 1), the wave's odd last
+    // full chunk alone; the ring holds at least 2 chunks (depth 1 runs as 2), so the ring
+    // depth never changes the arithmetic.
+    constexpr bool PAIRS = D <= 64;
+    constexpr int PR = PAIRS && P < 2 ? 2 : P;
     const int r_hi = min(w_hi, c_full);
     if (w_lo < r_hi) {
         const F16LaneOff<D> lo = f16_lane_offsets<D>(p, i16, g, 15);
         const int last = r_hi - 1;
-        ChunkF16<D> ring[P];
-        int pg_cur = chunk_pages<P>(p, b, w_lo, last, 0, 0);
-        int pg_nxt = chunk_pages<P>(p, b, w_lo + P, last, 0, 0);
+        ChunkF16<D> ring[PR];
+        int pg_cur = chunk_pages<PR>(p, b, w_lo, last, 0, 0);
+        int pg_nxt = chunk_pages<PR>(p, b, w_lo + PR, last, 0, 0);
         // Issued slot by slot: a slot's loads moved behind a later slot's would make the
         // ring's waits (vmcnt counts the loads issued after the awaited one) drain it.
 #pragma unroll
-        for (int i = 0; i < P; ++i) {
+        for (int i = 0; i < PR; ++i) {
             load_chunk_f16<D>(p, kvc, min(w_lo + i, last), lo,
                               __builtin_amdgcn_readlane(pg_cur, i), ring[i]);
             __builtin_amdgcn_sched_barrier(0);
         }
-        for (int c0 = w_lo; c0 < r_hi; c0 += P) {
-            pg_cur = pg_nxt;  // pages of chunks c0 + P .. c0 + 2P - 1
-            pg_nxt = chunk_pages<P>(p, b, c0 + 2 * P, last, 0, 0);
+        for (int c0 = w_lo; c0 < r_hi; c0 += PR) {
+            pg_cur = pg_nxt;  // pages of chunks c0 + PR .. c0 + 2PR - 1
+            pg_nxt = chunk_pages<PR>(p, b, c0 + 2 * PR, last, 0, 0);
+            if constexpr (PAIRS) {
 #pragma unroll
-            for (int i = 0; i < P; ++i) {
-                if (c0 + i < r_hi) chunk_f16<D, false>(ring[i], qop, sl2, 16, g, kst, st);
-                load_chunk_f16<D>(p, kvc, min(c0 + i + P, last), lo,
-                                  __builtin_amdgcn_readlane(pg_cur, i), ring[i]);
+                for (int i = 0; i < PR; i += 2) {
+                    const int c = c0 + i;
+                    if (c + 1 < r_hi)
+                        chunk_pair_f16<D>(ring[i], ring[i + 1], qop, sl2, g, kst, st);
+                    else if (c < r_hi)
+                        chunk_f16<D, false>(ring[i], qop, sl2, 16, g, kst, st);
+                    load_chunk_f16<D>(p, kvc, min(c + PR, last), lo,
+                                      __builtin_amdgcn_readlane(pg_cur, i), ring[i]);
+                    load_chunk_f16<D>(p, kvc, min(c + 1 + PR, last), lo,
+                                      __builtin_amdgcn_readlane(pg_cur, i + 1), ring[i + 1]);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < PR; ++i) {
+                    if (c0 + i < r_hi) chunk_f16<D, false>(ring[i], qop, sl2, 16, g, kst, st);
+                    load_chunk_f16<D>(p, kvc, min(c0 + i + PR, last), lo,
+                                      __builtin_amdgcn_readlane(pg_cur, i), ring[i]);
+                }
             }
         }
     }
