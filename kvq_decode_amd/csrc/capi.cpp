@@ -349,6 +349,14 @@ int units_params(const kvq_decode_args* args, int32_t units, float* o_part, floa
     return KVQ_OK;
 }
 
+// Head dims below 128 move fewer bytes per 16-token chunk through about the same per-chunk
+// work, so they need proportionally more waves in flight. Measured on MI355X (32 q / 8 kv
+// heads, full steps): fp16 at head_dim 64 0.43 -> 0.72 of peak at batch 8 x 32k and 0.37
+// -> 0.57 at batch 1 x 64k, at head_dim 32 0.14 -> 0.27; quantized work units +1-19% at
+// head_dim 64. The quantized split plan (single sequences) measured 2-9% slower with the
+// extra waves and keeps the 128 plan, and so does head_dim 256 everywhere.
+int64_t head_dim_scale(int32_t head_dim) { return head_dim < 128 ? 128 / head_dim : 1; }
+
 }  // namespace
 
 extern "C" {
@@ -392,14 +400,6 @@ int kvq_choose_num_splits(int32_t batch, int32_t kv_heads, int32_t block_size,
     const int64_t s = p2 < cap ? p2 : cap;
     return int(s < 1 ? 1 : s);
 }
-
-// Head dims below 128 move fewer bytes per 16-token chunk through about the same per-chunk
-// work, so they need proportionally more waves in flight. Measured on MI355X (32 q / 8 kv
-// heads, full steps): fp16 at head_dim 64 0.43 -> 0.72 of peak at batch 8 x 32k and 0.37
-// -> 0.57 at batch 1 x 64k, at head_dim 32 0.14 -> 0.27; quantized work units +1-19% at
-// head_dim 64. The quantized split plan (single sequences) measured 2-9% slower with the
-// extra waves and keeps the 128 plan, and so does head_dim 256 everywhere.
-int64_t head_dim_scale(int32_t head_dim) { return head_dim < 128 ? 128 / head_dim : 1; }
 
 int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t max_pages,
                     int32_t kv_format, int32_t head_dim, int32_t cu_count, int32_t* splits_out,
