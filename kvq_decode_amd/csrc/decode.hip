@@ -261,6 +261,191 @@ __device__ __forceinline__ void chunk_pair_f16(const ChunkF16<D>& ca, const Chun
     }
 }
 
+// Reference max a quad-step stream starts from: finite, so that a slot that has seen no
+// valid token yet (all scores -inf) gets p = 2^(-inf - m) = 0 rather than NaN, and its
+// first real scores rescale it by 2^(m - m') = 0.
+constexpr float kQuadM0 = -1e30f;
+
+// Four chunks at once, for head dim 32 and at most 4 q heads per kv head: the 16
+// MFMA columns hold 4 chunk slots x 4 heads (column j: head j & 3, slot j >> 2), so every
+// column's softmax works on real scores (the single-chunk step runs it on 16 columns, of
+// which G are heads). Each chunk's QK^T goes into its own accumulator against the same Q^T
+// (head j & 3 in column j) and each lane keeps its slot's scores; PV is two 16x16x32
+// products, over chunks (0, 1) and (2, 3) (k-slots 8g + r: the pair's first chunk's token
+// 4g + r, 8g + 4 + r: the second's), each lane's P in its slot's half of its product and
+// zeros elsewhere. A lane's state is its slot's stream; f16_quad_range merges the 4 streams
+// of a head (columns j, j ^ 4, j ^ 8, j ^ 12) at the end. Slot s takes its chunk's first
+// valid_s tokens (MASK; 0 = an empty slot). Measured at B8 x 32k, 32 q / 8 kv heads, stage 1
+// at the default plan: head dim 32 95.1 -> 88.2 us against chunk pairs, but head dim 64
+// 85.7 -> 94.6 us (its 4-chunk ring has nothing in flight while a quad computes).
+template <int D, bool MASK>
+__device__ __forceinline__ void chunk_quad_f16(const ChunkF16<D>* ch, const h8* qop, float sl2,
+                                               int valid0, int valid1, int valid2, int valid3,
+                                               int g, char* kst, SoftmaxState<D>& st) {
+    typedef ChunkF16<D> C;
+    constexpr int NST = C::NST;
+    constexpr int DV = C::DV;
+    const int lane = __lane_id();
+    const int slot = (lane & 15) >> 2;
+    f4 s[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int i = 0; i < NST; ++i)
+            *(h8*)(kst + kstage_off<D>(C::RPL * i + lane / C::PC, lane % C::PC)) = ch[j].k[i];
+        h8 kop[NST];
+#pragma unroll
+        for (int k = 0; k < NST; ++k)
+            kop[k] = *(const h8*)(kst + kstage_off<D>(lane & 15, 4 * k + g));
+        s[j] = (f4)0.f;
+#pragma unroll
+        for (int k = 0; k < NST; ++k)
+            s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[k], qop[k], s[j], 0, 0, 0);
+    }
+    float s2[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float x = slot == 0 ? s[0][r] : slot == 1 ? s[1][r] : slot == 2 ? s[2][r] : s[3][r];
+        s2[r] = x * sl2;
+    }
+    if (MASK) {
+        const int v = slot == 0 ? valid0 : slot == 1 ? valid1 : slot == 2 ? valid2 : valid3;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s2[r] = 4 * g + r < v ? s2[r] : -INFINITY;
+    }
+    const float lm = fmaxf(fmaxf(s2[0], s2[1]), fmaxf(s2[2], s2[3]));
+    float alpha = 1.f;
+    if (__builtin_amdgcn_ballot_w64(lm > st.m + kLazyMax) != 0) {
+        const float mn = fmaxf(st.m, rows_max(lm));
+        alpha = fast_exp2(st.m - mn);
+        st.m = mn;
+    }
+    st.l *= alpha;
+    float pr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(s2[r] - st.m);
+    st.l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+    h8 b01, b23;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const _Float16 x = (_Float16)pr[r], z = (_Float16)0.f;
+        b01[r] = slot == 0 ? x : z;
+        b01[4 + r] = slot == 1 ? x : z;
+        b23[r] = slot == 2 ? x : z;
+        b23[4 + r] = slot == 3 ? x : z;
+    }
+#pragma unroll
+    for (int t = 0; t < DV; ++t) {
+        h8 a01, a23;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            a01[r] = ch[0].v[r][t];
+            a01[4 + r] = ch[1].v[r][t];
+            a23[r] = ch[2].v[r][t];
+            a23[4 + r] = ch[3].v[r][t];
+        }
+        st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a01, b01, st.acc[t] * alpha, 0, 0, 0);
+        st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a23, b23, st.acc[t], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// f16_range for head dim 32 and at most 4 q heads per kv head: quad steps over a
+// 4-chunk ring (chunks w_lo + 4k .. w_lo + 4k + 3; the wave's last full chunks, fewer than
+// 4, fill the first slots of a masked step, the sequence's partial last chunk slot 0 of
+// one more), then the 4 slot streams of each head merged and stored as in f16_range.
+template <int D, int W, bool FINAL>
+__device__ __forceinline__ void f16_quad_range(const DecodeParams& p, int kvh, int b,
+                                               int seq_len, int w_lo, int w_hi, int wave,
+                                               int64_t part_base, int64_t part_stride) {
+    constexpr int NST = D / 32;
+    constexpr int DV = D / 16;
+    const int lane = threadIdx.x & 63;
+    const int i16 = lane & 15, g = lane >> 4;
+    const int G = p.group;
+    const int head = i16 & 3;  // column j holds head j & 3
+    const bool head_ok = head < G;
+    const int c_full = seq_len >> 4;
+    const int kvc = cache_head(p, kvh);
+    h8 qop[NST];
+    {
+        const _Float16* qrow = (const _Float16*)p.q + (int64_t)b * p.q_sb +
+                               (int64_t)(kvh * G + (head_ok ? head : 0)) * p.q_sh + 8 * g;
+#pragma unroll
+        for (int k = 0; k < NST; ++k) {
+            h8 x = *(const h8*)(qrow + 32 * k);
+            qop[k] = head_ok ? x : (h8)(_Float16)0;
+        }
+    }
+    SoftmaxState<D> st;
+#pragma unroll
+    for (int t = 0; t < DV; ++t) st.acc[t] = (f4)0.f;
+    st.m = kQuadM0;
+    st.l = 0.f;
+    const float sl2 = p.scale_log2;
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    char* kst = (char*)smem + wave * 32 * D;
+
+    const int r_hi = min(w_hi, c_full);
+    if (w_lo < r_hi) {
+        const F16LaneOff<D> lo = f16_lane_offsets<D>(p, i16, g, 15);
+        const int last = r_hi - 1;
+        ChunkF16<D> ring[4];
+        int pg_cur = chunk_pages<4>(p, b, w_lo, last, 0, 0);
+        int pg_nxt = chunk_pages<4>(p, b, w_lo + 4, last, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            load_chunk_f16<D>(p, kvc, min(w_lo + i, last), lo,
+                              __builtin_amdgcn_readlane(pg_cur, i), ring[i]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        for (int c0 = w_lo; c0 < r_hi; c0 += 4) {
+            pg_cur = pg_nxt;  // pages of chunks c0 + 4 .. c0 + 7
+            pg_nxt = chunk_pages<4>(p, b, c0 + 8, last, 0, 0);
+            const int n = min(r_hi - c0, 4);
+            if (n == 4)
+                chunk_quad_f16<D, false>(ring, qop, sl2, 16, 16, 16, 16, g, kst, st);
+            else
+                chunk_quad_f16<D, true>(ring, qop, sl2, 16, n > 1 ? 16 : 0, n > 2 ? 16 : 0, 0,
+                                        g, kst, st);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                load_chunk_f16<D>(p, kvc, min(c0 + 4 + i, last), lo,
+                                  __builtin_amdgcn_readlane(pg_cur, i), ring[i]);
+        }
+    }
+    if (w_lo <= r_hi && r_hi < w_hi) {  // this wave owns the partial last chunk c_full
+        const int c = r_hi;
+        const int valid = seq_len - (c << 4);
+        const int pg = chunk_pages<1>(p, b, c, c, 0, 0);
+        ChunkF16<D> q4[4];
+        load_chunk_f16<D>(p, kvc, c, f16_lane_offsets<D>(p, i16, g, valid - 1),
+                          __builtin_amdgcn_readlane(pg, 0), q4[0]);
+        q4[1] = q4[0];
+        q4[2] = q4[0];
+        q4[3] = q4[0];
+        chunk_quad_f16<D, true>(q4, qop, sl2, valid, 0, 0, 0, g, kst, st);
+    }
+
+    // the 4 slot streams of each head: columns j, j ^ 4, j ^ 8, j ^ 12
+#pragma unroll
+    for (int x = 4; x <= 8; x <<= 1) {
+        const float m_o = __shfl_xor(st.m, x), l_o = __shfl_xor(st.l, x);
+        const float M = fmaxf(st.m, m_o);
+        const float wa = fast_exp2(st.m - M), wb = fast_exp2(m_o - M);
+        st.l = wa * st.l + wb * l_o;
+#pragma unroll
+        for (int t = 0; t < DV; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                st.acc[t][r] = wa * st.acc[t][r] + wb * __shfl_xor(st.acc[t][r], x);
+        st.m = M;
+    }
+    __syncthreads();  // every wave is done with its staging tile
+    combine_store<D, W, FINAL>(p, st.acc, 1.f, 0.f, st.m, rows_sum(st.l), wave, i16, g, kvh, b,
+                               part_base, part_stride);
+}
+
 // P-deep register ring: chunk c + P is loaded while chunk c computes, the block-table
 // entries of chunks c + 2P .. c + 3P - 1 meanwhile. Every load is issued on every path
 // (chunks past the wave's last fully valid chunk re-read that chunk and are not used), so
@@ -276,6 +461,13 @@ __device__ __forceinline__ void f16_range(const DecodeParams& p, int kvh, int b,
                                           int64_t part_stride) {
     constexpr int NST = D / 32;
     constexpr int DV = D / 16;
+    if constexpr (D <= 32) {
+        if (p.group <= 4) {
+            f16_quad_range<D, W, FINAL>(p, kvh, b, seq_len, w_lo, w_hi, wave, part_base,
+                                        part_stride);
+            return;
+        }
+    }
 
     const int lane = threadIdx.x & 63;
     const int i16 = lane & 15, g = lane >> 4;
