@@ -310,7 +310,8 @@ def test_chunk_pairs_five_to_eight_heads(fmt, G):
     (the hi and lo lanes of a head each weight one chunk): a one-token sequence, partial
     last chunks and odd chunk counts (single-chunk steps at both ends of a wave), single
     pass, splits, work units and the default plan; every ring depth and workgroup shape
-    within tolerance, and the ring depth never changes a result bit."""
+    within tolerance, and the ring depth never changes a result bit; K groups of 16
+    chunks."""
     from kvq_decode_amd import paged_decode_attention
     from kvq_decode_amd.quant import quantize_paged_cache
     Hkv = 2
@@ -331,6 +332,16 @@ def test_chunk_pairs_five_to_eight_heads(fmt, G):
                     for ring in (1, 2, 4)]
             check_close(outs[0], ref, f"{fmt} G={G} splits={splits} waves={waves}")
             assert all(torch.equal(outs[0], o) for o in outs[1:]), (fmt, G, splits, waves)
+    # K groups of 16 chunks: a group's q'' serves several pair steps
+    qc = quantize_paged_cache(gpu(kc), gpu(vc), gpu(bt), gpu(sl), fmt, k_group=256)
+    host = {n: getattr(qc, n).cpu().numpy() for n in
+            ("k_codes", "v_codes", "k_scale", "k_zero", "v_scale", "v_zero")}
+    kd, vd = kivi.dequantize_paged_cache(host, bt, sl, fmt, group=256)
+    ref = paged_decode_attention_ref(q.astype(np.float32), kd, vd, bt, sl, out_dtype=np.float32)
+    args = (gpu(q), qc.k_codes, qc.v_codes, gpu(bt), gpu(sl))
+    for extra in ({"num_splits": 3}, {"units": 7}):
+        out = paged_decode_attention(*args, **extra, **qc.decode_kwargs())
+        check_close(out, ref, f"{fmt} G={G} k_group=256 {extra}")
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
