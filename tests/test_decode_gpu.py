@@ -155,6 +155,26 @@ def test_ring_depths_other_head_dims(D, pipeline):
         check_close(out, ref, f"D={D} pipe={pipeline} splits={splits}")
 
 
+@pytest.mark.parametrize("Hq,Hkv", [(4, 4), (4, 2), (16, 4)])
+@pytest.mark.parametrize("D", [32, 64])
+def test_small_head_dim_chunk_groups(Hq, Hkv, D):
+    """Head dim 32 with up to 4 q heads per kv head runs 4-chunk steps (chunk slots in the MFMA
+    columns), head dim 64 2-chunk steps: lengths that leave 1, 2 and 3 full chunks after the
+    last full step and partial last chunks, on the single-pass, split, work-unit and default
+    paths against the oracle, and every ring depth gives the same bits."""
+    from kvq_decode_amd import paged_decode_attention
+    lens = [16 * 4 + 5, 16 * 5, 16 * 6 + 1, 16 * 7, 1, 16 * 37 + 9]
+    q, kc, vc, bt, sl = make(Hq, Hkv, D, 16, lens, seed=23)
+    ref = paged_decode_attention_ref(q, kc, vc, bt, sl, out_dtype=np.float32)
+    args = to_gpu(q, kc, vc, bt, sl)
+    for extra in ({"num_splits": 1}, {"num_splits": 3}, {"units": 5}, {}):
+        out = paged_decode_attention(*args, **extra)
+        check_close(out, ref, f"D={D} Hq={Hq} Hkv={Hkv} {extra}")
+    for extra in ({"num_splits": 2}, {"units": 3}):
+        outs = [paged_decode_attention(*args, pipeline=ring, **extra) for ring in (1, 2, 4)]
+        assert all(torch.equal(outs[0], o) for o in outs[1:]), (D, Hq, Hkv, extra)
+
+
 def _baseline_case(B, ctx, pool, seed=0):
     """q, K, V ~ N(0,1) fp16, block_table a random permutation of the
     pool, block_size 16, every sequence ctx tokens (generated on the GPU, copied back
