@@ -33,6 +33,9 @@ def test_library_exports_every_declared_symbol():
                          text=True).stdout
     exported = sorted(set(re.findall(r"\bT (kvq_\w+)$", out, re.M)))
     assert exported == names
+    # and no other C-linkage function (C++ helpers are mangled, runtime symbols start with _)
+    c_functions = sorted(set(re.findall(r"\bT ([A-Za-z]\w*)$", out, re.M)))
+    assert c_functions == names, sorted(set(c_functions) - set(names))
 
 
 def test_struct_layout_matches_header():
