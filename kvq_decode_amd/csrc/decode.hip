@@ -446,6 +446,64 @@ __device__ __forceinline__ void f16_quad_range(const DecodeParams& p, int kvh, i
                                part_base, part_stride);
 }
 
+// Ring depth of f16_range: head dims up to 64 run chunk pairs and keep at least 2 chunks
+// in flight.
+template <int D, int P>
+constexpr int f16_ring() { return D <= 64 && P < 2 ? 2 : P; }
+
+// The rows of the Q^T operand of kv head kvh of sequence b, unmasked: lane (i16, g) loads
+// Q[head][32*k + 8*g + 0..7] of head i16, or of head 0 for the padding lanes i16 >= group,
+// whose operand q_operand then zeroes. Loads only, so a caller can issue them ahead.
+template <int D>
+__device__ __forceinline__ void load_q_raw(const DecodeParams& p, int kvh, int b, h8* qraw) {
+    const int lane = threadIdx.x & 63;
+    const int i16 = lane & 15, g = lane >> 4;
+    const int G = p.group;
+    const _Float16* qrow = (const _Float16*)p.q + (int64_t)b * p.q_sb +
+                           (int64_t)(kvh * G + (i16 < G ? i16 : 0)) * p.q_sh + 8 * g;
+#pragma unroll
+    for (int k = 0; k < D / 32; ++k) qraw[k] = *(const h8*)(qrow + 32 * k);
+}
+
+template <int D>
+__device__ __forceinline__ void q_operand(const DecodeParams& p, const h8* qraw, h8* qop) {
+    const bool head_ok = (threadIdx.x & 15) < p.group;
+#pragma unroll
+    for (int k = 0; k < D / 32; ++k) qop[k] = head_ok ? qraw[k] : (h8)(_Float16)0;
+}
+
+// The first loads of a wave's range, issued ahead by the work units for their guessed
+// first segment (decode_common.h for_unit_segments) and not used there: the q rows of
+// sequence b and the raw block-table entries of the ring's first two fills for the range
+// [w_lo, last].
+template <int D, int P>
+struct F16Pre {
+    h8 qraw[D / 32];
+    int pg_cur, pg_nxt;
+    int b, w_lo, last;
+    bool live;
+};
+
+template <int D, int P>
+__device__ __forceinline__ F16Pre<D, P> f16_prefetch(const DecodeParams& p, int kvh,
+                                                     const SegGuess& gs) {
+    constexpr int PR = f16_ring<D, P>();
+    F16Pre<D, P> f;
+    f.live = false;
+    if constexpr (D == 128) {  // the other head dims' kernels take no prefetch (registers)
+        f.live = gs.live;
+        f.b = gs.b;
+        f.w_lo = gs.w_lo;
+        f.last = min(gs.w_hi, gs.seq_len >> 4) - 1;
+        // indices stay inside row b of the table: chunks >= 0 and <= max(last, 0)
+        const int last0 = max(f.last, 0);
+        load_q_raw<D>(p, kvh, gs.b, f.qraw);
+        f.pg_cur = chunk_pages_raw<PR>(p, gs.b, min(f.w_lo, last0), last0, 0, 0);
+        f.pg_nxt = chunk_pages_raw<PR>(p, gs.b, min(f.w_lo + PR, last0), last0, 0, 0);
+    }
+    return f;
+}
+
 // P-deep register ring: chunk c + P is loaded while chunk c computes, the block-table
 // entries of chunks c + 2P .. c + 3P - 1 meanwhile. Every load is issued on every path
 // (chunks past the wave's last fully valid chunk re-read that chunk and are not used), so
@@ -455,10 +513,15 @@ __device__ __forceinline__ void f16_quad_range(const DecodeParams& p, int kvh, i
 // f16_range runs one wave's chunk range [w_lo, w_hi) of sequence b (of length seq_len)
 // for kv head kvh and stores the workgroup's result (partial rows part_base + h *
 // part_stride, or the output row for FINAL).
+//
+// `pre` holds loads issued ahead for a guessed range (f16_prefetch); with use_pre, those
+// that match this range (same sequence; same first chunk and last full chunk) replace the
+// range's own.
 template <int D, int W, bool FINAL, int P>
 __device__ __forceinline__ void f16_range(const DecodeParams& p, int kvh, int b, int seq_len,
                                           int w_lo, int w_hi, int wave, int64_t part_base,
-                                          int64_t part_stride) {
+                                          int64_t part_stride, const F16Pre<D, P>& pre,
+                                          bool use_pre) {
     constexpr int NST = D / 32;
     constexpr int DV = D / 16;
     if constexpr (D <= 32) {
@@ -471,21 +534,18 @@ __device__ __forceinline__ void f16_range(const DecodeParams& p, int kvh, int b,
 
     const int lane = threadIdx.x & 63;
     const int i16 = lane & 15, g = lane >> 4;
-    const int G = p.group;
-    const bool head_ok = i16 < G;
     const int c_full = seq_len >> 4;  // chunks below this index are fully valid
     const int kvc = cache_head(p, kvh);
+    const bool pre_b = use_pre && pre.live && pre.b == b;
 
     // Q^T operand: lane (head i16, g) holds Q[head][32*k + 8*g + 0..7]; padded heads = 0.
     h8 qop[NST];
-    {
-        const _Float16* qrow = (const _Float16*)p.q + (int64_t)b * p.q_sb +
-                               (int64_t)(kvh * G + (head_ok ? i16 : 0)) * p.q_sh + 8 * g;
-#pragma unroll
-        for (int k = 0; k < NST; ++k) {
-            h8 x = *(const h8*)(qrow + 32 * k);
-            qop[k] = head_ok ? x : (h8)(_Float16)0;
-        }
+    if (pre_b) {
+        q_operand<D>(p, pre.qraw, qop);
+    } else {
+        h8 qraw[NST];
+        load_q_raw<D>(p, kvh, b, qraw);
+        q_operand<D>(p, qraw, qop);
     }
 
     SoftmaxState<D> st;
@@ -504,14 +564,20 @@ __device__ __forceinline__ void f16_range(const DecodeParams& p, int kvh, int b,
     // full chunk alone; the ring holds at least 2 chunks (depth 1 runs as 2), so the ring
     // depth never changes the arithmetic.
     constexpr bool PAIRS = D <= 64;
-    constexpr int PR = PAIRS && P < 2 ? 2 : P;
+    constexpr int PR = f16_ring<D, P>();
     const int r_hi = min(w_hi, c_full);
     if (w_lo < r_hi) {
         const F16LaneOff<D> lo = f16_lane_offsets<D>(p, i16, g, 15);
         const int last = r_hi - 1;
         ChunkF16<D> ring[PR];
-        int pg_cur = chunk_pages<PR>(p, b, w_lo, last, 0, 0);
-        int pg_nxt = chunk_pages<PR>(p, b, w_lo + PR, last, 0, 0);
+        int pg_cur, pg_nxt;
+        if (pre_b && pre.w_lo == w_lo && pre.last == last) {
+            pg_cur = clamp_page(p, pre.pg_cur);
+            pg_nxt = clamp_page(p, pre.pg_nxt);
+        } else {
+            pg_cur = chunk_pages<PR>(p, b, w_lo, last, 0, 0);
+            pg_nxt = chunk_pages<PR>(p, b, w_lo + PR, last, 0, 0);
+        }
         // Issued slot by slot: a slot's loads moved behind a later slot's would make the
         // ring's waits (vmcnt counts the loads issued after the awaited one) drain it.
 #pragma unroll
@@ -569,8 +635,9 @@ void decode_f16_kernel(const DecodeParams p) {
     const WgCoord wc = wg_coord(p, FINAL ? 1 : p.num_splits);
     if (!wc.live) return;
     const WaveRange wr = wave_range<W>(p, wc.b, wc.split, wave);
+    const F16Pre<D, P> none{};
     f16_range<D, W, FINAL, P>(p, wc.kvh, wc.b, wr.seq_len, wr.w_lo, wr.w_hi, wave,
-                              split_part_base(p, wc.b, wc.split), p.num_splits);
+                              split_part_base(p, wc.b, wc.split), p.num_splits, none, false);
 }
 
 // Work units (decode_common.h UnitSpace): workgroup = (kv head, unit), W waves; the unit
@@ -579,10 +646,13 @@ template <int D, int W, int P>
 __global__ __launch_bounds__(W * 64)
 void decode_f16_units_kernel(const DecodeParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    for_unit_segments<W>(p, [&](int kvh, int b, int seq_len, int w_lo, int w_hi, int64_t base,
-                                int64_t stride) {
-        f16_range<D, W, false, P>(p, kvh, b, seq_len, w_lo, w_hi, wave, base, stride);
-    });
+    for_unit_segments<W>(
+        p, [&](int kvh, const SegGuess& gs) { return f16_prefetch<D, P>(p, kvh, gs); },
+        [&](int kvh, int b, int seq_len, int w_lo, int w_hi, int64_t base, int64_t stride,
+            const F16Pre<D, P>& pf, bool first) {
+            f16_range<D, W, false, P>(p, kvh, b, seq_len, w_lo, w_hi, wave, base, stride, pf,
+                                      first);
+        });
 }
 
 // Merges the S partial rows row0 .. row0 + S - 1 into the fp16 output row `out`.

@@ -57,9 +57,13 @@ constexpr float kLazyMax = 8.0f;
 // V (scale, zero) groups (lane 2P + j, 2^vshift chunks), chunks clamped to `last` so the
 // load is issued on every path. Used one ring ahead: the compiler's wait for this
 // register then counts the chunk loads issued since, and never drains the loads in flight.
+//
+// chunk_pages_raw is the block-table load alone (c >= 0 and last >= 0 keep it inside the
+// sequence's table row), clamp_page the clamp of an entry into the pool; a caller that
+// issues the load ahead of its use applies the clamp at the use.
 template <int P>
-__device__ __forceinline__ int chunk_pages(const DecodeParams& p, int b, int c, int last,
-                                           int gshift, int vshift) {
+__device__ __forceinline__ int chunk_pages_raw(const DecodeParams& p, int b, int c, int last,
+                                               int gshift, int vshift) {
     static_assert(4 * P <= 64, "three lane regions of P chunks in one wave");
     const int j = __lane_id() & (4 * P - 1);
     int cj = min(c + (j & (P - 1)), last);
@@ -68,8 +72,17 @@ __device__ __forceinline__ int chunk_pages(const DecodeParams& p, int b, int c, 
     } else if (j >= P) {
         cj = (cj >> gshift) << gshift;
     }
-    const int phys = p.bt[(int64_t)b * p.bt_sb + (cj >> p.cpp_shift)];
+    return p.bt[(int64_t)b * p.bt_sb + (cj >> p.cpp_shift)];
+}
+
+__device__ __forceinline__ int clamp_page(const DecodeParams& p, int phys) {
     return min(max(phys, 0), p.num_blocks - 1);
+}
+
+template <int P>
+__device__ __forceinline__ int chunk_pages(const DecodeParams& p, int b, int c, int last,
+                                           int gshift, int vshift) {
+    return clamp_page(p, chunk_pages_raw<P>(p, b, c, last, gshift, vshift));
 }
 
 // Buffer resource for raw (untyped) loads at a wave-uniform base: stride 0, no range
@@ -263,12 +276,16 @@ template <int PER>
 __device__ __forceinline__ void unit_prefix(const DecodeParams& p, int* pref, int* len_out,
                                             int t, int per) {
     const int B = p.batch, cap = p.max_blocks * p.block_size;
+    // all PER loads first, at clamped indices (no branch between a load and the next)
+    int raw[PER];
+#pragma unroll
+    for (int e = 0; e < PER; ++e) raw[e] = p.seq_lens[min(per * t + e, B - 1)];
     int n[PER], local = 0;
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
         const int b = per * t + e;
         const bool mine = e < per && b < B;
-        const int len = mine ? min(max(p.seq_lens[b], 0), cap) : 0;
+        const int len = mine ? min(max(raw[e], 0), cap) : 0;
         if (mine) len_out[b] = len;
         n[e] = cdiv(len, 16);
         local += n[e];
@@ -289,16 +306,54 @@ __device__ __forceinline__ void unit_prefix(const DecodeParams& p, int* pref, in
     if (t == 63) pref[B] = incl;
 }
 
-// Runs fn(kvh, b, seq_len, w_lo, w_hi, part_base, part_stride) for each segment of this
-// workgroup's unit (workgroup = (kv head, unit), W waves), in batch order, with a
+// The calling wave's share of its unit's first segment in the partition where every
+// sequence fills its block-table row (n_b = max_blocks * block_size / 16 for all b, so
+// P_b = b * n_b): what for_unit_segments computes from the scanned prefix whenever every
+// sequence of the batch has that chunk count. `live` is false for a unit past that
+// partition's last (its fields then describe the last unit's share, inside the batch).
+struct SegGuess {
+    int b, seq_len, w_lo, w_hi;
+    bool live;
+};
+
+template <int W>
+__device__ __forceinline__ SegGuess unit_guess(const DecodeParams& p, int u, int wave) {
+    const int cap = p.max_blocks * p.block_size;  // a multiple of 16
+    const int ng = cap >> 4;
+    UnitSpace ug;
+    ug.N = p.batch * ng;  // the host checks batch * cdiv(cap, 16) <= INT32_MAX
+    ug.NU = min(p.units, ug.N);
+    SegGuess g;
+    g.live = u < ug.NU;
+    const int uu = min(u, ug.NU - 1);
+    const int lo = unit_lo(ug, uu), hi = unit_lo(ug, uu + 1);
+    g.b = lo / ng;
+    const int p0 = g.b * ng;
+    const int c_lo = lo - p0, c_hi = min(hi - p0, ng);
+    const int per = cdiv(c_hi - c_lo, W);
+    g.w_lo = min(c_lo + wave * per, c_hi);
+    g.w_hi = min(g.w_lo + per, c_hi);
+    g.seq_len = cap;
+    return g;
+}
+
+// Runs fn(kvh, b, seq_len, w_lo, w_hi, part_base, part_stride, pf, first) for each segment
+// of this workgroup's unit (workgroup = (kv head, unit), W waves), in batch order, with a
 // barrier between segments (they reuse the LDS of the range functions). [w_lo, w_hi) is
 // the calling wave's contiguous share of the segment's chunks.
+//
+// The segments come from the batch's chunk prefix, which wave 0 scans from seq_lens, and a
+// segment's first loads (q, block-table entries) depend on it: one more dependent memory
+// round trip before the first KV bytes than a split has. Every wave therefore first calls
+// pf = pre(kvh, guess) with its unit_guess share, which issues those loads for the
+// guessed segment without using them, so they travel with the seq_lens loads; fn gets pf
+// and first = true for the unit's first segment, and uses what matches the real one.
 //
 // Workgroup order: plain (kv head fastest), or with xcd_group and units a multiple of
 // kXcds, grouped so that the kv heads of one unit share an XCD (workgroup i runs on XCD
 // i % kXcds) and with it the L2 lines of the V scales, which interleave kv heads.
-template <int W, typename Fn>
-__device__ __forceinline__ void for_unit_segments(const DecodeParams& p, Fn&& fn) {
+template <int W, typename Pre, typename Fn>
+__device__ __forceinline__ void for_unit_segments(const DecodeParams& p, Pre&& pre, Fn&& fn) {
     __shared__ UnitLds s;
     int kvh, u;
     if (p.xcd_group && p.units % kXcds == 0) {
@@ -311,6 +366,7 @@ __device__ __forceinline__ void for_unit_segments(const DecodeParams& p, Fn&& fn
     }
     const int t = threadIdx.x, B = p.batch;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const auto pf = pre(kvh, unit_guess<W>(p, u, wave));
     if (t < 64) {  // lane t: sequences per * t .. per * t + per - 1
         const int per = (B + 63) >> 6;
         if (per <= 4)  // batches up to 256: the short scan
@@ -331,6 +387,7 @@ __device__ __forceinline__ void for_unit_segments(const DecodeParams& p, Fn&& fn
         if (__builtin_amdgcn_readfirstlane(s.pref[mid]) <= lo) b = mid;
         else top = mid;
     }
+    bool first = true;
     for (; b < B; ++b) {
         const int p0 = __builtin_amdgcn_readfirstlane(s.pref[b]);
         if (p0 >= hi) break;
@@ -340,9 +397,21 @@ __device__ __forceinline__ void for_unit_segments(const DecodeParams& p, Fn&& fn
         const int per = cdiv(c_hi - c_lo, W);
         const int w_lo = min(c_lo + wave * per, c_hi), w_hi = min(w_lo + per, c_hi);
         fn(kvh, b, __builtin_amdgcn_readfirstlane(s.len[b]), w_lo, w_hi, (int64_t)u + b,
-           (int64_t)p.units + B);
+           (int64_t)p.units + B, pf, first);
+        first = false;
         __syncthreads();
     }
+}
+
+// Without loads ahead: fn(kvh, b, seq_len, w_lo, w_hi, part_base, part_stride).
+struct NoPrefetch {};
+
+template <int W, typename Fn>
+__device__ __forceinline__ void for_unit_segments(const DecodeParams& p, Fn&& fn) {
+    for_unit_segments<W>(
+        p, [](int, const SegGuess&) { return NoPrefetch{}; },
+        [&](int kvh, int b, int seq_len, int w_lo, int w_hi, int64_t base, int64_t stride,
+            const NoPrefetch&, bool) { fn(kvh, b, seq_len, w_lo, w_hi, base, stride); });
 }
 
 // The chunk range [w_lo, w_hi) of one wave: split `split` of the sequence covers pages
