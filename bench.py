@@ -56,6 +56,11 @@ CONFIGS = {
     "C3": (1, 131072, 8192, "fp16", "C3: fp16 KV, batch 1, seq_len 131072 (reference: split-KV "
            "+ merge)"),
     "B1_64K": (1, 65536, 4096, "fp16", "fp16 KV, batch 1, seq_len 65536 (north-star 50% point)"),
+    # the reference's published "batch 8-32 / ctx 16k-64k" points (bench_triton_fp16.py:17-20)
+    "B8_16K": (8, 16384, 8192, "fp16", "fp16 KV, batch 8, seq_len 16384 (north-star 80% "
+               "corner)"),
+    "B32_16K": (32, 16384, 32768, "fp16", "fp16 KV, batch 32, seq_len 16384"),
+    "B8_64K": (8, 65536, 32768, "fp16", "fp16 KV, batch 8, seq_len 65536"),
     "C4_INT8": (16, 32768, 32768, "int8", "C4: INT8 KIVI KV, batch 16, seq_len 32768"),
     "C4_FP8": (16, 32768, 32768, "fp8_e4m3", "C4: FP8-e4m3 KIVI KV, batch 16, seq_len 32768"),
     "B16_FP16": (16, 32768, 32768, "fp16", "fp16 KV, batch 16, seq_len 32768 (INT4 comparison)"),
@@ -604,20 +609,22 @@ def counter_summary(config, pmc_dir):
     log(f"wrote {path}")
 
 
-def default_plan(config, B, max_pages, cu_count=None, hkv=HKV, fmt_name=None, head_dim=D):
+def default_plan(config, B, max_pages, cu_count=None, hkv=HKV, fmt_name=None, head_dim=D,
+                 hq=HQ):
     """(splits, waves, units) the op would use with num_splits=None: the work-unit plan
     (units > 0) where the library prefers it, else the split plan (C1: no split,
     configs[0]). `fmt_name` defaults to the config's format."""
     from kvq_decode_amd import _sm_count
-    from kvq_decode_amd.ops import plan_decode, plan_units
+    from kvq_decode_amd.ops import head_blocks, plan_decode, plan_units
     if config == "C1":
         return 1, 0, 0
     cus = cu_count or _sm_count(0)
     fmt_name = fmt_name or CONFIGS[config][3]
-    units, waves = plan_units(B, hkv, BS, max_pages, cus, fmt_name, head_dim)
+    grid_heads = hkv * head_blocks(hq, hkv)
+    units, waves = plan_units(B, grid_heads, BS, max_pages, cus, fmt_name, head_dim, hq)
     if units:
         return 0, waves, units
-    return (*plan_decode(B, hkv, BS, max_pages, cus, fmt_name, head_dim), 0)
+    return (*plan_decode(B, grid_heads, BS, max_pages, cus, fmt_name, head_dim, hq), 0)
 
 
 def run_config(config, steps, warmup, splits=None, waves=0, pipeline=0, flushed=True,
@@ -676,7 +683,7 @@ def build_layers(B, ctx, pool, fmt_name, layers, shape=(HQ, HKV, D), config=None
                                            shape=shape)
         lens = lens or [int(x) for x in sl.tolist()]
         splits, waves, units = default_plan(config, B, bt.shape[1], hkv=shape[1],
-                                            fmt_name=fmt_name, head_dim=shape[2])
+                                            fmt_name=fmt_name, head_dim=shape[2], hq=shape[0])
         step_list.append(Step(q, k, v, bt, sl, splits, waves, 0, fmt, units))
         del q, k, v, bt, sl, fmt
     return step_list, lens

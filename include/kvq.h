@@ -66,7 +66,16 @@ typedef enum kvq_status {
  *                    block_table[b][j * VG / block_size], token t at index t % VG (with
  *                    16-token pages, a page pair's 32 pairs of one kv head fill one
  *                    128-byte line; other blocks' entries are unused)
- * The quantized formats decode at head_dim D = 64, 128 or 256 (fp16: 32-256).
+ * Sharing: the pairs of a K or V group are written into the group's lead block (the
+ * block of its first token), also for the tokens of the group's other blocks, so a lead
+ * block must belong to one sequence. Two sequences that share a block that leads a
+ * group but not the group's other blocks (prefix caching, beam forks; with 16-token
+ * pages page 2j leads the V group of pages 2j and 2j + 1) overwrite each other's pairs:
+ * copy such a block on write, or share whole groups only.
+ * The quantized formats decode at head_dim D = 64, 128 or 256 (fp16: 32-256), and the
+ * quantizers (kvq_quantize_cache, kvq_quantize_append) write exactly those head dims:
+ * any other returns KVQ_ERR_UNSUPPORTED from both, so no cache is written that no decode
+ * can read.
  * Scale and zero are stored interleaved: one fp16 [nb, Hkv, D, 2] (K) and one
  * [nb, Hkv, VG, 2] (V) tensor of (scale, zero) pairs, so that a decode loads both of a
  * token (V) or a channel (K) with one access. k_scale / v_scale point at element 0 of that
@@ -139,8 +148,8 @@ int kvq_choose_num_splits(int32_t batch, int32_t kv_heads, int32_t block_size,
  * kv head in one MFMA column block, so a group G > 16 is cut into k blocks of G / k heads,
  * k the smallest divisor of G with G / k <= 16, and each block runs as a kv head of its own
  * that reads the same cache head: the caches are read k times, and the kernels' grids
- * count kv_heads * k kv heads. Pass kv_heads * k as `kv_heads` to kvq_plan_decode and
- * kvq_plan_units. Returns k (1 for G <= 16), or KVQ_ERR_SHAPE when q_heads is not a
+ * count kv_heads * k kv heads. Pass kv_heads * k as `kv_heads` (and q_heads unchanged) to
+ * kvq_plan_decode and kvq_plan_units. Returns k (1 for G <= 16), or KVQ_ERR_SHAPE when q_heads is not a
  * positive multiple of kv_heads. The decode entry points return KVQ_ERR_UNSUPPORTED when
  * kv_heads * k exceeds 65535. */
 int kvq_head_blocks(int32_t q_heads, int32_t kv_heads);
@@ -164,11 +173,16 @@ int kvq_head_blocks(int32_t q_heads, int32_t kv_heads);
  * partitions (all measured on MI355X for batch 1..64 and 32k..128k contexts). fp16 head
  * dims below 128 move fewer bytes per chunk through about the same per-chunk work and
  * need s times the waves (the quantized split plans measured slower with them).
+ * A workgroup's LDS (its waves' cross-wave combine, proportional to waves * q heads per
+ * kv head * head_dim, or their staging tiles) must fit 64 KB: where it would not (large
+ * q-head groups at head dim 256), waves is halved and splits doubled until it does.
+ * kv_heads counts the kernels' kv heads (kv_heads * kvq_head_blocks(q_heads, kv_heads))
+ * and q_heads all q heads: q_heads / kv_heads is 1..16 (KVQ_ERR_SHAPE otherwise).
  * head_dim is a power of two >= 16 (KVQ_ERR_SHAPE otherwise). Writes
  * both outputs (splits before kvq_normalize_splits); returns KVQ_OK or an error. */
-int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t max_pages,
-                    int32_t kv_format, int32_t head_dim, int32_t cu_count, int32_t* splits_out,
-                    int32_t* waves_out);
+int kvq_plan_decode(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t block_size,
+                    int32_t max_pages, int32_t kv_format, int32_t head_dim, int32_t cu_count,
+                    int32_t* splits_out, int32_t* waves_out);
 
 /* Work-unit plan, the library's default for batches of 2 to 1024 sequences (no reference
  * counterpart; it takes the place of the split heuristic, triton_fp16.py:175-180). For
@@ -180,12 +194,14 @@ int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t
  *           T = 4 s, waves = 4; INT4 T = 8 s, waves = min(2 s, 4)
  *           (s = max(1, 128 / head_dim)),
  * for kvq_decode_units; otherwise units = waves = 0 (use kvq_plan_decode's split plan).
+ * As in kvq_plan_decode, waves is halved (and units doubled) until a workgroup's LDS fits
+ * 64 KB, and q_heads / kv_heads must be 1..16.
  * Units balance ragged batches (a static split count sizes every sequence's splits by
  * the longest one); on uniform batches the two plans run within a few percent of each
  * other on MI355X. Returns KVQ_OK or an error. */
-int kvq_plan_units(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t max_pages,
-                   int32_t kv_format, int32_t head_dim, int32_t cu_count, int32_t* units_out,
-                   int32_t* waves_out);
+int kvq_plan_units(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t block_size,
+                   int32_t max_pages, int32_t kv_format, int32_t head_dim, int32_t cu_count,
+                   int32_t* units_out, int32_t* waves_out);
 
 /* Split normalization, triton_fp16.py:211-217: clamps num_splits to [1, max_pages], then
  * pages_per_split = cdiv(max_pages, S) and S = cdiv(max_pages, pages_per_split).

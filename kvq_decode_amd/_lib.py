@@ -108,9 +108,9 @@ def lib():
         L.kvq_choose_num_splits.restype = ctypes.c_int
         L.kvq_choose_num_splits.argtypes = [_i32] * 7
         L.kvq_plan_decode.restype = ctypes.c_int
-        L.kvq_plan_decode.argtypes = [_i32] * 7 + [ctypes.POINTER(_i32)] * 2
+        L.kvq_plan_decode.argtypes = [_i32] * 8 + [ctypes.POINTER(_i32)] * 2
         L.kvq_plan_units.restype = ctypes.c_int
-        L.kvq_plan_units.argtypes = [_i32] * 7 + [ctypes.POINTER(_i32)] * 2
+        L.kvq_plan_units.argtypes = [_i32] * 8 + [ctypes.POINTER(_i32)] * 2
         L.kvq_normalize_splits.restype = ctypes.c_int
         L.kvq_normalize_splits.argtypes = [_i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)]
         args_p = ctypes.POINTER(DecodeArgs)

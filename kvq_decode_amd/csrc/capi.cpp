@@ -166,19 +166,25 @@ kvq::DecodeParams make_params(const kvq_decode_args* a) {
     return p;
 }
 
-int64_t lds_bytes(const kvq_decode_args* a, int waves) {
-    const int group = int(a->q_heads / grid_heads(a));  // q heads per kernel kv head
-    const int64_t combine = int64_t(4) * (int64_t(waves) * group * a->head_dim + 32 * waves);
-    // fp16: the waves' K staging tiles (16 rows of head_dim halves each), which the
-    // combine reuses; quantized: region 0 (combine or staging tiles), a K-scale slot of
-    // 4 head_dim bytes per wave and 32 head_dim bytes of q in k-operand order
-    if (a->kv_format == KVQ_KV_F16) {
-        const int64_t stage = int64_t(waves) * 32 * a->head_dim;
+// Dynamic LDS of a decode workgroup of `waves` waves serving `group` q heads per kernel kv
+// head: the cross-wave combine ([waves][group][head_dim] + [waves][16] m and l floats);
+// fp16: or the waves' K staging tiles (16 rows of head_dim halves each), which the combine
+// reuses; quantized: region 0 (combine or staging tiles), a K-scale slot of 4 head_dim
+// bytes per wave and 32 head_dim bytes of q in k-operand order.
+int64_t lds_need(int group, int head_dim, int kv_format, int waves) {
+    const int64_t combine = int64_t(4) * (int64_t(waves) * group * head_dim + 32 * waves);
+    if (kv_format == KVQ_KV_F16) {
+        const int64_t stage = int64_t(waves) * 32 * head_dim;
         return combine > stage ? combine : stage;
     }
-    return int64_t(4) * (kvq::quant_lds_region0(waves, group, a->kv_format, a->head_dim) +
-                         int64_t(a->head_dim) * waves) +
-           32 * int64_t(a->head_dim);
+    return int64_t(4) * (kvq::quant_lds_region0(waves, group, kv_format, head_dim) +
+                         int64_t(head_dim) * waves) +
+           32 * int64_t(head_dim);
+}
+
+int64_t lds_bytes(const kvq_decode_args* a, int waves) {
+    const int group = int(a->q_heads / grid_heads(a));  // q heads per kernel kv head
+    return lds_need(group, a->head_dim, a->kv_format, waves);
 }
 
 // Waves per workgroup: the caller's choice if given, else as many as give each wave at
@@ -227,7 +233,9 @@ int check_quant_args(const kvq_decode_args* a) {
         return KVQ_ERR_SHAPE;
     if (!is_pow2(a->block_size) || a->block_size < 16) return KVQ_ERR_SHAPE;
     if (!is_pow2(a->head_dim) || a->head_dim < 16) return KVQ_ERR_SHAPE;
-    if (a->head_dim < 32 || a->head_dim > 256) return KVQ_ERR_UNSUPPORTED;
+    // the head dims the quantized decode reads (check_decode_args): a cache the decode
+    // could not read is not written
+    if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256) return KVQ_ERR_UNSUPPORTED;
     if (a->k_group < a->block_size || a->k_group % a->block_size != 0) return KVQ_ERR_UNSUPPORTED;
     if (a->batch > 65535 || a->kv_heads > 65535) return KVQ_ERR_UNSUPPORTED;
     // 1-D grids over (kv head, K group) and (kv head, 64-row tile); tokens are int32
@@ -401,11 +409,14 @@ int kvq_choose_num_splits(int32_t batch, int32_t kv_heads, int32_t block_size,
     return int(s < 1 ? 1 : s);
 }
 
-int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t max_pages,
-                    int32_t kv_format, int32_t head_dim, int32_t cu_count, int32_t* splits_out,
-                    int32_t* waves_out) {
+int kvq_plan_decode(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t block_size,
+                    int32_t max_pages, int32_t kv_format, int32_t head_dim, int32_t cu_count,
+                    int32_t* splits_out, int32_t* waves_out) {
     if (!splits_out || !waves_out) return KVQ_ERR_NULL_POINTER;
     if (batch < 1 || kv_heads < 1 || max_pages < 1 || cu_count < 1) return KVQ_ERR_SHAPE;
+    // kv_heads counts the kernels' kv heads, each serving at most kMaxGroup q heads
+    if (q_heads < kv_heads || q_heads % kv_heads || q_heads / kv_heads > kMaxGroup)
+        return KVQ_ERR_SHAPE;
     if (!is_pow2(block_size) || block_size < 16) return KVQ_ERR_SHAPE;
     if (!is_pow2(head_dim) || head_dim < 16) return KVQ_ERR_SHAPE;
     if (kv_format < KVQ_KV_F16 || kv_format > KVQ_KV_INT4) return KVQ_ERR_FORMAT;
@@ -436,18 +447,22 @@ int kvq_plan_decode(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t
         waves = per_pair / 8;
         waves = waves < 1 ? 1 : (waves > wmax ? wmax : waves);
     }
+    // fewer, smaller workgroups (more splits, the same waves per pair) where a workgroup's
+    // LDS would pass the budget (large q-head groups at head dim 256)
+    while (waves > 1 && lds_need(q_heads / kv_heads, head_dim, kv_format, int(waves)) > kLdsBudget)
+        waves >>= 1;
     *waves_out = int32_t(waves);
     *splits_out = int32_t(per_pair / waves);
     return KVQ_OK;
 }
 
-int kvq_plan_units(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t max_pages,
-                   int32_t kv_format, int32_t head_dim, int32_t cu_count, int32_t* units_out,
-                   int32_t* waves_out) {
+int kvq_plan_units(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t block_size,
+                   int32_t max_pages, int32_t kv_format, int32_t head_dim, int32_t cu_count,
+                   int32_t* units_out, int32_t* waves_out) {
     if (!units_out || !waves_out) return KVQ_ERR_NULL_POINTER;
     int32_t splits = 0, split_waves = 0;
-    const int st = kvq_plan_decode(batch, kv_heads, block_size, max_pages, kv_format, head_dim,
-                                   cu_count, &splits, &split_waves);
+    const int st = kvq_plan_decode(batch, q_heads, kv_heads, block_size, max_pages, kv_format,
+                                   head_dim, cu_count, &splits, &split_waves);
     if (st != KVQ_OK) return st;
     *units_out = 0;
     *waves_out = 0;
@@ -468,6 +483,9 @@ int kvq_plan_units(int32_t batch, int32_t kv_heads, int32_t block_size, int32_t 
     const int64_t waves_per_cu = (kv_format == KVQ_KV_F16 ? 2 : int4 ? 8 : 4) * scale;
     int64_t waves = kv_format == KVQ_KV_F16 || int4 ? 2 * scale : 4;
     if (waves > 4) waves = 4;
+    // smaller unit workgroups, more units, where the LDS would pass the budget
+    while (waves > 1 && lds_need(q_heads / kv_heads, head_dim, kv_format, int(waves)) > kLdsBudget)
+        waves >>= 1;
     const int64_t units = waves_per_cu * cu_count / (waves * int64_t(kv_heads));
     *units_out = int32_t(units < 1 ? 1 : units);
     *waves_out = int32_t(waves);

@@ -76,7 +76,8 @@ def head_blocks(q_heads: int, kv_heads: int) -> int:
 
 
 def plan_decode(batch: int, kv_heads: int, block_size: int, max_pages: int,
-                cu_count: int, kv_format: str = "fp16", head_dim: int = 128) -> Tuple[int, int]:
+                cu_count: int, kv_format: str = "fp16", head_dim: int = 128,
+                q_heads: Optional[int] = None) -> Tuple[int, int]:
     """(num_splits, waves_per_group) for the MI355X kernels when num_splits is None: the
     split-KV decomposition the reference's heuristic aims at (triton_fp16.py:175-180:
     enough programs to fill the GPU, no tiny splits), counted in waves because one
@@ -86,20 +87,23 @@ def plan_decode(batch: int, kv_heads: int, block_size: int, max_pages: int,
     (quantized) 16-token chunks per wave; up to 2 waves per workgroup for fp16, and for
     quantized caches one wave per 8 waves of the (sequence, kv head) pair, up to 4 (INT4:
     8). fp16 head dims below 128 get 128 / head_dim times the waves, in workgroups of up
-    to 4 waves."""
+    to 4 waves. Waves are halved (splits doubled) until a workgroup's LDS, which grows with
+    the q heads per kv head, fits 64 KB. `kv_heads` counts the kernels' kv heads (see
+    `head_blocks`); `q_heads` (default: kv_heads, one q head per kv head) all q heads."""
     _require(kv_format in KV_FORMATS, f"kv_format must be one of {tuple(KV_FORMATS)}")
     s, w = ctypes.c_int32(), ctypes.c_int32()
     _lib.check("kvq_plan_decode",
-               _lib.lib().kvq_plan_decode(batch, kv_heads, block_size, max_pages,
-                                          KV_FORMATS[kv_format], head_dim, cu_count,
+               _lib.lib().kvq_plan_decode(batch, q_heads or kv_heads, kv_heads, block_size,
+                                          max_pages, KV_FORMATS[kv_format], head_dim, cu_count,
                                           ctypes.byref(s), ctypes.byref(w)))
     return s.value, w.value
 
 
 def auto_splits(batch: int, kv_heads: int, block_size: int, max_pages: int,
-                cu_count: int, kv_format: str = "fp16", head_dim: int = 128) -> int:
+                cu_count: int, kv_format: str = "fp16", head_dim: int = 128,
+                q_heads: Optional[int] = None) -> int:
     return plan_decode(batch, kv_heads, block_size, max_pages, cu_count, kv_format,
-                       head_dim)[0]
+                       head_dim, q_heads)[0]
 
 
 @functools.lru_cache(maxsize=4096)
@@ -115,19 +119,22 @@ def normalize_splits(num_splits: int, max_pages: int) -> Tuple[int, int]:
 
 @functools.lru_cache(maxsize=4096)
 def plan_units(batch: int, kv_heads: int, block_size: int, max_pages: int,
-               cu_count: int, kv_format: str = "fp16", head_dim: int = 128) -> Tuple[int, int]:
+               cu_count: int, kv_format: str = "fp16", head_dim: int = 128,
+               q_heads: Optional[int] = None) -> Tuple[int, int]:
     """(units, waves_per_group) of the work-unit partition when the library prefers it
     for num_splits=None, else (0, 0) (kvq_plan_units): batches of 2 to 1024 sequences
     whose split plan (`plan_decode`) has 2 or more splits, or whose longest context is at
     least 4096 tokens, get 2 waves per CU in 2-wave
     unit workgroups (fp16), 4 in 4-wave workgroups (INT8, FP8) or 8 in 2-wave workgroups
     (INT4), which keeps ragged batches balanced. Head dims below 128 get 128 / head_dim
-    times the waves per CU, and fp16 / INT4 unit workgroups of up to 4 waves."""
+    times the waves per CU, and fp16 / INT4 unit workgroups of up to 4 waves. As in
+    `plan_decode`, waves are halved (units doubled) until a workgroup's LDS fits 64 KB, and
+    `q_heads` defaults to kv_heads."""
     _require(kv_format in KV_FORMATS, f"kv_format must be one of {tuple(KV_FORMATS)}")
     u, w = ctypes.c_int32(), ctypes.c_int32()
     _lib.check("kvq_plan_units",
-               _lib.lib().kvq_plan_units(batch, kv_heads, block_size, max_pages,
-                                         KV_FORMATS[kv_format], head_dim, cu_count,
+               _lib.lib().kvq_plan_units(batch, q_heads or kv_heads, kv_heads, block_size,
+                                         max_pages, KV_FORMATS[kv_format], head_dim, cu_count,
                                          ctypes.byref(u), ctypes.byref(w)))
     return u.value, w.value
 
@@ -151,11 +158,11 @@ def plan_workspace_shapes(batch: int, q_heads: int, kv_heads: int, head_dim: int
     a graph capture."""
     grid_heads = kv_heads * head_blocks(q_heads, kv_heads)
     units, _ = plan_units(batch, grid_heads, block_size, max_pages, cu_count, kv_format,
-                          head_dim)
+                          head_dim, q_heads)
     if units:
         return units_workspace_shapes(batch, q_heads, head_dim, units)
     splits, _ = plan_decode(batch, grid_heads, block_size, max_pages, cu_count, kv_format,
-                            head_dim)
+                            head_dim, q_heads)
     splits = normalize_splits(splits, max_pages)[0]
     return None if splits == 1 else workspace_shapes(batch, q_heads, head_dim, splits)
 
@@ -308,7 +315,7 @@ def paged_decode_attention(
     grid_heads = Hkv * head_blocks(Hq, Hkv)  # the plans count the kernels' kv heads
     if num_splits is None and units == 0:
         units, planned_waves = plan_units(B, grid_heads, block_size, max_pages,
-                                          _sm_count(dev.index or 0), kv_format, D)
+                                          _sm_count(dev.index or 0), kv_format, D, Hq)
         if units > 0 and waves_per_group == 0:
             waves_per_group = planned_waves
     if units > 0:
@@ -331,7 +338,7 @@ def paged_decode_attention(
         return out
     if num_splits is None:
         splits, planned_waves = plan_decode(B, grid_heads, block_size, max_pages,
-                                            _sm_count(dev.index or 0), kv_format, D)
+                                            _sm_count(dev.index or 0), kv_format, D, Hq)
         if waves_per_group == 0:
             waves_per_group = planned_waves
     else:

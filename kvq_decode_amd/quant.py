@@ -29,6 +29,8 @@ from kvq_decode_amd.ops import (DEFAULT_K_GROUP, KvqArgumentError, _require, che
                                 v_group_tokens)
 
 QUANT_FORMATS = ("int8", "fp8_e4m3", "int4")
+# head dims of the quantized decode kernels, and so of the quantizers (include/kvq.h)
+QUANT_HEAD_DIMS = (64, 128, 256)
 
 
 # The on-device format these caches follow (include/kvq.h KVQ_CACHE_FORMAT_VERSION); a
@@ -83,6 +85,8 @@ def allocate_quantized_cache(num_blocks: int, block_size: int, kv_heads: int, he
     an HBM cache line - token-major storage would fetch every line twice, once for each
     of the two heads sharing it, from workgroups on different XCDs."""
     _require(kv_format in QUANT_FORMATS, f"kv_format must be one of {QUANT_FORMATS}")
+    _require(head_dim in QUANT_HEAD_DIMS,
+             f"quantized caches take head_dim {QUANT_HEAD_DIMS} (the decode's), not {head_dim}")
     dc = head_dim // 2 if kv_format == "int4" else head_dim
     shape = (num_blocks, kv_heads, block_size, dc)
     kc = torch.empty(shape, dtype=torch.uint8, device=device).permute(0, 2, 1, 3)
@@ -118,6 +122,8 @@ def _check_cache(cache: QuantizedKVCache, block_table, seq_lens, head_dim):
     """Every check the quantizer entry points share; all of them run on tensor metadata
     before any launch, so a mismatch raises instead of reading or writing out of bounds."""
     _require(cache.kv_format in QUANT_FORMATS, f"kv_format must be one of {QUANT_FORMATS}")
+    _require(head_dim in QUANT_HEAD_DIMS,
+             f"quantized caches take head_dim {QUANT_HEAD_DIMS} (the decode's), not {head_dim}")
     _require(block_table.dtype == seq_lens.dtype == torch.int32,
              "block_table and seq_lens must be int32")
     _require(block_table.dim() == 2 and seq_lens.dim() == 1

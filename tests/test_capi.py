@@ -148,16 +148,16 @@ def test_plan_decode():
     assert plan_decode(1, 8, 32, 4096, 256, "fp16") == (32, 2)  # 2 chunks per page
     L = _lib.lib()
     s, w = ctypes.c_int32(), ctypes.c_int32()
-    assert L.kvq_plan_decode(0, 8, 16, 64, 0, 128, 256, ctypes.byref(s), ctypes.byref(w)) == \
+    assert L.kvq_plan_decode(0, 32, 8, 16, 64, 0, 128, 256, ctypes.byref(s), ctypes.byref(w)) == \
         _lib.KVQ_ERR_SHAPE
-    assert L.kvq_plan_decode(1, 8, 16, 64, 7, 128, 256, ctypes.byref(s), ctypes.byref(w)) == \
+    assert L.kvq_plan_decode(1, 32, 8, 16, 64, 7, 128, 256, ctypes.byref(s), ctypes.byref(w)) == \
         _lib.KVQ_ERR_FORMAT
-    assert L.kvq_plan_decode(1, 8, 24, 64, 0, 128, 256, ctypes.byref(s), ctypes.byref(w)) == \
+    assert L.kvq_plan_decode(1, 32, 8, 24, 64, 0, 128, 256, ctypes.byref(s), ctypes.byref(w)) == \
         _lib.KVQ_ERR_SHAPE
-    assert L.kvq_plan_decode(1, 8, 16, 64, 0, 128, 256, None, ctypes.byref(w)) == \
+    assert L.kvq_plan_decode(1, 32, 8, 16, 64, 0, 128, 256, None, ctypes.byref(w)) == \
         _lib.KVQ_ERR_NULL_POINTER
     for hd in (0, 24, -64):  # head_dim: a power of two >= 16
-        assert L.kvq_plan_decode(1, 8, 16, 64, 0, hd, 256, ctypes.byref(s),
+        assert L.kvq_plan_decode(1, 32, 8, 16, 64, 0, hd, 256, ctypes.byref(s),
                                  ctypes.byref(w)) == _lib.KVQ_ERR_SHAPE, hd
 
 
@@ -215,12 +215,40 @@ def test_plan_units():
     assert plan_units(8, 1, 16, 2048, 256, "fp16") == (256, 2)  # MQA
     L = _lib.lib()
     u, w = ctypes.c_int32(), ctypes.c_int32()
-    assert L.kvq_plan_units(0, 8, 16, 64, 0, 128, 256, ctypes.byref(u), ctypes.byref(w)) == \
+    assert L.kvq_plan_units(0, 32, 8, 16, 64, 0, 128, 256, ctypes.byref(u), ctypes.byref(w)) == \
         _lib.KVQ_ERR_SHAPE
-    assert L.kvq_plan_units(2, 8, 16, 64, 7, 128, 256, ctypes.byref(u), ctypes.byref(w)) == \
+    assert L.kvq_plan_units(2, 32, 8, 16, 64, 7, 128, 256, ctypes.byref(u), ctypes.byref(w)) == \
         _lib.KVQ_ERR_FORMAT
-    assert L.kvq_plan_units(2, 8, 16, 64, 0, 128, 256, None, ctypes.byref(w)) == \
+    assert L.kvq_plan_units(2, 32, 8, 16, 64, 0, 128, 256, None, ctypes.byref(w)) == \
         _lib.KVQ_ERR_NULL_POINTER
+
+
+def test_plan_lds_budget():
+    """The plans keep a workgroup's LDS within 64 KB: where the waves they would pick give
+    a cross-wave combine larger than that (large q-head groups at head dim 256 or 16 q
+    heads per kv head), they halve the waves and double the splits or units, so the waves
+    per CU stay. LDS bytes (quantized) = 4 * (max(W*G*D + 32*W, W*D*(4 INT4 | 9 INT8)) +
+    D*W) + 32*D."""
+    from kvq_decode_amd.ops import plan_decode, plan_units
+    # INT4, head_dim 256, 32 q / 4 kv heads, batch 1 x 32k: 512 waves per pair; 8-wave
+    # workgroups would need 82944 B, 4-wave ones 45568 B
+    assert plan_decode(1, 4, 16, 2048, 256, "int4", 256, q_heads=32) == (128, 4)
+    assert plan_decode(1, 4, 16, 2048, 256, "int4", 256) == (64, 8)  # 1 q head per kv head
+    # INT8, head_dim 256, 32 q / 2 kv heads: 4-wave workgroups need 78336 B, 2-wave 43264 B
+    assert plan_units(16, 2, 16, 2048, 256, "int8", 256, q_heads=32) == (256, 2)
+    assert plan_decode(1, 2, 16, 2048, 256, "int8", 256, q_heads=32) == (256, 2)
+    # INT4, head_dim 128, 16 q heads per kv head, batch 1: 8 waves need 74752 B, 4 39424 B
+    assert plan_decode(1, 8, 16, 2048, 256, "int4", 128, q_heads=128) == (64, 4)
+    # the common shapes are unchanged (4 q heads per kv head)
+    assert plan_decode(1, 8, 16, 4096, 256, "int4", 128, q_heads=32) == (32, 8)
+    assert plan_units(8, 8, 16, 2048, 256, "fp16", 128, q_heads=32) == (32, 2)
+    L = _lib.lib()
+    s, w = ctypes.c_int32(), ctypes.c_int32()
+    for hq, hkv in ((7, 8), (12, 8), (136, 8)):  # q_heads / kv_heads must be 1..16
+        assert L.kvq_plan_decode(1, hq, hkv, 16, 64, 0, 128, 256, ctypes.byref(s),
+                                 ctypes.byref(w)) == _lib.KVQ_ERR_SHAPE, (hq, hkv)
+        assert L.kvq_plan_units(2, hq, hkv, 16, 64, 0, 128, 256, ctypes.byref(s),
+                                ctypes.byref(w)) == _lib.KVQ_ERR_SHAPE, (hq, hkv)
 
 
 def test_plan_workspace_shapes():
@@ -437,6 +465,39 @@ def test_merge_and_quantize_reject():
     a.k_group = 128
     assert L.kvq_quantize_append(ctypes.byref(a), 0, 1 << 40, 1 << 41, None) == \
         _lib.KVQ_ERR_NULL_POINTER
+
+
+def test_quantizers_take_the_decode_head_dims():
+    """The quantizers write exactly the head dims the quantized decode reads (64, 128,
+    256): head_dim 32 (and 512) is KVQ_ERR_UNSUPPORTED for both the bulk quantizer and the
+    append, as for the decode, so no cache can be built that no decode reads. Accepted
+    head dims reach the next check (a null source pointer)."""
+    L = _lib.lib()
+    op, lse = 1 << 41, 1 << 42
+    for fmt in (1, 2, 3):
+        for D in (32, 512):
+            a = good_args()
+            a.kv_format = fmt
+            set_scale_pairs(a)
+            a.head_dim, a.q_stride_b, a.q_stride_h = D, 32 * D, D
+            a.o_stride_b, a.o_stride_h = 32 * D, D
+            assert L.kvq_quantize_cache(ctypes.byref(a), 1 << 40, 1 << 40, 0, 0, 0, None) == \
+                _lib.KVQ_ERR_UNSUPPORTED, (fmt, D)
+            assert L.kvq_quantize_append(ctypes.byref(a), 1 << 40, 1 << 40, 1 << 41, None) == \
+                _lib.KVQ_ERR_UNSUPPORTED, (fmt, D)
+            assert L.kvq_decode_split(ctypes.byref(a), 4, 16, op, lse, None) == \
+                _lib.KVQ_ERR_UNSUPPORTED, (fmt, D)
+        for D in (64, 128, 256):
+            a = good_args()
+            a.kv_format = fmt
+            set_scale_pairs(a)
+            a.head_dim = D
+            assert L.kvq_quantize_cache(ctypes.byref(a), 0, 1 << 40, 0, 0, 0, None) == \
+                _lib.KVQ_ERR_NULL_POINTER, (fmt, D)
+    from kvq_decode_amd.quant import allocate_quantized_cache
+    from kvq_decode_amd.ops import KvqArgumentError
+    with pytest.raises(KvqArgumentError):
+        allocate_quantized_cache(4, 16, 2, 32, "int8", "cpu")
 
 
 def test_python_op_argument_errors_and_no_cpu_fallback():

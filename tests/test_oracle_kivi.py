@@ -135,3 +135,28 @@ def test_paged_quantization_round_trip(fmt, bs):
             lead = bt[b, (t // vg) * vg // bs]
             assert np.array_equal(qc["v_scale"][lead, :, t % vg].view(np.uint16), vs[t].view(np.uint16))
             assert np.array_equal(qc["v_zero"][lead, :, t % vg].view(np.uint16), vz[t].view(np.uint16))
+
+
+def test_shared_lead_block_collides():
+    """The hazard include/kvq.h states for quantized caches: a V group's (scale, zero)
+    pairs (32 tokens with 16-token pages) and a K group's are stored in the group's lead
+    block, also for the tokens of its other blocks. Two sequences that share page 0 but
+    not page 1 (a prefix fork) therefore overwrite each other's pairs, and the first one
+    no longer dequantizes to what it was quantized from; copying the shared page (so each
+    sequence owns its lead block) removes the collision."""
+    rng = np.random.default_rng(5)
+    bs, hkv, d = 16, 2, 64
+    k = rng.standard_normal((4, bs, hkv, d)).astype(np.float16)
+    v = rng.standard_normal((4, bs, hkv, d)).astype(np.float16)
+    k[3], v[3] = k[0], v[0]  # page 3: a copy of the shared page 0
+    lens = np.array([32, 32], np.int32)
+    alone = kivi.quantize_paged_cache(k, v, np.array([[0, 1]], np.int32), lens[:1], "int8")
+    want_k, want_v = kivi.dequantize_paged_cache(alone, np.array([[0, 1]], np.int32),
+                                                 lens[:1], "int8")
+    for table, collide in (([[0, 1], [0, 2]], True), ([[0, 1], [3, 2]], False)):
+        bt = np.array(table, np.int32)
+        qc = kivi.quantize_paged_cache(k, v, bt, lens, "int8")
+        got_k, got_v = kivi.dequantize_paged_cache(qc, bt, lens, "int8")
+        same = (np.array_equal(got_k[[0, 1]], want_k[[0, 1]]) and
+                np.array_equal(got_v[[0, 1]], want_v[[0, 1]]))
+        assert same != collide, table

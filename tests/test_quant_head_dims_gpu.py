@@ -134,3 +134,28 @@ def test_nan_garbage_other_head_dims(D, fmt):
     for extra in ({"num_splits": 1}, {"num_splits": 3}, {"units": 4}):
         out = paged_decode_attention(*args, **extra, **qc.decode_kwargs())
         tq.check_close(out, ref, f"{fmt} D={D} poisoned {extra}")
+
+
+@pytest.mark.parametrize("fmt, D, Hq, Hkv, lens", [
+    ("int4", 256, 32, 4, [4096]),        # split plan: 8-wave workgroups would need 82944 B
+    ("int8", 256, 32, 2, [4096]),        # split plan: 4 waves, 78336 B
+    ("int8", 256, 32, 2, [4096, 3000]),  # work units: 4 waves, 78336 B
+    ("fp8_e4m3", 256, 32, 2, [4096, 3000]),
+    ("int4", 128, 128, 8, [4096]),       # 16 q heads per kv head: 8 waves, 74752 B
+])
+def test_default_plan_fits_lds(fmt, D, Hq, Hkv, lens):
+    """The default plan (num_splits=None) at shapes whose first-choice workgroups would
+    pass the 64 KB LDS budget: the plans halve the waves (more splits or units) instead of
+    handing the decode a workgroup it must reject, and the result matches the oracle."""
+    from kvq_decode_amd import paged_decode_attention
+    from kvq_decode_amd.ops import head_blocks, plan_decode, plan_units
+    args, kw, ref = case(fmt, D, lens, Hq=Hq, Hkv=Hkv, seed=11)
+    grid_heads = Hkv * head_blocks(Hq, Hkv)
+    pages = args[3].shape[1]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    units, uw = plan_units(len(lens), grid_heads, 16, pages, cus, fmt, D, Hq)
+    splits, sw = plan_decode(len(lens), grid_heads, 16, pages, cus, fmt, D, Hq)
+    print(f"{fmt} D={D} {Hq}q/{Hkv}kv lens={lens}: units {units}x{uw}, splits {splits}x{sw}",
+          flush=True)
+    out = paged_decode_attention(*args, **kw)
+    tq.check_close(out, ref, f"{fmt} D={D} Hq={Hq} Hkv={Hkv} default plan")
