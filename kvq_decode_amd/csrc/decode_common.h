@@ -270,16 +270,12 @@ struct __attribute__((aligned(16))) UnitLds {
 };
 
 // The chunk prefix of the batch, lane t of one wave taking sequences per * t .. + per - 1
-// (per <= PER): pref[b] = P_b, pref[B] = N, len[b] = the clamped length. Every load is
-// issued before the first is used (unrolled, predicated on e < per).
+// (per <= PER) whose seq_lens are raw[0 .. per - 1]: pref[b] = P_b, pref[B] = N, len[b] =
+// the clamped length.
 template <int PER>
-__device__ __forceinline__ void unit_prefix(const DecodeParams& p, int* pref, int* len_out,
-                                            int t, int per) {
+__device__ __forceinline__ void unit_prefix_scan(const DecodeParams& p, const int* raw,
+                                                 int* pref, int* len_out, int t, int per) {
     const int B = p.batch, cap = p.max_blocks * p.block_size;
-    // all PER loads first, at clamped indices (no branch between a load and the next)
-    int raw[PER];
-#pragma unroll
-    for (int e = 0; e < PER; ++e) raw[e] = p.seq_lens[min(per * t + e, B - 1)];
     int n[PER], local = 0;
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
@@ -304,6 +300,17 @@ __device__ __forceinline__ void unit_prefix(const DecodeParams& p, int* pref, in
         run += n[e];
     }
     if (t == 63) pref[B] = incl;
+}
+
+// The same, loading the seq_lens first: all PER loads before any use (clamped indices,
+// no branch between a load and the next).
+template <int PER>
+__device__ __forceinline__ void unit_prefix(const DecodeParams& p, int* pref, int* len_out,
+                                            int t, int per) {
+    int raw[PER];
+#pragma unroll
+    for (int e = 0; e < PER; ++e) raw[e] = p.seq_lens[min(per * t + e, p.batch - 1)];
+    unit_prefix_scan<PER>(p, raw, pref, len_out, t, per);
 }
 
 // The calling wave's share of its unit's first segment in the partition where every
@@ -342,12 +349,17 @@ __device__ __forceinline__ SegGuess unit_guess(const DecodeParams& p, int u, int
 // barrier between segments (they reuse the LDS of the range functions). [w_lo, w_hi) is
 // the calling wave's contiguous share of the segment's chunks.
 //
-// The segments come from the batch's chunk prefix, which wave 0 scans from seq_lens, and a
-// segment's first loads (q, block-table entries) depend on it: one more dependent memory
-// round trip before the first KV bytes than a split has. Every wave therefore first calls
-// pf = pre(kvh, guess) with its unit_guess share, which issues those loads for the
-// guessed segment without using them, so they travel with the seq_lens loads; fn gets pf
-// and first = true for the unit's first segment, and uses what matches the real one.
+// The segments come from the batch's chunk prefix, and a segment's first loads (q,
+// block-table entries) depend on it. Two things keep that off the critical path:
+// * every wave first calls pf = pre(kvh, guess) with its unit_guess share, which issues
+//   those loads for the segment of the partition where every sequence has the table's
+//   chunk count, without using them; fn gets pf and first = true for the unit's first
+//   segment, and uses what matches the real one;
+// * for batches of up to 256 sequences every wave loads its lanes' seq_lens together with
+//   them, and when every sequence has that chunk count (a ballot) the prefix is the closed
+//   form P_b = b * n: the wave computes its segments from registers, with no scan, LDS
+//   table, barrier or search before its first chunk. Otherwise wave 0 scans the lengths
+//   into an LDS prefix table that every wave then searches.
 //
 // Workgroup order: plain (kv head fastest), or with xcd_group and units a multiple of
 // kXcds, grouped so that the kv heads of one unit share an XCD (workgroup i runs on XCD
@@ -364,40 +376,77 @@ __device__ __forceinline__ void for_unit_segments(const DecodeParams& p, Pre&& p
         kvh = blockIdx.x % p.kv_heads;
         u = blockIdx.x / p.kv_heads;
     }
-    const int t = threadIdx.x, B = p.batch;
+    const int t = threadIdx.x, B = p.batch, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const auto pf = pre(kvh, unit_guess<W>(p, u, wave));
-    if (t < 64) {  // lane t: sequences per * t .. per * t + per - 1
-        const int per = (B + 63) >> 6;
-        if (per <= 4)  // batches up to 256: the short scan
-            unit_prefix<4>(p, s.pref, s.len, t, per);
-        else
-            unit_prefix<kUnitMaxBatch / 64>(p, s.pref, s.len, t, per);
+    const int per = (B + 63) >> 6;
+    const int cap = p.max_blocks * p.block_size, ng = cap >> 4;  // cap: a multiple of 16
+    int raw[4];
+    bool uniform = false;
+    if (per <= 4) {  // lane t: sequences per * t .. per * t + per - 1
+#pragma unroll
+        for (int e = 0; e < 4; ++e) raw[e] = p.seq_lens[min(per * lane + e, B - 1)];
+        bool ok = true;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (e < per && per * lane + e < B) ok = ok && cdiv(min(max(raw[e], 0), cap), 16) == ng;
+        uniform = __ballot(!ok) == 0;
     }
-    __syncthreads();
+    // The unit's chunk range [lo, hi) and its first sequence b: from the closed form, or
+    // from wave 0's LDS prefix table after a barrier (the branch is uniform over the
+    // workgroup: every wave's ballot saw the same lengths). One segment loop serves both,
+    // so the range function is inlined once.
     UnitSpace us;
-    us.N = __builtin_amdgcn_readfirstlane(s.pref[B]);
+    int b = 0;
+    if (uniform) {  // P_b = b * ng, N = B * ng (the host checks B * ng <= INT32_MAX)
+        us.N = B * ng;
+    } else {
+        if (t < 64) {
+            if (per <= 4)  // batches up to 256: the short scan, over the lengths loaded above
+                unit_prefix_scan<4>(p, raw, s.pref, s.len, t, per);
+            else
+                unit_prefix<kUnitMaxBatch / 64>(p, s.pref, s.len, t, per);
+        }
+        __syncthreads();
+        us.N = __builtin_amdgcn_readfirstlane(s.pref[B]);
+    }
     us.NU = min(p.units, us.N);
     if (u >= us.NU) return;
     const int lo = unit_lo(us, u), hi = unit_lo(us, u + 1);
-    // the sequence holding chunk lo: the largest b with P_b <= lo (P_B = N > lo)
-    int b = 0, top = B;
-    while (top - b > 1) {
-        const int mid = (b + top) >> 1;
-        if (__builtin_amdgcn_readfirstlane(s.pref[mid]) <= lo) b = mid;
-        else top = mid;
+    if (uniform) {
+        b = lo / ng;
+    } else {  // the sequence holding chunk lo: the largest b with P_b <= lo (P_B = N > lo)
+        int top = B;
+        while (top - b > 1) {
+            const int mid = (b + top) >> 1;
+            if (__builtin_amdgcn_readfirstlane(s.pref[mid]) <= lo) b = mid;
+            else top = mid;
+        }
     }
     bool first = true;
     for (; b < B; ++b) {
-        const int p0 = __builtin_amdgcn_readfirstlane(s.pref[b]);
+        int p0, p1, len;
+        if (uniform) {
+            p0 = b * ng;
+            p1 = p0 + ng;
+            // b's length: element b % per of lane b / per
+            const int L = b / per, e = b - L * per;
+            int v = raw[0];
+            v = e == 1 ? raw[1] : v;
+            v = e == 2 ? raw[2] : v;
+            v = e == 3 ? raw[3] : v;
+            len = min(max(__builtin_amdgcn_readlane(v, L), 0), cap);
+        } else {
+            p0 = __builtin_amdgcn_readfirstlane(s.pref[b]);
+            p1 = __builtin_amdgcn_readfirstlane(s.pref[b + 1]);
+            len = __builtin_amdgcn_readfirstlane(s.len[b]);
+        }
         if (p0 >= hi) break;
-        const int p1 = __builtin_amdgcn_readfirstlane(s.pref[b + 1]);
         const int c_lo = max(lo, p0) - p0, c_hi = min(hi, p1) - p0;
         if (c_lo >= c_hi) continue;  // an empty sequence
-        const int per = cdiv(c_hi - c_lo, W);
-        const int w_lo = min(c_lo + wave * per, c_hi), w_hi = min(w_lo + per, c_hi);
-        fn(kvh, b, __builtin_amdgcn_readfirstlane(s.len[b]), w_lo, w_hi, (int64_t)u + b,
-           (int64_t)p.units + B, pf, first);
+        const int cnt = cdiv(c_hi - c_lo, W);
+        const int w_lo = min(c_lo + wave * cnt, c_hi), w_hi = min(w_lo + cnt, c_hi);
+        fn(kvh, b, len, w_lo, w_hi, (int64_t)u + b, (int64_t)p.units + B, pf, first);
         first = false;
         __syncthreads();
     }
