@@ -13,10 +13,13 @@ decode of the whole batch (stage 1 + stage 2), inputs resident in HBM. Algorithm
 bytes = KV reads only (reference src/bpt/roofline.py:1-4, bench/bench_triton_fp16.py:58):
 B * ctx * Hkv * 2 * D * 2 bytes for fp16.
 
-The default C2 line also carries the north star's other targets, timed the same way:
-fp16 batch 1 at 64k tokens (b1_64k_*: >= 50% of the peak) and INT4 against fp16 at batch
-16 / 32k tokens (b16_*, int4_speedup: >= 3x fewer µs per step); --no-targets skips them.
-roofline.kernel_us is stage 1 timed over back-to-back stage-1 launches.
+The default C2 line also carries, timed the same way (same steps and warmup, default
+plans), every other configuration of EXTRA_CONFIGS as <prefix>_* keys: the north star's
+targets (fp16 B1/64k >= 50% of the peak with the cache flushed, fp16 B8/16k >= 80%, INT4
+>= 3x fewer µs per step than fp16 at B16/32k; collected under `targets`), the reference's
+published grid points (B8/16k, B32/16k, B8/64k) and BASELINE.json's C3, C4 (INT8, FP8) and
+C5. --no-targets skips them. roofline.kernel_us is stage 1 timed over back-to-back
+stage-1 launches; `pre_timing` lists what runs before the warmup and timed steps.
 
 --layers N times a whole-model decode step instead: N layers, each with its own cache of
 the --config shape, decoded back to back - eagerly, and replayed from one captured HIP
@@ -213,7 +216,10 @@ def time_steps(step, steps, warmup):
     return wall_ms, ev0.elapsed_time(ev1) / steps
 
 
-def time_stage1(step, iters, blocks=5):
+STAGE1_BLOCKS = 5
+
+
+def time_stage1(step, iters, blocks=STAGE1_BLOCKS):
     """Average duration of the dominant kernel (stage 1): `blocks` runs of `iters` stage-1
     launches back to back, each run between one pair of HIP events recorded on the stream
     the launches go to, with nothing else between them; the median run. Inter-launch gaps
@@ -640,13 +646,15 @@ def run_config(config, steps, warmup, splits=None, waves=0, pipeline=0, flushed=
     step = Step(q, k, v, bt, sl, splits, waves, pipeline, fmt, units)
     nbytes = kv_bytes(lens, fmt_name)
     log(f"{config}: {desc}; {plan_text(step)} pages/split={step.pps} KV bytes/step={nbytes}")
-    # Kernel-level figures first, the headline steps last: MI355X raises its clock over the
-    # first tens of ms of sustained load after idle (measured: C2 steps 169 us in the first
-    # 20 ms of a process, 159 us after), so the timed steps run at the steady clock of a
-    # serving GPU rather than during the ramp. They are still exactly `warmup` untimed and
-    # `steps` timed steps.
-    stage1_ms = time_stage1(step, max(20, min(steps, 100)))
+    # The flushed steps first (each waits on the host, so the GPU idles between them),
+    # then the kernel-level figures, the headline steps last: MI355X raises its clock over
+    # the first tens of ms of sustained load after idle (measured: C2 steps 169 us in the
+    # first 20 ms of a process, 159 us after), so the timed steps follow the stage-1 runs'
+    # sustained load and run at the steady clock of a serving GPU rather than during the
+    # ramp. They are still exactly `warmup` untimed and `steps` timed steps.
     flushed_ms = time_flushed(step) if flushed else None
+    stage1_iters = max(20, min(steps, 100))
+    stage1_ms = time_stage1(step, stage1_iters)
     wall_ms, ev_ms = time_steps(step, steps, warmup)
     log(f"  wall {wall_ms * 1e3:.1f} us/step (events {ev_ms * 1e3:.1f}), stage 1 "
         f"{stage1_ms * 1e3:.1f} us" + (f", flushed median {flushed_ms * 1e3:.1f} us" if flushed else ""))
@@ -669,6 +677,10 @@ def run_config(config, steps, warmup, splits=None, waves=0, pipeline=0, flushed=
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
                      "traffic": read_traffic(config, plan_text(step)),
                      "kernel": f"{kernel} (stage 1)", "kernel_us": round(stage1_ms * 1e3, 2)},
+        # what runs before the `warmup` untimed and `steps` timed steps, in this order
+        "pre_timing": {"flushed_steps": FLUSH_SAMPLES if flushed else 0,
+                       "spin_up_ms": round(SPIN_UP_S * 1e3),
+                       "stage1_launches": STAGE1_BLOCKS * stage1_iters},
     }
     return res, (q, k, v, bt, sl)
 
@@ -827,31 +839,53 @@ def run_write_path(config, steps, warmup):
 
 
 def sweep(args):
+    """Split / waves / ring sweep of --config (and, with --sweep-units, work units), step
+    and stage-1 times; the table goes to stderr and to profiles/sweep_<config>.txt."""
     import torch
-    B, ctx, pool, fmt_name, _ = CONFIGS[args.config]
+    B, ctx, pool, fmt_name, desc = CONFIGS[args.config]
     q, k, v, bt, sl, fmt = make_inputs(B, ctx, pool, kv_format=fmt_name)
     nbytes = kv_bytes([int(x) for x in sl.tolist()], fmt_name)
-    log(f"{args.config}: B={B} ctx={ctx} {fmt_name} kv={nbytes / 1e9:.3f} GB")
-    log(f"{'splits':>6}{'waves':>6}{'pipe':>5}{'step_us':>10}{'stage1_us':>11}{'TB/s':>8}{'%peak':>7}")
+    splits0, waves0, units0 = default_plan(args.config, B, bt.shape[1])
+    lines = [f"# bench.py --sweep, {desc}",
+             f"# KV bytes per step {nbytes}; default plan: "
+             + (f"units {units0} x {waves0} waves" if units0 else f"splits {splits0} x {waves0}"),
+             "# command: python3 bench.py " + " ".join(sys.argv[1:]),
+             "# step_us: events around 20 back-to-back steps after 5 warmup; stage1_us: "
+             "median of 5 runs of 20 stage-1 launches",
+             f"{'plan':>6}{'n':>6}{'waves':>6}{'ring':>5}{'step_us':>10}{'stage1_us':>11}"
+             f"{'TB/s':>8}{'%peak':>7}"]
+    log("\n".join(lines))
     if args.sweep_pipes:
         pipes = tuple(int(x) for x in args.sweep_pipes.split(","))
     else:
         pipes = (1, 2) if fmt_name == "fp16" else (4,)
-    for splits in [int(s) for s in args.sweep_splits.split(",")]:
+    plans = [("splits", int(x)) for x in args.sweep_splits.split(",") if x]
+    plans += [("units", int(x)) for x in (args.sweep_units or "").split(",") if x]
+    for kind, n in plans:
         for waves in [int(w) for w in args.sweep_waves.split(",")]:
             for pipe in pipes:
                 try:
-                    st = Step(q, k, v, bt, sl, splits, waves, pipe, fmt)
+                    if kind == "units":
+                        st = Step(q, k, v, bt, sl, None, waves, pipe, fmt, n)
+                    else:
+                        st = Step(q, k, v, bt, sl, n, waves, pipe, fmt)
                     _, ev_ms = time_steps(st, 20, 5)
                     s1 = time_stage1(st, 20)
                 except Exception as e:  # invalid combination for this config
-                    log(f"{splits:>6}{waves:>6}{pipe:>5}  skipped: {e}")
+                    log(f"{kind:>6}{n:>6}{waves:>6}{pipe:>5}  skipped: {e}")
                     continue
                 tbs = nbytes / (ev_ms * 1e-3) / 1e12
-                log(f"{st.splits:>6}{waves:>6}{pipe:>5}{ev_ms * 1e3:>10.1f}{s1 * 1e3:>11.1f}"
-                    f"{tbs:>8.3f}{100 * tbs * 1e3 / PEAK_GBPS:>7.1f}")
+                line = (f"{kind:>6}{st.units if kind == 'units' else st.splits:>6}{waves:>6}"
+                        f"{pipe:>5}{ev_ms * 1e3:>10.1f}{s1 * 1e3:>11.1f}{tbs:>8.3f}"
+                        f"{100 * tbs * 1e3 / PEAK_GBPS:>7.1f}")
+                lines.append(line)
+                log(line)
                 del st
                 torch.cuda.synchronize()
+    out = os.path.join(REPO, "profiles", f"sweep_{args.config}.txt")
+    with open(out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    log(f"wrote {out}")
 
 
 def main():
@@ -867,11 +901,12 @@ def main():
     ap.add_argument("--pipeline", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-targets", action="store_true",
-                    help="C2 only: skip timing the north star's B1/64k and INT4-vs-fp16 "
-                         "targets")
+                    help="C2 only: skip timing the other configurations (EXTRA_CONFIGS)")
     ap.add_argument("--sweep", action="store_true", help="split/waves sweep, table on stderr")
     ap.add_argument("--sweep-splits", default="1,2,4,8,16,32,64,128")
     ap.add_argument("--sweep-waves", default="1,2,4,8")
+    ap.add_argument("--sweep-units", default=None,
+                    help="also sweep these work-unit counts per kv head (comma list)")
     ap.add_argument("--sweep-pipes", default=None,
                     help="chunks in flight per wave (default: 1,2 for fp16, 4 quantized)")
     ap.add_argument("--suite", action="store_true",
@@ -956,34 +991,59 @@ def main():
         print(json.dumps(result), flush=True)
 
 
+# The default line's other configurations, timed like the headline (same steps and
+# warmup, default plans): key prefix -> config. The north star's three targets (B1/64k
+# >= 50% of peak with the cache flushed, fp16 at batch >= 8 / ctx >= 16k >= 80%, INT4 >= 3x
+# fewer µs per step than fp16 at B16/32k), the reference's published grid points
+# (bench_triton_fp16.py:17-20; README.md:24), and every BASELINE.json configuration.
+EXTRA_CONFIGS = (
+    ("b1_64k", "B1_64K"), ("b8_16k", "B8_16K"), ("b32_16k", "B32_16K"),
+    ("b8_64k", "B8_64K"), ("c3", "C3"), ("c4_int8", "C4_INT8"), ("c4_fp8", "C4_FP8"),
+    ("b16_fp16", "B16_FP16"), ("b16_int4", "B16_INT4"), ("c5", "C5"),
+)
+
+
+def config_keys(prefix, res):
+    """The JSON keys of one extra configuration: µs per step and % of the HBM peak
+    (back-to-back steps, and the median with the 256 MB Infinity Cache flushed before each
+    step), and the stage-1 kernel's µs and fraction of the peak."""
+    nbytes = res["config"]["kv_bytes_per_step"]
+    flushed_us = res["us_per_step_flushed_median"]
+    return {
+        f"{prefix}_us_per_step": res["us_per_step"],
+        f"{prefix}_pct_of_peak": res["pct_of_hbm_peak"],
+        f"{prefix}_us_per_step_flushed": flushed_us,
+        f"{prefix}_pct_of_peak_flushed": round(100 * nbytes / (flushed_us * 1e-6)
+                                               / (PEAK_GBPS * 1e9), 2),
+        f"{prefix}_stage1_us": res["roofline"]["kernel_us"],
+        f"{prefix}_stage1_frac": res["roofline"]["frac"],
+    }
+
+
 def north_star_targets(steps, warmup):
-    """The north star's other two targets, timed like the headline (same steps and warmup,
-    default plans, wall clock per step): fp16 batch 1 at 64k tokens against >= 50% of the
-    HBM peak, and INT4 against fp16 at batch 16 / 32k tokens against >= 3x fewer µs per
-    step. Returns the extra keys of the JSON line."""
+    """Every configuration of EXTRA_CONFIGS, timed like the headline, as extra keys of the
+    JSON line, plus `targets`: the north star's three target figures with their bars.
+    B1/64k's target figure is the flushed median (its 268 MB of KV barely exceed the
+    Infinity Cache); B8/16k's is the back-to-back figure, like the headline's (537 MB)."""
     import torch
-    out = {}
-    b1, _ = run_config("B1_64K", steps, warmup)
-    torch.cuda.empty_cache()
-    out["b1_64k_us_per_step"] = b1["us_per_step"]
-    out["b1_64k_pct_of_peak"] = b1["pct_of_hbm_peak"]
-    out["b1_64k_pct_of_peak_flushed"] = round(
-        100 * b1["config"]["kv_bytes_per_step"] / (b1["us_per_step_flushed_median"] * 1e-6)
-        / (PEAK_GBPS * 1e9), 2)
-    fp16, _ = run_config("B16_FP16", steps, warmup)
-    torch.cuda.empty_cache()
-    int4, _ = run_config("B16_INT4", steps, warmup)
-    torch.cuda.empty_cache()
-    out["b16_fp16_us_per_step"] = fp16["us_per_step"]
-    out["b16_int4_us_per_step"] = int4["us_per_step"]
-    out["int4_speedup"] = round(fp16["us_per_step"] / int4["us_per_step"], 3)
-    out["b16_fp16_stage1_us"] = fp16["roofline"]["kernel_us"]
-    out["b16_int4_stage1_us"] = int4["roofline"]["kernel_us"]
-    out["b16_int4_stage1_frac"] = int4["roofline"]["frac"]
-    out["int4_speedup_flushed"] = round(fp16["us_per_step_flushed_median"]
-                                        / int4["us_per_step_flushed_median"], 3)
-    log(f"targets: B1/64k {out['b1_64k_pct_of_peak']}% of peak (>= 50); INT4 vs fp16 at "
-        f"B16/32k {out['int4_speedup']}x (>= 3)")
+    out, res = {}, {}
+    for prefix, config in EXTRA_CONFIGS:
+        r, _ = run_config(config, steps, warmup)
+        torch.cuda.empty_cache()
+        res[prefix] = r
+        out.update(config_keys(prefix, r))
+    out["int4_speedup"] = round(res["b16_fp16"]["us_per_step"] / res["b16_int4"]["us_per_step"],
+                                3)
+    out["int4_speedup_flushed"] = round(res["b16_fp16"]["us_per_step_flushed_median"]
+                                        / res["b16_int4"]["us_per_step_flushed_median"], 3)
+    out["targets"] = {
+        "b1_64k_pct_of_peak_flushed": {"value": out["b1_64k_pct_of_peak_flushed"],
+                                       "bar": ">= 50"},
+        "b8_16k_pct_of_peak": {"value": out["b8_16k_pct_of_peak"], "bar": ">= 80"},
+        "int4_speedup": {"value": out["int4_speedup"], "bar": ">= 3"},
+    }
+    log("targets: " + "; ".join(f"{k} {v['value']} ({v['bar']})"
+                                for k, v in out["targets"].items()))
     return out
 
 

@@ -192,10 +192,13 @@ def _baseline_case(B, ctx, pool, seed=0):
 
 @pytest.mark.parametrize("B,ctx,pool,splits", [
     (1, 4096, 256, 1),        # C1: no split
-    (8, 32768, 16384, None),  # C2: auto split (32 on 256 CUs)
+    (8, 32768, 16384, None),  # C2: the default plan (work units)
     (8, 32768, 16384, 8),
-    (1, 131072, 8192, None),  # C3: auto split
+    (8, 32768, 16384, 32),    # C2 at the reference's own auto count (choose_num_splits)
+    (1, 131072, 8192, None),  # C3: the default plan (splits)
     (1, 131072, 8192, 16),
+    (8, 16384, 8192, None),   # B8/16k, the north star's 80% corner: the default plan
+    (8, 16384, 8192, 4),
 ])
 def test_baseline_configs_match_oracle(B, ctx, pool, splits):
     from kvq_decode_amd import paged_decode_attention
