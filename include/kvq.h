@@ -72,7 +72,7 @@ typedef enum kvq_status {
  * group but not the group's other blocks (prefix caching, beam forks; with 16-token
  * pages page 2j leads the V group of pages 2j and 2j + 1) overwrite each other's pairs:
  * copy such a block on write, or share whole groups only.
- * The quantized formats decode at head_dim D = 64, 128 or 256 (fp16: 32-256), and the
+ * The quantized formats decode at head_dim D = 64, 128 or 256 (fp16: 16-256), and the
  * quantizers (kvq_quantize_cache, kvq_quantize_append) write exactly those head dims:
  * any other returns KVQ_ERR_UNSUPPORTED from both, so no cache is written that no decode
  * can read.

@@ -72,7 +72,7 @@ int check_decode_args(const kvq_decode_args* a, bool need_out) {
     // (triton_fp16.py:197-198); anything else is a shape error here too.
     if (!is_pow2(a->head_dim) || a->head_dim < 16) return KVQ_ERR_SHAPE;
     if (!is_pow2(a->block_size) || a->block_size < 16) return KVQ_ERR_SHAPE;
-    if (a->head_dim < 32 || a->head_dim > 256) return KVQ_ERR_UNSUPPORTED;
+    if (a->head_dim > 256) return KVQ_ERR_UNSUPPORTED;
     if (a->block_size > 4096) return KVQ_ERR_UNSUPPORTED;
     // token positions are 32-bit
     if (int64_t(a->max_blocks) * a->block_size > INT32_MAX) return KVQ_ERR_UNSUPPORTED;
@@ -536,7 +536,7 @@ int kvq_decode_merge(const float* o_part, const float* lse, void* out, int64_t o
     if (batch < 1 || q_heads < 1 || num_splits < 1) return KVQ_ERR_SHAPE;
     if (batch > 65535) return KVQ_ERR_UNSUPPORTED;
     if (!is_pow2(head_dim) || head_dim < 16) return KVQ_ERR_SHAPE;
-    if (head_dim < 32 || head_dim > 256) return KVQ_ERR_UNSUPPORTED;
+    if (head_dim > 256) return KVQ_ERR_UNSUPPORTED;
     return hip_status(kvq::launch_merge(o_part, lse, out, o_stride_b, o_stride_h, batch, q_heads,
                                         head_dim, num_splits,
                                         reinterpret_cast<hipStream_t>(stream)));

@@ -41,14 +41,19 @@ namespace kvq {
 // One 16-token chunk of one kv head, fp16 cache, as held by one lane. K in row layout:
 // load i holds K[RPL*i + l/PC][8*(l%PC) .. +8] (PC = D/8 16-byte pieces per row, RPL =
 // 64/PC rows per load); V as the PV product's A operand needs it (see the file header).
+// Head dim 16 (the reference's smallest) is the exception: one 8-byte load per lane
+// gives the 16x16x16 QK product's A operand directly (lane (i16, g): row i16, halves
+// 4g .. 4g + 3), held in the low half of k[0].
 template <int D>
 struct ChunkF16 {
     static constexpr int NST = D / 32;   // K loads per chunk = k-steps of the QK product
+    static constexpr int KN = D >= 32 ? NST : 1;
     static constexpr int DV = D / 16;
     static constexpr int PC = D / 8;     // 16-byte pieces per K row
     static constexpr int RPL = 64 / PC;  // K rows per load instruction
-    typedef typename HalfVec<DV>::type vrow;
-    h8 k[NST];
+    // a lane's D/16 halves of a V row (D = 16: the one half in element 0 of a pair)
+    typedef typename HalfVec<(DV > 1 ? DV : 2)>::type vrow;
+    h8 k[KN];
     vrow v[4];
 };
 
@@ -60,7 +65,7 @@ struct ChunkF16 {
 // chunk_f16.
 template <int D>
 struct F16LaneOff {
-    uint32_t k[D / 32], v[4];
+    uint32_t k[ChunkF16<D>::KN], v[4];
 };
 
 template <int D>
@@ -69,10 +74,14 @@ __device__ __forceinline__ F16LaneOff<D> f16_lane_offsets(const DecodeParams& p,
     typedef ChunkF16<D> C;
     const int lane = __lane_id();
     F16LaneOff<D> o;
+    if constexpr (D == 16) {
+        o.k[0] = (uint32_t)(min(i16, last) * (int)p.k_stok + 4 * g) * 2u;
+    } else {
 #pragma unroll
-    for (int i = 0; i < C::NST; ++i)
-        o.k[i] = (uint32_t)(min(C::RPL * i + lane / C::PC, last) * (int)p.k_stok +
-                            8 * (lane % C::PC)) * 2u;
+        for (int i = 0; i < C::NST; ++i)
+            o.k[i] = (uint32_t)(min(C::RPL * i + lane / C::PC, last) * (int)p.k_stok +
+                                8 * (lane % C::PC)) * 2u;
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r)
         o.v[r] = (uint32_t)(min(4 * g + r, last) * (int)p.v_stok + C::DV * i16) * 2u;
@@ -84,12 +93,16 @@ __device__ __forceinline__ F16LaneOff<D> f16_lane_offsets(const DecodeParams& p,
 // about 10% faster than default-policy ones.
 constexpr int kNT = 2;
 
-// D/16 consecutive halves (4, 8, 16 or 32 bytes) at byte offset `off` of a page.
+// D/16 consecutive halves (2, 4, 8, 16 or 32 bytes) at byte offset `off` of a page (head dim
+// 16: the one half in element 0 of a pair).
 template <int DV>
-__device__ __forceinline__ typename HalfVec<DV>::type load_vrow(__amdgpu_buffer_rsrc_t r,
-                                                                uint32_t off) {
-    typedef typename HalfVec<DV>::type vrow;
-    if constexpr (DV == 2) {
+__device__ __forceinline__ typename HalfVec<(DV > 1 ? DV : 2)>::type load_vrow(
+    __amdgpu_buffer_rsrc_t r, uint32_t off) {
+    typedef typename HalfVec<(DV > 1 ? DV : 2)>::type vrow;
+    if constexpr (DV == 1) {
+        const uint32_t x = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, kNT);
+        return __builtin_bit_cast(vrow, x);
+    } else if constexpr (DV == 2) {
         return __builtin_bit_cast(vrow, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kNT));
     } else if constexpr (DV == 4) {
         return __builtin_bit_cast(vrow, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kNT));
@@ -118,6 +131,11 @@ __device__ __forceinline__ void load_chunk_f16(const DecodeParams& p, int kvh, i
     const char* vb = (const char*)p.v + block_offset(phys, 2 * p.v_sblk) +
                      2 * ((int64_t)slot * p.v_stok + (int64_t)kvh * p.v_sh);
     const auto rk = page_rsrc(kb), rv = page_rsrc(vb);
+    if constexpr (D == 16) {
+        const u2 x = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(rk, lo.k[0], 0, kNT));
+        const u4v w = {x[0], x[1], 0u, 0u};
+        ch.k[0] = __builtin_bit_cast(h8, w);
+    }
 #pragma unroll
     for (int st = 0; st < D / 32; ++st)
         ch.k[st] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rk, lo.k[st], 0,
@@ -136,6 +154,33 @@ __device__ __forceinline__ uint32_t kstage_off(int row, int piece) {
     return (uint32_t)(row * 2 * D + 16 * (piece ^ (row & (PC - 1))));
 }
 
+// The PV product's A operand of tile t from a lane's 4 token rows (its D/16 halves of each):
+// {v[0][t], v[1][t], v[2][t], v[3][t]}. With 2-half rows (head dim 32) the halves are
+// picked by v_perm, two instructions; element-wise, the compiler assembled them through
+// scratch memory.
+template <int D>
+__device__ __forceinline__ h4 pv_rows(const typename ChunkF16<D>::vrow* v, int t) {
+    if constexpr (ChunkF16<D>::DV == 2) {
+        const uint32_t sel = t ? 0x07060302u : 0x05040100u;
+        const u2 w = {__builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, v[1]),
+                                            __builtin_bit_cast(uint32_t, v[0]), sel),
+                      __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, v[3]),
+                                            __builtin_bit_cast(uint32_t, v[2]), sel)};
+        return __builtin_bit_cast(h4, w);
+    } else {
+        h4 a;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) a[r] = v[r][t];
+        return a;
+    }
+}
+
+// Two lanes' worth of rows for a 16x16x32 product: chunk a's in k-slots 0-3, b's in 4-7.
+template <int D>
+__device__ __forceinline__ h8 pv_rows2(const ChunkF16<D>& a, const ChunkF16<D>& b, int t) {
+    return __builtin_shufflevector(pv_rows<D>(a.v, t), pv_rows<D>(b.v, t), 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
 // One chunk: QK^T, softmax update, PV. MASK handles the sequence's partial last chunk.
 // `kst` is the wave's K staging tile in LDS (32 * D bytes).
 template <int D, bool MASK>
@@ -146,16 +191,23 @@ __device__ __forceinline__ void chunk_f16(const ChunkF16<D>& ch, const h8* qop, 
     constexpr int DV = C::DV;
     typedef typename ChunkF16<D>::vrow vrow;
     const int lane = __lane_id();
-#pragma unroll
-    for (int i = 0; i < NST; ++i)
-        *(h8*)(kst + kstage_off<D>(C::RPL * i + lane / C::PC, lane % C::PC)) = ch.k[i];
-    h8 kop[NST];
-#pragma unroll
-    for (int k = 0; k < NST; ++k) kop[k] = *(const h8*)(kst + kstage_off<D>(lane & 15, 4 * k + g));
     f4 s = (f4)0.f;
+    if constexpr (D == 16) {  // the loaded halves are the A operand; q in qop[0]'s low half
+        const h4 kop = {ch.k[0][0], ch.k[0][1], ch.k[0][2], ch.k[0][3]};
+        const h4 qo = {qop[0][0], qop[0][1], qop[0][2], qop[0][3]};
+        s = __builtin_amdgcn_mfma_f32_16x16x16f16(kop, qo, s, 0, 0, 0);
+    } else {
 #pragma unroll
-    for (int k = 0; k < NST; ++k)
-        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[k], qop[k], s, 0, 0, 0);
+        for (int i = 0; i < NST; ++i)
+            *(h8*)(kst + kstage_off<D>(C::RPL * i + lane / C::PC, lane % C::PC)) = ch.k[i];
+        h8 kop[NST];
+#pragma unroll
+        for (int k = 0; k < NST; ++k)
+            kop[k] = *(const h8*)(kst + kstage_off<D>(lane & 15, 4 * k + g));
+#pragma unroll
+        for (int k = 0; k < NST; ++k)
+            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[k], qop[k], s, 0, 0, 0);
+    }
     float s2[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) s2[r] = s[r] * sl2;
@@ -186,11 +238,7 @@ __device__ __forceinline__ void chunk_f16(const ChunkF16<D>& ch, const h8* qop, 
     // from hoisting all multiplies (and their registers) ahead of the MFMAs.
 #pragma unroll
     for (int t = 0; t < DV; ++t) {
-        h4 a;
-        a[0] = ch.v[0][t];
-        a[1] = ch.v[1][t];
-        a[2] = ch.v[2][t];
-        a[3] = ch.v[3][t];
+        const h4 a = pv_rows<D>(ch.v, t);
         st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pop, st.acc[t] * alpha, 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -250,12 +298,7 @@ __device__ __forceinline__ void chunk_pair_f16(const ChunkF16<D>& ca, const Chun
     for (int r = 0; r < 8; ++r) pop[r] = (_Float16)pr[r];
 #pragma unroll
     for (int t = 0; t < DV; ++t) {
-        h8 a;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            a[r] = ca.v[r][t];
-            a[4 + r] = cb.v[r][t];
-        }
+        const h8 a = pv_rows2<D>(ca, cb, t);
         st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pop, st.acc[t] * alpha, 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -336,14 +379,7 @@ __device__ __forceinline__ void chunk_quad_f16(const ChunkF16<D>* ch, const h8* 
     }
 #pragma unroll
     for (int t = 0; t < DV; ++t) {
-        h8 a01, a23;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            a01[r] = ch[0].v[r][t];
-            a01[4 + r] = ch[1].v[r][t];
-            a23[r] = ch[2].v[r][t];
-            a23[4 + r] = ch[3].v[r][t];
-        }
+        const h8 a01 = pv_rows2<D>(ch[0], ch[1], t), a23 = pv_rows2<D>(ch[2], ch[3], t);
         st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a01, b01, st.acc[t] * alpha, 0, 0, 0);
         st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a23, b23, st.acc[t], 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
@@ -460,7 +496,13 @@ __device__ __forceinline__ void load_q_raw(const DecodeParams& p, int kvh, int b
     const int i16 = lane & 15, g = lane >> 4;
     const int G = p.group;
     const _Float16* qrow = (const _Float16*)p.q + (int64_t)b * p.q_sb +
-                           (int64_t)(kvh * G + (i16 < G ? i16 : 0)) * p.q_sh + 8 * g;
+                           (int64_t)(kvh * G + (i16 < G ? i16 : 0)) * p.q_sh +
+                           (D == 16 ? 4 : 8) * g;
+    if constexpr (D == 16) {  // halves 4g .. 4g + 3, in the low half of qraw[0]
+        const u2 x = *(const u2*)qrow;
+        const u4v w = {x[0], x[1], 0u, 0u};
+        qraw[0] = __builtin_bit_cast(h8, w);
+    }
 #pragma unroll
     for (int k = 0; k < D / 32; ++k) qraw[k] = *(const h8*)(qrow + 32 * k);
 }
@@ -469,7 +511,7 @@ template <int D>
 __device__ __forceinline__ void q_operand(const DecodeParams& p, const h8* qraw, h8* qop) {
     const bool head_ok = (threadIdx.x & 15) < p.group;
 #pragma unroll
-    for (int k = 0; k < D / 32; ++k) qop[k] = head_ok ? qraw[k] : (h8)(_Float16)0;
+    for (int k = 0; k < ChunkF16<D>::KN; ++k) qop[k] = head_ok ? qraw[k] : (h8)(_Float16)0;
 }
 
 // The first loads of a wave's range, issued ahead by the work units for their guessed
@@ -478,7 +520,7 @@ __device__ __forceinline__ void q_operand(const DecodeParams& p, const h8* qraw,
 // [w_lo, last].
 template <int D, int P>
 struct F16Pre {
-    h8 qraw[D / 32];
+    h8 qraw[ChunkF16<D>::KN];
     int pg_cur, pg_nxt;
     int b, w_lo, last;
     bool live;
@@ -524,7 +566,7 @@ __device__ __forceinline__ void f16_range(const DecodeParams& p, int kvh, int b,
                                           bool use_pre) {
     constexpr int NST = D / 32;
     constexpr int DV = D / 16;
-    if constexpr (D <= 32) {
+    if constexpr (D == 32) {
         if (p.group <= 4) {
             f16_quad_range<D, W, FINAL>(p, kvh, b, seq_len, w_lo, w_hi, wave, part_base,
                                         part_stride);
@@ -538,12 +580,13 @@ __device__ __forceinline__ void f16_range(const DecodeParams& p, int kvh, int b,
     const int kvc = cache_head(p, kvh);
     const bool pre_b = use_pre && pre.live && pre.b == b;
 
-    // Q^T operand: lane (head i16, g) holds Q[head][32*k + 8*g + 0..7]; padded heads = 0.
-    h8 qop[NST];
+    // Q^T operand: lane (head i16, g) holds Q[head][32*k + 8*g + 0..7] (D = 16:
+    // Q[head][4g .. 4g + 3]); padded heads = 0.
+    h8 qop[ChunkF16<D>::KN];
     if (pre_b) {
         q_operand<D>(p, pre.qraw, qop);
     } else {
-        h8 qraw[NST];
+        h8 qraw[ChunkF16<D>::KN];
         load_q_raw<D>(p, kvh, b, qraw);
         q_operand<D>(p, qraw, qop);
     }
@@ -563,7 +606,7 @@ __device__ __forceinline__ void f16_range(const DecodeParams& p, int kvh, int b,
     // Head dims up to 64 run chunk pairs (w_lo + 2k, w_lo + 2k + 1), the wave's odd last
     // full chunk alone; the ring holds at least 2 chunks (depth 1 runs as 2), so the ring
     // depth never changes the arithmetic.
-    constexpr bool PAIRS = D <= 64;
+    constexpr bool PAIRS = D >= 32 && D <= 64;
     constexpr int PR = f16_ring<D, P>();
     const int r_hi = min(w_hi, c_full);
     if (w_lo < r_hi) {
@@ -660,8 +703,9 @@ template <int D>
 __device__ __forceinline__ void merge_rows(const float* __restrict__ o_part,
                                            const float* __restrict__ lse, int64_t row0, int S,
                                            _Float16* __restrict__ out) {
-    constexpr int PER = D / 32;  // columns per thread (1..8)
+    constexpr int PER = D >= 32 ? D / 32 : 1;  // columns per thread (1..8)
     const int t = threadIdx.x, lane32 = t & 31, grp = t >> 5;
+    const bool cols = lane32 * PER < D;  // head dim 16: lanes 16-31 of a group hold none
     float m = -INFINITY, wsum = 0.f;
     float acc[PER];
 #pragma unroll
@@ -669,10 +713,10 @@ __device__ __forceinline__ void merge_rows(const float* __restrict__ o_part,
 #pragma unroll 4
     for (int s = grp; s < S; s += 8) {
         const float l = lse[row0 + s] * kLog2e;
-        const float* src = o_part + (row0 + s) * D + lane32 * PER;
+        const float* src = o_part + (row0 + s) * D + (cols ? lane32 * PER : 0);
         float o[PER];
 #pragma unroll
-        for (int e = 0; e < PER; ++e) o[e] = src[e];
+        for (int e = 0; e < PER; ++e) o[e] = cols ? src[e] : 0.f;
         if (l > m) {  // the running max grows: rescale what is summed so far
             const float r = fast_exp2(m - l);  // 0 while nothing is summed (m = -inf)
             wsum *= r;
@@ -688,7 +732,8 @@ __device__ __forceinline__ void merge_rows(const float* __restrict__ o_part,
     __shared__ float sm_acc[8][D];
     __shared__ float sm_m[8], sm_w[8];
 #pragma unroll
-    for (int e = 0; e < PER; ++e) sm_acc[grp][lane32 * PER + e] = acc[e];
+    for (int e = 0; e < PER; ++e)
+        if (cols) sm_acc[grp][lane32 * PER + e] = acc[e];
     if (lane32 == 0) {
         sm_m[grp] = m;
         sm_w[grp] = wsum;
@@ -853,6 +898,7 @@ hipError_t launch_decode_units(const DecodeParams& p, int kv_format, int head_di
     if (kv_format != KVQ_KV_F16)
         return launch_decode_q_units(p, kv_format, head_dim, waves, ring, stream);
     switch (head_dim) {
+        case 16: return launch_units_d<16>(p, waves, ring, stream);
         case 32: return launch_units_d<32>(p, waves, ring, stream);
         case 64: return launch_units_d<64>(p, waves, ring, stream);
         case 128: return launch_units_d<128>(p, waves, ring, stream);
@@ -864,6 +910,7 @@ hipError_t launch_decode_units(const DecodeParams& p, int kv_format, int head_di
 hipError_t launch_merge_units(const DecodeParams& p, int head_dim, hipStream_t stream) {
     const dim3 grid(p.q_heads, p.batch);
     switch (head_dim) {
+        case 16: hipLaunchKernelGGL(merge_units_kernel<16>, grid, dim3(256), 0, stream, p); break;
         case 32: hipLaunchKernelGGL(merge_units_kernel<32>, grid, dim3(256), 0, stream, p); break;
         case 64: hipLaunchKernelGGL(merge_units_kernel<64>, grid, dim3(256), 0, stream, p); break;
         case 128: hipLaunchKernelGGL(merge_units_kernel<128>, grid, dim3(256), 0, stream, p); break;
@@ -878,6 +925,7 @@ hipError_t launch_decode(const DecodeParams& p, int kv_format, int head_dim, boo
     if (kv_format != KVQ_KV_F16)
         return launch_decode_q(p, kv_format, head_dim, final_out, waves, pipe, stream);
     switch (head_dim) {
+        case 16: return launch_f16_d<16>(p, final_out, waves, pipe, stream);
         case 32: return launch_f16_d<32>(p, final_out, waves, pipe, stream);
         case 64: return launch_f16_d<64>(p, final_out, waves, pipe, stream);
         case 128: return launch_f16_d<128>(p, final_out, waves, pipe, stream);
@@ -892,6 +940,10 @@ hipError_t launch_merge(const float* o_part, const float* lse, void* out, int64_
     const dim3 grid(q_heads, batch);
     _Float16* o = (_Float16*)out;
     switch (head_dim) {
+        case 16:
+            hipLaunchKernelGGL(merge_kernel<16>, grid, dim3(256), 0, stream, o_part, lse, o,
+                               o_sb, o_sh, q_heads, num_splits);
+            break;
         case 32:
             hipLaunchKernelGGL(merge_kernel<32>, grid, dim3(256), 0, stream, o_part, lse, o,
                                o_sb, o_sh, q_heads, num_splits);

@@ -51,8 +51,6 @@
 
 namespace kvq {
 
-typedef uint32_t u2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 // v_perm_b32: byte k of the result is byte sel.k of {hi:lo} (0-3 = lo, 4-7 = hi, 12 = 0x00).

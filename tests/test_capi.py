@@ -385,7 +385,7 @@ def test_quantized_tuning_limits():
 
 
 def test_quantized_head_dims():
-    """Quantized caches: head_dim 64, 128 or 256 (fp16 takes 32-256); head_dim 256 takes
+    """Quantized caches: head_dim 64, 128 or 256 (fp16 takes 16-256); head_dim 256 takes
     rings of 1 or 2 chunks. A call whose arguments pass the checks reaches the split-count
     check (KVQ_ERR_SPLITS for num_splits 0)."""
     L = _lib.lib()

@@ -140,10 +140,11 @@ def test_workgroup_shapes_agree(waves, pipeline):
         assert torch.equal(out, base), f"ring depth {pipeline} changed bits (splits={splits})"
 
 
-@pytest.mark.parametrize("D", [32, 64, 256])
+@pytest.mark.parametrize("D", [16, 32, 64, 256])
 @pytest.mark.parametrize("pipeline", [1, 2, 4])
 def test_ring_depths_other_head_dims(D, pipeline):
-    """The ring's loads for head_dim 32 / 64 / 256 (4-, 8- and 32-byte V rows per lane)."""
+    """The ring's loads for head_dim 16 / 32 / 64 / 256 (2-, 4-, 8- and 32-byte V rows per
+    lane; head_dim 16 takes its K rows as the 16x16x16 product's operand, 8 bytes per lane)."""
     from kvq_decode_amd import paged_decode_attention
     if D == 256 and pipeline == 4:
         pytest.skip("ring depth 4 is built up to head_dim 128")
@@ -155,13 +156,15 @@ def test_ring_depths_other_head_dims(D, pipeline):
         check_close(out, ref, f"D={D} pipe={pipeline} splits={splits}")
 
 
-@pytest.mark.parametrize("Hq,Hkv", [(4, 4), (4, 2), (16, 4)])
-@pytest.mark.parametrize("D", [32, 64])
+@pytest.mark.parametrize("Hq,Hkv", [(4, 4), (4, 2), (16, 4), (16, 1)])
+@pytest.mark.parametrize("D", [16, 32, 64])
 def test_small_head_dim_chunk_groups(Hq, Hkv, D):
     """Head dim 32 with up to 4 q heads per kv head runs 4-chunk steps (chunk slots in the MFMA
-    columns), head dim 64 2-chunk steps: lengths that leave 1, 2 and 3 full chunks after the
-    last full step and partial last chunks, on the single-pass, split, work-unit and default
-    paths against the oracle, and every ring depth gives the same bits."""
+    columns), head dim 64 2-chunk steps, head dim 16 (the reference's smallest) single chunks
+    of one 16x16x16 QK product (16 q heads per kv head fill its columns): lengths that leave
+    1, 2 and 3 full chunks after the last full step and partial last chunks, on the
+    single-pass, split, work-unit and default paths against the oracle, and every ring depth
+    gives the same bits."""
     from kvq_decode_amd import paged_decode_attention
     lens = [16 * 4 + 5, 16 * 5, 16 * 6 + 1, 16 * 7, 1, 16 * 37 + 9]
     q, kc, vc, bt, sl = make(Hq, Hkv, D, 16, lens, seed=23)

@@ -30,7 +30,7 @@ def test_units_match_reference(Hq, Hkv, D, block_size, lens, units):
     check_close(out, ref, f"units={units} Hq={Hq} Hkv={Hkv} D={D} bs={block_size} lens={lens}")
 
 
-@pytest.mark.parametrize("D", [32, 256])
+@pytest.mark.parametrize("D", [16, 32, 256])
 @pytest.mark.parametrize("pipeline", [1, 2, 4])
 def test_units_head_dims_and_ring_depths(D, pipeline):
     from kvq_decode_amd import paged_decode_attention
@@ -219,7 +219,7 @@ def test_plan_workspace_shapes_fit_the_default_plan(lens):
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("D", [32, 64])
+@pytest.mark.parametrize("D", [16, 32, 64])
 @pytest.mark.parametrize("lens", [[3000, 17, 900, 64], [5000]])
 def test_head_dim_plans_default_path(D, lens):
     """Below head_dim 128 the default plan runs more waves (fp16: work units in 4-wave
