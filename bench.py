@@ -17,8 +17,8 @@ The default C2 line also carries, timed the same way (same steps and warmup, def
 plans), every other configuration of EXTRA_CONFIGS as <prefix>_* keys: the north star's
 targets (fp16 B1/64k >= 50% of the peak with the cache flushed, fp16 B8/16k >= 80%, INT4
 >= 3x fewer µs per step than fp16 at B16/32k; collected under `targets`), the reference's
-published grid points (B8/16k, B32/16k, B8/64k) and BASELINE.json's C3, C4 (INT8, FP8) and
-C5. --no-targets skips them. roofline.kernel_us is stage 1 timed over back-to-back
+published grid points (B8/16k, B32/16k, B8/64k) and BASELINE.json's C1 (its single pass), C3,
+C4 (INT8, FP8) and C5. --no-targets skips them. roofline.kernel_us is stage 1 timed over back-to-back
 stage-1 launches; `pre_timing` lists what runs before the warmup and timed steps.
 
 --layers N times a whole-model decode step instead: N layers, each with its own cache of
@@ -999,7 +999,7 @@ def main():
 EXTRA_CONFIGS = (
     ("b1_64k", "B1_64K"), ("b8_16k", "B8_16K"), ("b32_16k", "B32_16K"),
     ("b8_64k", "B8_64K"), ("c3", "C3"), ("c4_int8", "C4_INT8"), ("c4_fp8", "C4_FP8"),
-    ("b16_fp16", "B16_FP16"), ("b16_int4", "B16_INT4"), ("c5", "C5"),
+    ("b16_fp16", "B16_FP16"), ("b16_int4", "B16_INT4"), ("c5", "C5"), ("c1", "C1"),
 )
 
 

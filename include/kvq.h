@@ -158,7 +158,8 @@ int kvq_head_blocks(int32_t q_heads, int32_t kv_heads);
  * heuristic above (triton_fp16.py:175-180) on this hardware. It sizes the decomposition
  * in waves, because a workgroup here holds several waves that combine through LDS:
  *   per_pair = pow2_floor(T * cu_count / (batch * kv_heads)), T = 2 s waves per CU (fp16,
- *              s = max(1, 128 / head_dim)), 4 (INT8, FP8) or 8 (INT4), raised to
+ *              s = max(1, 128 / head_dim); head dims 16 and 32: 64 / head_dim), 4 (INT8,
+ *              FP8) or 8 (INT4), raised to
  *              pow2_floor(cdiv(chunks, C)) (C = 512 chunks per wave for fp16; quantized
  *              256, or 64 when batch * kv_heads > cu_count, so that uneven sequence
  *              lengths still balance), capped at pow2_floor(chunks / 4);
@@ -172,7 +173,9 @@ int kvq_head_blocks(int32_t q_heads, int32_t kv_heads);
  * (sequence, kv head) and, for large ragged batches, several waves per workgroup on small
  * partitions (all measured on MI355X for batch 1..64 and 32k..128k contexts). fp16 head
  * dims below 128 move fewer bytes per chunk through about the same per-chunk work and
- * need s times the waves (the quantized split plans measured slower with them).
+ * need s times the waves (the quantized split plans measured slower with them); at 16 and
+ * 32 the kv heads' rows share 128-byte lines, served from one L2 by the grouped XCD order,
+ * so half of 128 / head_dim suffices.
  * A workgroup's LDS (its waves' cross-wave combine, proportional to waves * q heads per
  * kv head * head_dim, or their staging tiles) must fit 64 KB: where it would not (large
  * q-head groups at head dim 256), waves is halved and splits doubled until it does.
@@ -192,7 +195,7 @@ int kvq_plan_decode(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t bl
  *   units = T * cu_count / (waves * kv_heads) (at least 1), with T waves per CU and
  *           `waves` per unit workgroup: fp16 T = 2 s, waves = min(2 s, 4); INT8 / FP8
  *           T = 4 s, waves = 4; INT4 T = 8 s, waves = min(2 s, 4)
- *           (s = max(1, 128 / head_dim)),
+ *           (s as in kvq_plan_decode),
  * for kvq_decode_units; otherwise units = waves = 0 (use kvq_plan_decode's split plan).
  * As in kvq_plan_decode, waves is halved (and units doubled) until a workgroup's LDS fits
  * 64 KB, and q_heads / kv_heads must be 1..16.

@@ -160,9 +160,13 @@ kvq::DecodeParams make_params(const kvq_decode_args* a) {
     p.k_group_shift = a->kv_format == KVQ_KV_F16 ? 0 : ilog2(a->k_group / 16);
     p.k_group_pages = a->kv_format == KVQ_KV_F16 ? 0 : a->k_group / a->block_size;
     p.scale_log2 = a->scale * 1.4426950408889634f;
-    // grouped XCD order for the quantized caches, whose kv heads share V-scale lines;
-    // plain for fp16 (measured about 1% faster there)
-    p.xcd_group = a->kv_format != KVQ_KV_F16;
+    // grouped XCD order (the kv heads of a unit on one XCD, so one L2 serves a line they
+    // share) for the quantized caches and for fp16 rows shorter than a 128-byte line (head
+    // dims 16 and 32: the vLLM layout puts 2 or 4 heads' rows of a token in one line, which
+    // the plain order fetched once per head, on different XCDs; measured at B8 x 32k,
+    // 32 q / 8 kv heads: stage 1 D = 32 89.3 -> 69.0 us, D = 16 85.1 -> 50.0 us); plain for
+    // fp16 rows of whole lines (measured about 1% faster there)
+    p.xcd_group = a->kv_format != KVQ_KV_F16 || a->head_dim < 64;
     return p;
 }
 
@@ -363,7 +367,15 @@ int units_params(const kvq_decode_args* args, int32_t units, float* o_part, floa
 // -> 0.57 at batch 1 x 64k, at head_dim 32 0.14 -> 0.27; quantized work units +1-19% at
 // head_dim 64. The quantized split plan (single sequences) measured 2-9% slower with the
 // extra waves and keeps the 128 plan, and so does head_dim 256 everywhere.
-int64_t head_dim_scale(int32_t head_dim) { return head_dim < 128 ? 128 / head_dim : 1; }
+// Waves-per-CU factor of the head dims below 128, whose chunks carry fewer bytes for the
+// same per-chunk work: 128 / D, except that head dims 16 and 32 take 64 / D. Their rows
+// share 128-byte lines between kv heads, which the grouped XCD order serves from one L2, so
+// part of their bytes come from L2 and fewer waves keep HBM busy (measured at B8 x 32k,
+// 32 q / 8 kv heads, stage 1: D = 32 68.3 us at 8 waves per CU, 66.3 at 4; D = 16 49.3 us
+// at 16, 46.2-46.9 at 8).
+int64_t head_dim_scale(int32_t head_dim) {
+    return head_dim >= 128 ? 1 : head_dim >= 64 ? 128 / head_dim : 64 / head_dim;
+}
 
 }  // namespace
 

@@ -111,11 +111,12 @@ __device__ __forceinline__ int cache_head(const DecodeParams& p, int kvh) {
 // round-robin by linear id, and each XCD has its own L2. The decode kernels run a 1-D grid
 // and map its ids to (kv head, split, sequence) units (U = splits * batch of them) in one
 // of two orders, chosen by the host (DecodeParams::xcd_group):
-//   plain:   id = kvh + kv_heads * u, the kv heads of a unit spread over the XCDs (fp16,
-//            whose heads share no cache lines);
+//   plain:   id = kvh + kv_heads * u, the kv heads of a unit spread over the XCDs (fp16
+//            at head dims of 64 and more, whose heads share no cache lines);
 //   grouped: every kv head of a unit on one XCD, back to back, so that a line they share
-//            (the quantized caches' V scales: 4 heads per 128-byte line) is fetched by one
-//            L2. With a split count that is a multiple of 8, split s of sequence b runs on
+//            (fp16 at head dims 16 and 32, whose token-major rows put 4 or 2 heads in one
+//            128-byte line; the quantized caches) is fetched by one L2. With a split count
+//            that is a multiple of 8, split s of sequence b runs on
 //            XCD (s + b) % 8 - a sequence's early splits, the ones short sequences have,
 //            land on different XCDs for different sequences; otherwise unit u runs on XCD
 //            u % 8 (U rounded up to a multiple of 8; workgroups past the last unit exit).

@@ -86,8 +86,8 @@ def plan_decode(batch: int, kv_heads: int, block_size: int, max_pages: int,
     512 (fp16) / 256 or, for batches whose (sequence, kv head) pairs outnumber the CUs, 64
     (quantized) 16-token chunks per wave; up to 2 waves per workgroup for fp16, and for
     quantized caches one wave per 8 waves of the (sequence, kv head) pair, up to 4 (INT4:
-    8). fp16 head dims below 128 get 128 / head_dim times the waves, in workgroups of up
-    to 4 waves. Waves are halved (splits doubled) until a workgroup's LDS, which grows with
+    8). fp16 head dims below 128 get 128 / head_dim times the waves (16 and 32, whose rows
+    share lines between kv heads: 64 / head_dim), in workgroups of up to 4 waves. Waves are halved (splits doubled) until a workgroup's LDS, which grows with
     the q heads per kv head, fits 64 KB. `kv_heads` counts the kernels' kv heads (see
     `head_blocks`); `q_heads` (default: kv_heads, one q head per kv head) all q heads."""
     _require(kv_format in KV_FORMATS, f"kv_format must be one of {tuple(KV_FORMATS)}")
@@ -127,7 +127,8 @@ def plan_units(batch: int, kv_heads: int, block_size: int, max_pages: int,
     least 4096 tokens, get 2 waves per CU in 2-wave
     unit workgroups (fp16), 4 in 4-wave workgroups (INT8, FP8) or 8 in 2-wave workgroups
     (INT4), which keeps ragged batches balanced. Head dims below 128 get 128 / head_dim
-    times the waves per CU, and fp16 / INT4 unit workgroups of up to 4 waves. As in
+    times the waves per CU (16 and 32: 64 / head_dim), and fp16 / INT4 unit workgroups of up
+    to 4 waves. As in
     `plan_decode`, waves are halved (units doubled) until a workgroup's LDS fits 64 KB, and
     `q_heads` defaults to kv_heads."""
     _require(kv_format in KV_FORMATS, f"kv_format must be one of {tuple(KV_FORMATS)}")

@@ -162,13 +162,15 @@ def test_plan_decode():
 
 
 def test_plan_head_dims():
-    """Head dims below 128 get 128 / head_dim times the waves per CU in the work-unit plan
-    (fp16 and INT4 unit workgroups of up to 4 waves) and, for fp16 only, in the split plan
-    (workgroups of up to 4); 256 keeps the 128 plan."""
+    """Head dims below 128 get 128 / head_dim times the waves per CU (16 and 32, whose rows
+    share lines between kv heads: 64 / head_dim) in the work-unit plan (fp16 and INT4 unit
+    workgroups of up to 4 waves) and, for fp16 only, in the split plan (workgroups of up to
+    4); 256 keeps the 128 plan."""
     from kvq_decode_amd.ops import plan_decode, plan_units
     decode_cases = [  # batch, max_pages, format, head_dim -> (splits, waves)
         (8, 2048, "fp16", 64, (4, 4)),    # 4 waves per CU: 16 per pair
-        (8, 2048, "fp16", 32, (8, 4)),    # 8 waves per CU: 32 per pair
+        (8, 2048, "fp16", 32, (4, 4)),    # 4 waves per CU: 16 per pair
+        (8, 2048, "fp16", 16, (8, 4)),    # 8 waves per CU: 32 per pair
         (8, 2048, "fp16", 256, (4, 2)),   # as at 128
         (16, 2048, "int8", 64, (8, 1)),   # quantized split plans: as at 128
         (16, 2048, "int4", 64, (8, 2)),
@@ -178,7 +180,8 @@ def test_plan_head_dims():
         assert plan_decode(batch, 8, 16, pages, 256, fmt, hd) == want, (batch, fmt, hd)
     units_cases = [  # batch, max_pages, format, head_dim -> (units, waves)
         (8, 2048, "fp16", 64, (32, 4)),    # 4 waves per CU in 4-wave workgroups
-        (8, 2048, "fp16", 32, (64, 4)),    # 8 waves per CU
+        (8, 2048, "fp16", 32, (32, 4)),    # 4 waves per CU
+        (8, 2048, "fp16", 16, (64, 4)),    # 8 waves per CU
         (8, 2048, "fp16", 256, (32, 2)),   # as at 128
         (64, 2048, "int4", 64, (128, 4)),  # 16 waves per CU
         (16, 2048, "int8", 64, (64, 4)),   # 8 waves per CU
@@ -260,8 +263,8 @@ def test_plan_workspace_shapes():
     assert plan_workspace_shapes(1, 32, 8, 128, 16, 4096, 256) == ((1, 32, 32, 128), (1, 32, 32))
     # a single pass over short contexts needs none
     assert plan_workspace_shapes(64, 32, 8, 128, 16, 64, 256) is None
-    # head_dim 32: 8 waves per CU in 4-wave unit workgroups, 64 units per kv head
-    assert plan_workspace_shapes(8, 32, 8, 32, 16, 2048, 256) == ((32, 72, 32), (32, 72))
+    # head_dim 32: 4 waves per CU in 4-wave unit workgroups, 32 units per kv head
+    assert plan_workspace_shapes(8, 32, 8, 32, 16, 2048, 256) == ((32, 40, 32), (32, 40))
 
 
 def test_normalize_splits():
