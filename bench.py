@@ -521,6 +521,54 @@ def stats_summary(config, kt_dir, steps=200, warmup=20):
     log(f"wrote {out}")
 
 
+def write_stats_summary(config, kt_dir, line_path):
+    """Writes profiles/write_<config>_kernel_stats.txt from a rocprofv3 --kernel-trace
+    --stats run of `bench.py --config <config> --write-path` (kt_dir/kt_kernel_stats.csv)
+    and that run's JSON line (line_path): the write path's kernels, their calls and
+    average / min / max durations and share of the write-path GPU time, then the line."""
+    import csv
+    import glob
+    import json
+    B, ctx, pool, fmt_name, desc = CONFIGS[config]
+    path = glob.glob(os.path.join(kt_dir, "**", "*kernel_stats.csv"), recursive=True)[0]
+    rows = [r for r in csv.DictReader(open(path))
+            if "kvq::" in r["Name"] and ("quant" in r["Name"] or "append" in r["Name"])]
+    total = sum(float(r["TotalDurationNs"]) for r in rows)
+    line = json.loads(open(line_path).read().strip().splitlines()[-1])
+    lines = [
+        f"# rocprofv3 kernel-trace statistics, KV write path of {config}: {desc}",
+        f"# (block_size 16, Llama-3-8B GQA shape: {HKV} kv heads, head_dim {D}; K groups of "
+        "128 tokens)",
+        "# command:",
+        f"#   rocprofv3 --kernel-trace --stats -d D -o kt -f csv -- python3 bench.py --config "
+        f"{config} --write-path > LINE",
+        f"#   python3 bench.py --config {config} --write-stats-summary D --write-line LINE",
+        "# source: D/kt_kernel_stats.csv (kvq write-path kernels; the rest is input generation)",
+        "# calls = bulk: 20 warmup + 200 timed; append: 20 warmup + 200 timed eager + 200 in "
+        "the captured graph, replayed 1 + 3 times",
+        "",
+        f"{'kernel':50s}{'calls':>9s}{'avg_us':>10s}{'min_us':>10s}{'max_us':>10s}{'pct':>7s}",
+    ]
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
+        name = r["Name"].replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")
+        lines.append(f"{name[:50]:50s}{int(r['Calls']):>9d}{float(r['AverageNs']) / 1e3:>10.2f}"
+                     f"{float(r['MinNs']) / 1e3:>10.2f}{float(r['MaxNs']) / 1e3:>10.2f}"
+                     f"{100 * float(r['TotalDurationNs']) / total:>7.2f}")
+    keys = ("bulk_us", "bulk_bytes", "bulk_tb_s", "append_us_eager", "append_us_graph")
+    lines += ["", "bench.py --write-path line (HIP events; append_us_graph = GPU µs per one-token "
+              "append of the whole batch, from the captured graph; append_us_eager includes the "
+              "Python call):",
+              "  " + ", ".join(f"{k} = {line[k]}" for k in keys if k in line)]
+    if "bulk_bytes" in line:
+        lines.append("bulk bytes = fp16 K and V rows read + codes and (scale, zero) pairs "
+                     f"written; {line['bulk_bytes']} per call")
+    out = os.path.join(REPO, "profiles", f"write_{config}_kernel_stats.txt")
+    with open(out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    log("\n".join(lines))
+    log(f"wrote {out}")
+
+
 # Counter passes of --counter-summary: rocprofv3 collects a limited number of counters per
 # block in one run, so each pass is a run of its own (PMC_DIR/<pass>/).
 COUNTER_PASSES = {
@@ -927,6 +975,11 @@ def main():
     ap.add_argument("--stats-summary", metavar="KT_DIR",
                     help="write profiles/decode_<config>_kernel_stats.txt from a rocprofv3 "
                          "--kernel-trace --stats output directory")
+    ap.add_argument("--write-stats-summary", metavar="KT_DIR",
+                    help="write profiles/write_<config>_kernel_stats.txt from a rocprofv3 "
+                         "--kernel-trace --stats output directory of a --write-path run and "
+                         "its JSON line (--write-line)")
+    ap.add_argument("--write-line", metavar="FILE", help="the --write-path run's JSON line")
     ap.add_argument("--counter-summary", metavar="PMC_DIR",
                     help="write profiles/decode_<config>_counters.txt from PMC_DIR/{sq,tp,tc}")
     ap.add_argument("--traffic-summary", metavar="PMC_DIR",
@@ -947,6 +1000,9 @@ def main():
         return
     if args.stats_summary:
         stats_summary(args.config, args.stats_summary)
+        return
+    if args.write_stats_summary:
+        write_stats_summary(args.config, args.write_stats_summary, args.write_line)
         return
     if args.calibrate_copy:
         calibrate_copy()

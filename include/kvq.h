@@ -282,9 +282,13 @@ int kvq_quantize_cache(const kvq_decode_args* args, const void* k_src, const voi
 /* Quantize-on-append (no reference counterpart; KIVI write path). For each sequence b,
  * the token at position p = seq_lens[b] - 1 is new: k_new/v_new fp16 [batch, kv_heads,
  * head_dim] hold it. V is quantized per token into its slot immediately. K is written
- * to the fp16 residual k_resid [batch, kv_heads, k_group, head_dim] at row p % k_group,
- * and the group containing p is (re)quantized from the residual rows 0..p%k_group, so
- * the cache always equals kvq_quantize_cache of all tokens so far.
+ * to the fp16 residual k_resid [batch, kv_heads, k_group + 2, head_dim] at row p % k_group;
+ * rows k_group and k_group + 1 hold the per-channel min and max of the group's rows so far
+ * (the append keeps them; kvq_decode_amd.quant.init_k_residual fills all of it after a
+ * bulk quantization). The channels whose min or max the new row moves are re-encoded from
+ * the residual rows 0..p%k_group, the others keep their codes, so the cache always equals
+ * kvq_quantize_cache of all tokens so far. Appends are sequential per sequence: position
+ * p follows p - 1 (or the bulk quantization and init_k_residual).
  * args->seq_lens must already count the new token. A sequence whose seq_lens[b] is below
  * 1 or above max_blocks * block_size writes nothing (codes, pairs and residual), and a
  * row whose block-table entry lies outside [0, num_blocks) is not written (a K group

@@ -109,7 +109,8 @@ struct QuantParams {
     const int32_t* seq_lens;
     const _Float16* k_new;   // append only: [batch, kv_heads, head_dim]
     const _Float16* v_new;
-    _Float16* k_resid;       // append only: [batch, kv_heads, k_group, head_dim]
+    _Float16* k_resid;       // append only: [batch, kv_heads, k_group + 2, head_dim]: the
+                             // open K group's rows, then their per-channel min and max
     int32_t batch, kv_heads, head_dim, block_size, max_blocks, num_blocks, k_group;
     int32_t bs_shift;        // log2(block_size) (a power of two)
     int32_t vg_shift;        // log2 of tokens per V (scale, zero) group, max(block_size, 32)

@@ -133,48 +133,46 @@ __device__ __forceinline__ void store8(uint8_t* row, int c, const uint32_t* code
     }
 }
 
+// Codes of one row's 8 channels 8c .. 8c + 7 under (scale, zero) q, into the row's page
+// slot (phys: its block).
+template <int FMT>
+__device__ __forceinline__ void emit_k_row(const QuantParams& p, int kvh, int c, int t,
+                                           int phys, h8q v, const ScaleZero* q) {
+    float x[8];
+    to_float8(v, x);
+    uint32_t code[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) code[e] = encode<FMT>(x[e], q[e]);
+    store8<FMT>(p.k_codes + (int64_t)phys * p.k_sblk + (int64_t)(t & (p.block_size - 1)) * p.k_stok +
+                    (int64_t)kvh * p.k_sh,
+                c, code);
+}
+
 // K: workgroup = (kv head, group, sequence), 256 threads. Lane (c, slice) owns channels
 // 8c .. 8c + 7 (16-byte loads; D/8 lanes per row) of the group's rows t0 + slice,
 // t0 + slice + RS, ... (RS = 2048 / D row slices). Pass 1 reduces min / max over each
 // slice and then across the slices through LDS, keeping the slice's first 8 rows in
 // registers; pass 2 encodes them (re-reading rows past the 8th) with the group's (scale,
 // zero). Codes go to each token's page slot, the pairs to the group's first block.
-// Append: the group holding the newest token, read from the fp16 residual except the new
-// row itself (from k_new), which also joins the residual for later appends.
-// Rows whose page lies outside the pool are not written (bulk: not read either, so they
-// do not enter the group's min / max); a group whose first page lies outside the pool
-// writes nothing. An append whose length has no slot (append_len_of) writes nothing, the
-// residual included.
-template <int FMT, int D, bool APPEND>
+// Rows whose page lies outside the pool are neither read nor written, so they do not
+// enter the group's min / max; a group whose first page lies outside the pool writes
+// nothing.
+template <int FMT, int D>
 __device__ __forceinline__ void quant_k_group(const QuantParams& p, int kvh, int grp, int b) {
     constexpr int LPR = D / 8, RS = 256 / LPR, CACHE = 8;
     const int c = threadIdx.x % LPR, rs = threadIdx.x / LPR;
-    const int n = APPEND ? append_len_of(p, b) : seq_len_of(p, b);
-    int t0 = grp * p.k_group, t1 = min(t0 + p.k_group, n);
-    if (APPEND) {  // only the group holding the newest token, rows 0..(n-1) % k_group
-        if (n < 1) return;
-        t0 = ((n - 1) / p.k_group) * p.k_group;
-        t1 = n;
-    }
+    const int n = seq_len_of(p, b);
+    const int t0 = grp * p.k_group, t1 = min(t0 + p.k_group, n);
     if (t0 >= t1) return;  // uniform over the workgroup
     // the group's (scale, zero) pairs live in its first page: without it the group's codes
     // could not be read back, so a group whose first page is outside the pool writes nothing
     const int lead = phys_of(p, b, t0 >> p.bs_shift);
     if (lead < 0) return;
-    const int64_t resid = ((int64_t)b * p.kv_heads + kvh) * p.k_group * D + 8 * c;
-    const _Float16* kn = p.k_new + ((int64_t)b * p.kv_heads + kvh) * D + 8 * c;
-    if (APPEND && rs == 0)  // the new token's K joins the fp16 residual of its group
-        *(h8q*)(p.k_resid + resid + (int64_t)(t1 - 1 - t0) * D) = *(const h8q*)kn;
-    // row t of the group, from the page `phys` holding it (bulk) or the residual (append)
+    // row t of the group, from the page `phys` holding it
     auto load = [&](int t, int phys) -> h8q {
-        const _Float16* src;
-        if (APPEND) {
-            src = t == t1 - 1 ? kn : p.k_resid + resid + (int64_t)(t - t0) * D;
-        } else {
-            src = p.k_src + (int64_t)phys * p.s_sblk + (int64_t)(t & (p.block_size - 1)) * p.s_stok +
-                  (int64_t)kvh * p.s_sh + 8 * c;
-        }
-        return *(const h8q*)src;
+        return *(const h8q*)(p.k_src + (int64_t)phys * p.s_sblk +
+                             (int64_t)(t & (p.block_size - 1)) * p.s_stok + (int64_t)kvh * p.s_sh +
+                             8 * c);
     };
     float mn[8], mx[8];
 #pragma unroll
@@ -199,7 +197,7 @@ __device__ __forceinline__ void quant_k_group(const QuantParams& p, int kvh, int
         cphys[i] = -1;
         if (t < t1) {
             cphys[i] = phys_of(p, b, t >> p.bs_shift);
-            if (APPEND || cphys[i] >= 0) {  // append rows come from the residual
+            if (cphys[i] >= 0) {
                 cache[i] = load(t, cphys[i]);
                 reduce(cache[i]);
             }
@@ -207,7 +205,7 @@ __device__ __forceinline__ void quant_k_group(const QuantParams& p, int kvh, int
     }
     for (int t = t0 + rs + CACHE * RS; t < t1; t += RS) {
         const int phys = phys_of(p, b, t >> p.bs_shift);
-        if (APPEND || phys >= 0) reduce(load(t, phys));
+        if (phys >= 0) reduce(load(t, phys));
     }
 
     __shared__ float4 part[256][4];  // per thread: min 0-3, min 4-7, max 0-3, max 4-7
@@ -249,16 +247,7 @@ __device__ __forceinline__ void quant_k_group(const QuantParams& p, int kvh, int
         const float2 pr = params[8 * c + e];
         q[e] = ScaleZero{pr.x, pr.y, pr.x == 0.f ? 0.f : __fdiv_rn(1.f, pr.x)};
     }
-    auto emit = [&](int t, int phys, h8q v) {
-        float x[8];
-        to_float8(v, x);
-        uint32_t code[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) code[e] = encode<FMT>(x[e], q[e]);
-        store8<FMT>(p.k_codes + (int64_t)phys * p.k_sblk + (int64_t)(t & (p.block_size - 1)) * p.k_stok +
-                        (int64_t)kvh * p.k_sh,
-                    c, code);
-    };
+    auto emit = [&](int t, int phys, h8q v) { emit_k_row<FMT>(p, kvh, c, t, phys, v, q); };
 #pragma unroll
     for (int i = 0; i < CACHE; ++i) {
         const int t = t0 + rs + i * RS;
@@ -340,11 +329,96 @@ __device__ __forceinline__ void quant_v_rows(const QuantParams& p, int kvh, int 
     }
 }
 
+// Append, K: the group holding the newest token (position n - 1, row r = (n - 1) % k_group
+// of the group that starts at t0). The residual [B][Hkv][k_group + 2][D] keeps the
+// group's fp16 rows and, in rows k_group and k_group + 1, their running per-channel min
+// and max (exact in fp16: min / max of fp16 values). Lane (c, slice) of the 256-thread
+// workgroup owns channels 8c .. 8c + 7; every lane loads the new row and its channels'
+// stored min / max together with the sequence length (none of them depends on it), so
+// the group's new (scale, zero) pairs are known one memory round trip in (r == 0 starts the
+// group from the new row alone). The new row is encoded with them. The group's earlier
+// rows are re-encoded only in the 8-channel slices whose min or max moved (a code depends
+// on its row and its channel's pair only), by the slice's 2048 / D lanes; in a full
+// 128-token group a new token moves about 2 of 128 channels' ranges. The slice's first lane
+// writes the pairs (when they moved), the min / max rows and the new residual row. A group
+// whose first page lies outside the pool writes nothing; rows whose page lies outside are
+// not written. Appends are sequential: the residual holds rows 0 .. r - 1 of the group and
+// their min / max (from the appends of positions t0 .. n - 2, or from init_k_residual).
+template <int FMT, int D>
+__device__ __forceinline__ void quant_k_append(const QuantParams& p, int kvh, int b) {
+    constexpr int LPR = D / 8, RS = 256 / LPR, CACHE = 8;
+    const int c = threadIdx.x % LPR, rs = threadIdx.x / LPR;
+    const int64_t head = (int64_t)b * p.kv_heads + kvh;
+    _Float16* res = p.k_resid + head * (p.k_group + 2) * D + 8 * c;  // row 0, this lane's channels
+    const h8q kn = *(const h8q*)(p.k_new + head * D + 8 * c);
+    const h8q smn = *(const h8q*)(res + (int64_t)p.k_group * D);
+    const h8q smx = *(const h8q*)(res + (int64_t)(p.k_group + 1) * D);
+    const int n = append_len_of(p, b);
+    if (n < 1) return;
+    const int t0 = ((n - 1) / p.k_group) * p.k_group, r = n - 1 - t0;
+    const int lead = phys_of(p, b, t0 >> p.bs_shift);
+    if (lead < 0) return;  // uniform over the workgroup
+    const int phys_new = phys_of(p, b, (n - 1) >> p.bs_shift);
+    float x[8], mn[8], mx[8];
+    to_float8(kn, x);
+    bool moved = r == 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float omn = r == 0 ? INFINITY : (float)smn[e];
+        const float omx = r == 0 ? -INFINITY : (float)smx[e];
+        mn[e] = fminf(omn, x[e]);
+        mx[e] = fmaxf(omx, x[e]);
+        moved = moved || mn[e] != omn || mx[e] != omx;
+    }
+    ScaleZero q[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q[e] = make_params<FMT>(mn[e], mx[e]);
+    if (moved) {  // re-encode rows 0 .. r - 1 of these channels: lane slice rs takes rows rs + k RS
+        for (int base = 0; base < r; base += RS * CACHE) {
+            h8q rows[CACHE];
+            int ph[CACHE];
+#pragma unroll
+            for (int i = 0; i < CACHE; ++i) {  // loads first, at clamped rows (r >= 1 here)
+                const int t = min(base + rs + i * RS, r - 1);
+                ph[i] = phys_of(p, b, (t0 + t) >> p.bs_shift);
+                rows[i] = *(const h8q*)(res + (int64_t)t * D);
+            }
+#pragma unroll
+            for (int i = 0; i < CACHE; ++i) {
+                const int t = base + rs + i * RS;
+                if (t < r && ph[i] >= 0) emit_k_row<FMT>(p, kvh, c, t0 + t, ph[i], rows[i], q);
+            }
+        }
+    }
+    if (rs == 0) {
+        if (phys_new >= 0) emit_k_row<FMT>(p, kvh, c, n - 1, phys_new, kn, q);
+        h8q nmn, nmx;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            nmn[e] = (_Float16)mn[e];
+            nmx[e] = (_Float16)mx[e];
+        }
+        *(h8q*)(res + (int64_t)r * D) = kn;
+        *(h8q*)(res + (int64_t)p.k_group * D) = nmn;
+        *(h8q*)(res + (int64_t)(p.k_group + 1) * D) = nmx;
+        if (moved) {  // (scale, zero) pairs of channels 8c .. 8c + 7, in the group's first page
+            h8q pairs[2];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                pairs[e / 4][2 * (e % 4)] = (_Float16)q[e].s;
+                pairs[e / 4][2 * (e % 4) + 1] = (_Float16)q[e].z;
+            }
+            const int64_t sz = ((int64_t)lead * p.kv_heads + kvh) * D + 8 * c;
+            *(h8q*)(p.k_scale + 2 * sz) = pairs[0];
+            *(h8q*)(p.k_scale + 2 * sz + 8) = pairs[1];
+        }
+    }
+}
+
 template <int FMT, int D>
 __global__ __launch_bounds__(256) void quant_k_kernel(const QuantParams p) {
     // grid (kv_heads * groups, batch): the groups of a sequence need no 16-bit grid axis
-    quant_k_group<FMT, D, false>(p, blockIdx.x % p.kv_heads, blockIdx.x / p.kv_heads,
-                                 blockIdx.y);
+    quant_k_group<FMT, D>(p, blockIdx.x % p.kv_heads, blockIdx.x / p.kv_heads, blockIdx.y);
 }
 
 template <int FMT, int D>
@@ -360,7 +434,7 @@ __global__ __launch_bounds__(256) void quant_v_kernel(const QuantParams p) {
 template <int FMT, int D>
 __global__ __launch_bounds__(256) void quant_append_kernel(const QuantParams p) {
     if (blockIdx.y == 0) {
-        quant_k_group<FMT, D, true>(p, blockIdx.x, 0, blockIdx.z);
+        quant_k_append<FMT, D>(p, blockIdx.x, blockIdx.z);
     } else if (threadIdx.x < D / 8) {
         quant_v_rows<FMT, D, true>(p, blockIdx.x, 0, blockIdx.z);
     }

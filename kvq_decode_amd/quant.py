@@ -186,12 +186,14 @@ def quantize_paged_cache(k_cache: torch.Tensor, v_cache: torch.Tensor,
 
 def init_k_residual(k_cache: torch.Tensor, block_table: torch.Tensor, seq_lens: torch.Tensor,
                     k_group: int = DEFAULT_K_GROUP) -> torch.Tensor:
-    """fp16 residual [B, Hkv, k_group, D] holding, for each sequence, the K rows of its
-    open (last, incomplete) group - what quantize_append needs after a bulk prefill.
-    Rows of a complete last group are zero (the next token opens a new group)."""
+    """fp16 residual [B, Hkv, k_group + 2, D] holding, for each sequence, the K rows of its
+    open (last, incomplete) group in rows 0 .. k_group - 1 and their per-channel min and max
+    in rows k_group and k_group + 1 - what quantize_append needs after a bulk prefill. Rows
+    of a complete last group are zero (the next token opens a new group, which ignores
+    them)."""
     B = block_table.shape[0]
     nb, bs, hkv, d = k_cache.shape
-    resid = torch.zeros((B, hkv, k_group, d), dtype=torch.float16, device=k_cache.device)
+    resid = torch.zeros((B, hkv, k_group + 2, d), dtype=torch.float16, device=k_cache.device)
     lens = seq_lens.tolist()
     for b, n in enumerate(lens):
         t0 = (n // k_group) * k_group
@@ -199,7 +201,10 @@ def init_k_residual(k_cache: torch.Tensor, block_table: torch.Tensor, seq_lens: 
             continue
         t = torch.arange(t0, n, device=k_cache.device)
         phys = block_table[b, t // bs].long()
-        resid[b, :, : n - t0] = k_cache[phys, t % bs].permute(1, 0, 2)
+        rows = k_cache[phys, t % bs].permute(1, 0, 2)  # [Hkv, n - t0, D]
+        resid[b, :, : n - t0] = rows
+        resid[b, :, k_group] = rows.amin(dim=1)
+        resid[b, :, k_group + 1] = rows.amax(dim=1)
     return resid
 
 
@@ -210,8 +215,10 @@ def quantize_append(cache: QuantizedKVCache, k_new: torch.Tensor, v_new: torch.T
 
     seq_lens must already count the new token: the token is at position seq_lens[b] - 1.
     k_new / v_new: fp16 [B, Hkv, D]. V is quantized per token into its slot. K joins the
-    fp16 residual k_resid [B, Hkv, k_group, D] of its group, and the group is re-quantized
-    from the residual, so the cache always equals quantize_paged_cache of all tokens."""
+    fp16 residual k_resid [B, Hkv, k_group + 2, D] of its group (init_k_residual: the rows,
+    then their running per-channel min and max), and the group's channels whose range moved
+    are re-encoded from it, so the cache always equals quantize_paged_cache of all tokens.
+    Appends are sequential per sequence (each one's position follows the last)."""
     _require(k_new.dim() == 3, "k_new must be [B, kv_heads, head_dim]")
     B, hkv, d = k_new.shape
     _check_cache(cache, block_table, seq_lens, d)
@@ -220,7 +227,7 @@ def quantize_append(cache: QuantizedKVCache, k_new: torch.Tensor, v_new: torch.T
     _require(cache.k_codes.shape[2] == hkv,
              f"the cache has {cache.k_codes.shape[2]} kv heads, k_new {hkv}")
     for name, t, shape in (("k_new", k_new, (B, hkv, d)), ("v_new", v_new, (B, hkv, d)),
-                           ("k_resid", k_resid, (B, hkv, cache.k_group, d))):
+                           ("k_resid", k_resid, (B, hkv, cache.k_group + 2, d))):
         _require(t.dtype == torch.float16 and tuple(t.shape) == shape and t.is_contiguous(),
                  f"{name} must be contiguous fp16 of shape {shape}")
     _check_devices(cache.k_codes.device, k_new=k_new, v_new=v_new, k_resid=k_resid)
