@@ -148,22 +148,23 @@ __device__ __forceinline__ void emit_k_row(const QuantParams& p, int kvh, int c,
                 c, code);
 }
 
-// K: workgroup = (kv head, group, sequence), 256 threads. Lane (c, slice) owns channels
-// 8c .. 8c + 7 (16-byte loads; D/8 lanes per row) of the group's rows t0 + slice,
-// t0 + slice + RS, ... (RS = 2048 / D row slices). Pass 1 reduces min / max over each
-// slice and then across the slices through LDS, keeping the slice's first 8 rows in
-// registers; pass 2 encodes them (re-reading rows past the 8th) with the group's (scale,
-// zero). Codes go to each token's page slot, the pairs to the group's first block.
-// Rows whose page lies outside the pool are neither read nor written, so they do not
-// enter the group's min / max; a group whose first page lies outside the pool writes
-// nothing.
+// K, bulk: one wave per (kv head, group, sequence), four groups per 256-thread workgroup.
+// Lane l owns channels 8c .. 8c + 7 (c = l % PC, PC = D/8 lanes per row: 16-byte loads) of
+// rows t0 + RPI j + l / PC (RPI = 64/PC rows per load instruction). Min / max run over the
+// lane's rows in registers, then across the RPI row groups of a channel by lane exchanges:
+// no LDS and no barrier. The lane's first KC rows stay in registers between the min / max
+// pass and the encode pass (every row of a 128-token group at head dims up to 128); longer
+// groups re-read the rest. Codes go to each token's page slot, the pairs to the group's
+// first block. Rows whose page lies outside the pool are neither read nor written, so they
+// do not enter the group's min / max; a group whose first page lies outside the pool
+// writes nothing.
 template <int FMT, int D>
 __device__ __forceinline__ void quant_k_group(const QuantParams& p, int kvh, int grp, int b) {
-    constexpr int LPR = D / 8, RS = 256 / LPR, CACHE = 8;
-    const int c = threadIdx.x % LPR, rs = threadIdx.x / LPR;
+    constexpr int PC = D / 8, RPI = 64 / PC, KC = D == 256 ? 16 : 32;
+    const int lane = threadIdx.x & 63, c = lane % PC, ri = lane / PC;
     const int n = seq_len_of(p, b);
     const int t0 = grp * p.k_group, t1 = min(t0 + p.k_group, n);
-    if (t0 >= t1) return;  // uniform over the workgroup
+    if (t0 >= t1) return;  // uniform over the wave
     // the group's (scale, zero) pairs live in its first page: without it the group's codes
     // could not be read back, so a group whose first page is outside the pool writes nothing
     const int lead = phys_of(p, b, t0 >> p.bs_shift);
@@ -189,73 +190,53 @@ __device__ __forceinline__ void quant_k_group(const QuantParams& p, int kvh, int
             mx[e] = fmaxf(mx[e], x[e]);
         }
     };
-    h8q cache[CACHE];
-    int cphys[CACHE];  // the cached rows' pages (-1: outside the pool), for pass 2
+    h8q cache[KC];
+    int cphys[KC];  // the cached rows' pages (-1: outside the pool or past the group)
 #pragma unroll
-    for (int i = 0; i < CACHE; ++i) {
-        const int t = t0 + rs + i * RS;
-        cphys[i] = -1;
-        if (t < t1) {
-            cphys[i] = phys_of(p, b, t >> p.bs_shift);
-            if (cphys[i] >= 0) {
-                cache[i] = load(t, cphys[i]);
-                reduce(cache[i]);
-            }
-        }
+    for (int i = 0; i < KC; ++i) {  // every load issued, at rows inside the pool
+        const int t = t0 + ri + i * RPI;
+        const int ph = phys_of(p, b, min(t, t1 - 1) >> p.bs_shift);
+        cphys[i] = t < t1 ? ph : -1;
+        cache[i] = load(min(t, t1 - 1), ph >= 0 ? ph : lead);
     }
-    for (int t = t0 + rs + CACHE * RS; t < t1; t += RS) {
+#pragma unroll
+    for (int i = 0; i < KC; ++i)
+        if (cphys[i] >= 0) reduce(cache[i]);
+    for (int t = t0 + ri + KC * RPI; t < t1; t += RPI) {
         const int phys = phys_of(p, b, t >> p.bs_shift);
         if (phys >= 0) reduce(load(t, phys));
     }
-
-    __shared__ float4 part[256][4];  // per thread: min 0-3, min 4-7, max 0-3, max 4-7
-    __shared__ float2 params[D];     // per channel: (scale, zero)
-    part[threadIdx.x][0] = make_float4(mn[0], mn[1], mn[2], mn[3]);
-    part[threadIdx.x][1] = make_float4(mn[4], mn[5], mn[6], mn[7]);
-    part[threadIdx.x][2] = make_float4(mx[0], mx[1], mx[2], mx[3]);
-    part[threadIdx.x][3] = make_float4(mx[4], mx[5], mx[6], mx[7]);
-    __syncthreads();
-    if (rs == 0) {
-        for (int k = 1; k < RS; ++k) {
-            const float4* o = part[k * LPR + c];
-            const float om[8] = {o[0].x, o[0].y, o[0].z, o[0].w, o[1].x, o[1].y, o[1].z, o[1].w};
-            const float oM[8] = {o[2].x, o[2].y, o[2].z, o[2].w, o[3].x, o[3].y, o[3].z, o[3].w};
+    // the channel's RPI row groups: lanes c, c + PC, c + 2 PC, ...
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                mn[e] = fminf(mn[e], om[e]);
-                mx[e] = fmaxf(mx[e], oM[e]);
-            }
+    for (int o = PC; o < 64; o <<= 1) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            mn[e] = fminf(mn[e], __shfl_xor(mn[e], o));
+            mx[e] = fmaxf(mx[e], __shfl_xor(mx[e], o));
         }
+    }
+    ScaleZero q[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q[e] = make_params<FMT>(mn[e], mx[e]);
+    if (ri == 0) {
         // (scale, zero) pairs of channels 8c .. 8c + 7: two 16-byte stores into the lead
         // page, which also holds row t0, so min / max saw at least that row
         h8q pairs[2];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const ScaleZero q = make_params<FMT>(mn[e], mx[e]);
-            params[8 * c + e] = make_float2(q.s, q.z);
-            pairs[e / 4][2 * (e % 4)] = (_Float16)q.s;
-            pairs[e / 4][2 * (e % 4) + 1] = (_Float16)q.z;
+            pairs[e / 4][2 * (e % 4)] = (_Float16)q[e].s;
+            pairs[e / 4][2 * (e % 4) + 1] = (_Float16)q[e].z;
         }
         const int64_t sz = ((int64_t)lead * p.kv_heads + kvh) * D + 8 * c;
         *(h8q*)(p.k_scale + 2 * sz) = pairs[0];
         *(h8q*)(p.k_scale + 2 * sz + 8) = pairs[1];
     }
-    __syncthreads();
-    ScaleZero q[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const float2 pr = params[8 * c + e];
-        q[e] = ScaleZero{pr.x, pr.y, pr.x == 0.f ? 0.f : __fdiv_rn(1.f, pr.x)};
-    }
-    auto emit = [&](int t, int phys, h8q v) { emit_k_row<FMT>(p, kvh, c, t, phys, v, q); };
-#pragma unroll
-    for (int i = 0; i < CACHE; ++i) {
-        const int t = t0 + rs + i * RS;
-        if (t < t1 && cphys[i] >= 0) emit(t, cphys[i], cache[i]);
-    }
-    for (int t = t0 + rs + CACHE * RS; t < t1; t += RS) {
+    for (int i = 0; i < KC; ++i)
+        if (cphys[i] >= 0) emit_k_row<FMT>(p, kvh, c, t0 + ri + i * RPI, cphys[i], cache[i], q);
+    for (int t = t0 + ri + KC * RPI; t < t1; t += RPI) {
         const int phys = phys_of(p, b, t >> p.bs_shift);
-        if (phys >= 0) emit(t, phys, load(t, phys));
+        if (phys >= 0) emit_k_row<FMT>(p, kvh, c, t, phys, load(t, phys), q);
     }
 }
 
@@ -417,8 +398,11 @@ __device__ __forceinline__ void quant_k_append(const QuantParams& p, int kvh, in
 
 template <int FMT, int D>
 __global__ __launch_bounds__(256) void quant_k_kernel(const QuantParams p) {
-    // grid (kv_heads * groups, batch): the groups of a sequence need no 16-bit grid axis
-    quant_k_group<FMT, D>(p, blockIdx.x % p.kv_heads, blockIdx.x / p.kv_heads, blockIdx.y);
+    // grid (kv_heads * cdiv(groups, 4), batch): the groups of a sequence need no 16-bit grid
+    // axis; wave w takes group 4 x + w (groups past the sequence return at once)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    quant_k_group<FMT, D>(p, blockIdx.x % p.kv_heads, 4 * (blockIdx.x / p.kv_heads) + wave,
+                          blockIdx.y);
 }
 
 template <int FMT, int D>
@@ -447,8 +431,9 @@ hipError_t launch_fmt_d(const QuantParams& p, hipStream_t stream) {
                            dim3(256), 0, stream, p);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL((quant_k_kernel<FMT, D>), dim3(p.kv_heads * p.max_groups, p.batch),
-                       dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((quant_k_kernel<FMT, D>),
+                       dim3(p.kv_heads * ((p.max_groups + 3) / 4), p.batch), dim3(256), 0,
+                       stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int tiles = (int)(((int64_t)p.max_blocks * p.block_size + kVRows - 1) / kVRows);
