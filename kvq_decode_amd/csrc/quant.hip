@@ -444,8 +444,7 @@ hipError_t launch_fmt_d(const QuantParams& p, hipStream_t stream) {
 
 template <int FMT, bool APPEND>
 hipError_t launch_fmt(const QuantParams& p, hipStream_t stream) {
-    switch (p.head_dim) {
-        case 32: return launch_fmt_d<FMT, 32, APPEND>(p, stream);
+    switch (p.head_dim) {  // the quantized formats' head dims (decode reads these)
         case 64: return launch_fmt_d<FMT, 64, APPEND>(p, stream);
         case 128: return launch_fmt_d<FMT, 128, APPEND>(p, stream);
         case 256: return launch_fmt_d<FMT, 256, APPEND>(p, stream);
