@@ -229,14 +229,7 @@ def time_stage1(step, iters, blocks=STAGE1_BLOCKS):
     import statistics
 
     import torch
-    # spin the clock up first: at least SPIN_UP_S of back-to-back launches (MI355X takes
-    # tens of ms of sustained load to reach its steady clock after idle, and after the CPU
-    # work of building a quantized config's inputs 50 ms was not always enough)
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < SPIN_UP_S:
-        for _ in range(10):
-            step.stage1()
-        torch.cuda.synchronize()
+    spin_up(step)
     runs = []
     for _ in range(blocks):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -251,6 +244,19 @@ def time_stage1(step, iters, blocks=STAGE1_BLOCKS):
 
 FLUSH_SAMPLES = 60
 SPIN_UP_S = 0.3
+
+
+def spin_up(step):
+    """At least SPIN_UP_S of back-to-back stage-1 launches. MI355X takes tens of ms of
+    sustained load to reach its steady clock after idle (after the CPU work of building a
+    quantized config's inputs 50 ms was not always enough); the short host waits of the
+    flushed steps do not let it fall again."""
+    import torch
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < SPIN_UP_S:
+        for _ in range(10):
+            step.stage1()
+        torch.cuda.synchronize()
 
 
 def time_flushed(step, iters=FLUSH_SAMPLES):
@@ -694,12 +700,15 @@ def run_config(config, steps, warmup, splits=None, waves=0, pipeline=0, flushed=
     step = Step(q, k, v, bt, sl, splits, waves, pipeline, fmt, units)
     nbytes = kv_bytes(lens, fmt_name)
     log(f"{config}: {desc}; {plan_text(step)} pages/split={step.pps} KV bytes/step={nbytes}")
-    # The flushed steps first (each waits on the host, so the GPU idles between them),
-    # then the kernel-level figures, the headline steps last: MI355X raises its clock over
-    # the first tens of ms of sustained load after idle (measured: C2 steps 169 us in the
-    # first 20 ms of a process, 159 us after), so the timed steps follow the stage-1 runs'
-    # sustained load and run at the steady clock of a serving GPU rather than during the
-    # ramp. They are still exactly `warmup` untimed and `steps` timed steps.
+    # Every figure is taken at the steady clock of a serving GPU, not during the ramp:
+    # MI355X raises its clock over the first tens of ms of sustained load after idle
+    # (measured: C2 steps 169 us in the first 20 ms of a process, 159 us after; flushed
+    # medians taken during the ramp read B16 fp16 at 333 us, 316 us after a spin-up). So
+    # the clock is spun up, then come the flushed steps (each waits on the host, so the
+    # GPU idles briefly between them), the kernel-level figures (spun up again) and the
+    # headline steps last, which are still exactly `warmup` untimed and `steps` timed steps.
+    if flushed:
+        spin_up(step)
     flushed_ms = time_flushed(step) if flushed else None
     stage1_iters = max(20, min(steps, 100))
     stage1_ms = time_stage1(step, stage1_iters)
@@ -727,7 +736,7 @@ def run_config(config, steps, warmup, splits=None, waves=0, pipeline=0, flushed=
                      "kernel": f"{kernel} (stage 1)", "kernel_us": round(stage1_ms * 1e3, 2)},
         # what runs before the `warmup` untimed and `steps` timed steps, in this order
         "pre_timing": {"flushed_steps": FLUSH_SAMPLES if flushed else 0,
-                       "spin_up_ms": round(SPIN_UP_S * 1e3),
+                       "spin_up_ms": round(SPIN_UP_S * 1e3) * (2 if flushed else 1),
                        "stage1_launches": STAGE1_BLOCKS * stage1_iters},
     }
     return res, (q, k, v, bt, sl)
