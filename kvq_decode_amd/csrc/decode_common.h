@@ -251,11 +251,19 @@ struct UnitSpace {
 };
 
 // First chunk of unit u, and the unit holding chunk x (the largest u with lo(u) <= x).
+// The products take 64 bits, but they fit in 32 for all but the largest partitions (u N <
+// 2^32), and the 32-bit quotient (a short float-reciprocal sequence) is taken then: the
+// 64-bit one is a long software routine that the kernels' start would wait on. The
+// branch is uniform (u, x and the partition are the same for the whole workgroup).
 __device__ __forceinline__ int unit_lo(UnitSpace us, int u) {
-    return (int)((int64_t)u * us.N / us.NU);
+    const uint64_t n = (uint64_t)(uint32_t)u * (uint32_t)us.N;
+    if ((n >> 32) == 0) return (int)((uint32_t)n / (uint32_t)us.NU);
+    return (int)(n / (uint32_t)us.NU);
 }
 __device__ __forceinline__ int unit_of(UnitSpace us, int64_t x) {
-    return (int)(((x + 1) * us.NU + us.N - 1) / us.N - 1);
+    const uint64_t n = (uint64_t)(x + 1) * (uint32_t)us.NU + (uint32_t)(us.N - 1);
+    if ((n >> 32) == 0) return (int)((uint32_t)n / (uint32_t)us.N) - 1;
+    return (int)(n / (uint32_t)us.N) - 1;
 }
 
 __device__ __forceinline__ int wave_sum(int x) {
@@ -367,8 +375,22 @@ __device__ __forceinline__ SegGuess unit_guess(const DecodeParams& p, int u, int
 // Workgroup order: plain (kv head fastest), or with xcd_group and units a multiple of
 // kXcds, grouped so that the kv heads of one unit share an XCD (workgroup i runs on XCD
 // i % kXcds) and with it the L2 lines of the V scales, which interleave kv heads.
+// Makes the kernel arguments the start of a work-unit kernel reads available in SGPRs at
+// this point. The compiler otherwise issues each argument load in the block that first
+// uses it, and the start then waits on several dependent scalar-load round trips before
+// its first memory access; loaded together they take one. (An empty asm statement with
+// SGPR inputs: it emits no instruction.)
+__device__ __forceinline__ void load_unit_args(const DecodeParams& p) {
+    asm volatile("" ::"s"(p.q), "s"(p.q_sb), "s"(p.q_sh), "s"(p.bt), "s"(p.bt_sb),
+                 "s"(p.seq_lens));
+    asm volatile("" ::"s"(p.batch), "s"(p.kv_heads), "s"(p.group), "s"(p.block_size),
+                 "s"(p.max_blocks), "s"(p.xcd_group), "s"(p.units), "s"(p.kv_rep),
+                 "s"(p.cpp_shift));
+}
+
 template <int W, typename Pre, typename Fn>
 __device__ __forceinline__ void for_unit_segments(const DecodeParams& p, Pre&& pre, Fn&& fn) {
+    load_unit_args(p);
     __shared__ UnitLds s;
     int kvh, u;
     if (p.xcd_group && p.units % kXcds == 0) {

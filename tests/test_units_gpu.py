@@ -105,6 +105,41 @@ def test_units_workspace_and_limits():
         paged_decode_attention(q2, kc2, vc2, bt2, sl2, units=8)
 
 
+def test_units_partition_past_32_bit_products():
+    """65537 units over 65537 chunks (two sequences of about 512k tokens): the unit bounds
+    u N / NU and the merge's unit lookups pass 2^32 for the upper units, where the kernels
+    leave their 32-bit arithmetic for 64-bit. Held to the split plan's result (the split
+    and unit paths are each checked against the oracle above)."""
+    from kvq_decode_amd import paged_decode_attention
+    g = torch.Generator(device="cuda").manual_seed(11)
+    lens = [524288, 524304]  # 32768 + 32769 chunks
+    Hq, Hkv, D, BS = 4, 1, 64, 16
+    pages = [(n + BS - 1) // BS for n in lens]
+    pool = sum(pages)
+    q = torch.randn(2, Hq, D, generator=g, device="cuda").half()
+    kc = torch.randn(pool, BS, Hkv, D, generator=g, device="cuda").half()
+    vc = torch.randn(pool, BS, Hkv, D, generator=g, device="cuda").half()
+    perm = torch.randperm(pool, generator=g, device="cuda").int()
+    bt = torch.zeros(2, max(pages), dtype=torch.int32, device="cuda")
+    bt[0, :pages[0]] = perm[:pages[0]]
+    bt[1, :pages[1]] = perm[pages[0]:]
+    sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    n_chunks = sum((n + 15) // 16 for n in lens)
+    assert (n_chunks - 1) * n_chunks >= 1 << 32
+    print(f"\n[units={n_chunks} over {n_chunks} chunks]", flush=True)
+    big = paged_decode_attention(q, kc, vc, bt, sl, units=n_chunks)
+    small = paged_decode_attention(q, kc, vc, bt, sl, units=1000)
+    split = paged_decode_attention(q, kc, vc, bt, sl, num_splits=64)
+    torch.cuda.synchronize()
+    ref = split.float().cpu().numpy()
+    for name, out in (("units=65537", big), ("units=1000", small)):
+        o = out.float().cpu().numpy()
+        diff = np.abs(o - ref)
+        print(f"[{name} vs 64 splits] max_abs={diff.max():.3e}", flush=True)
+        assert np.isfinite(o).all()
+        assert diff.max() < 2e-3 and np.all(diff <= 2e-3 + 1e-2 * np.abs(ref))
+
+
 QFORMATS = ["int8", "fp8_e4m3", "int4"]
 
 
