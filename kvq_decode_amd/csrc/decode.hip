@@ -516,11 +516,13 @@ __device__ __forceinline__ void q_operand(const DecodeParams& p, const h8* qraw,
 
 // The first loads of a wave's range, issued ahead by the work units for their guessed
 // first segment (decode_common.h for_unit_segments) and not used there: the q rows of
-// sequence b and the raw block-table entries of the ring's first two fills for the range
-// [w_lo, last].
+// sequence b, the raw block-table entries of the ring's first two fills for the range
+// [w_lo, last], and the ring's first fill itself (chunks w_lo .. w_lo + PR - 1 at their
+// pages clamped into the pool, so a wrong guess reads valid memory and is not used).
 template <int D, int P>
 struct F16Pre {
     h8 qraw[ChunkF16<D>::KN];
+    ChunkF16<D> ring[f16_ring<D, P>()];
     int pg_cur, pg_nxt;
     int b, w_lo, last;
     bool live;
@@ -542,6 +544,15 @@ __device__ __forceinline__ F16Pre<D, P> f16_prefetch(const DecodeParams& p, int 
         load_q_raw<D>(p, kvh, gs.b, f.qraw);
         f.pg_cur = chunk_pages_raw<PR>(p, gs.b, min(f.w_lo, last0), last0, 0, 0);
         f.pg_nxt = chunk_pages_raw<PR>(p, gs.b, min(f.w_lo + PR, last0), last0, 0, 0);
+        const int lane = threadIdx.x & 63;
+        const F16LaneOff<D> lo = f16_lane_offsets<D>(p, lane & 15, lane >> 4, 15);
+        const int pg = clamp_page(p, f.pg_cur);
+#pragma unroll
+        for (int i = 0; i < PR; ++i) {
+            load_chunk_f16<D>(p, cache_head(p, kvh), min(f.w_lo + i, last0), lo,
+                              __builtin_amdgcn_readlane(pg, i), f.ring[i]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
     return f;
 }
@@ -614,20 +625,23 @@ __device__ __forceinline__ void f16_range(const DecodeParams& p, int kvh, int b,
         const int last = r_hi - 1;
         ChunkF16<D> ring[PR];
         int pg_cur, pg_nxt;
-        if (pre_b && pre.w_lo == w_lo && pre.last == last) {
+        if (pre_b && pre.w_lo == w_lo && pre.last == last) {  // the first fill is in flight
             pg_cur = clamp_page(p, pre.pg_cur);
             pg_nxt = clamp_page(p, pre.pg_nxt);
+#pragma unroll
+            for (int i = 0; i < PR; ++i) ring[i] = pre.ring[i];
         } else {
             pg_cur = chunk_pages<PR>(p, b, w_lo, last, 0, 0);
             pg_nxt = chunk_pages<PR>(p, b, w_lo + PR, last, 0, 0);
-        }
-        // Issued slot by slot: a slot's loads moved behind a later slot's would make the
-        // ring's waits (vmcnt counts the loads issued after the awaited one) drain it.
+            // Issued slot by slot: a slot's loads moved behind a later slot's would make
+            // the ring's waits (vmcnt counts the loads issued after the awaited one) drain
+            // it.
 #pragma unroll
-        for (int i = 0; i < PR; ++i) {
-            load_chunk_f16<D>(p, kvc, min(w_lo + i, last), lo,
-                              __builtin_amdgcn_readlane(pg_cur, i), ring[i]);
-            __builtin_amdgcn_sched_barrier(0);
+            for (int i = 0; i < PR; ++i) {
+                load_chunk_f16<D>(p, kvc, min(w_lo + i, last), lo,
+                                  __builtin_amdgcn_readlane(pg_cur, i), ring[i]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
         for (int c0 = w_lo; c0 < r_hi; c0 += PR) {
             pg_cur = pg_nxt;  // pages of chunks c0 + PR .. c0 + 2PR - 1

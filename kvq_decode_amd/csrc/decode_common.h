@@ -403,14 +403,17 @@ __device__ __forceinline__ void for_unit_segments(const DecodeParams& p, Pre&& p
     }
     const int t = threadIdx.x, B = p.batch, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const auto pf = pre(kvh, unit_guess<W>(p, u, wave));
     const int per = (B + 63) >> 6;
     const int cap = p.max_blocks * p.block_size, ng = cap >> 4;  // cap: a multiple of 16
+    // the lengths are loaded before the prefetch, which may wait on its own loads
     int raw[4];
-    bool uniform = false;
     if (per <= 4) {  // lane t: sequences per * t .. per * t + per - 1
 #pragma unroll
         for (int e = 0; e < 4; ++e) raw[e] = p.seq_lens[min(per * lane + e, B - 1)];
+    }
+    const auto pf = pre(kvh, unit_guess<W>(p, u, wave));
+    bool uniform = false;
+    if (per <= 4) {
         bool ok = true;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
