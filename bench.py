@@ -15,8 +15,10 @@ B * ctx * Hkv * 2 * D * 2 bytes for fp16.
 
 The default C2 line also carries, timed the same way (same steps and warmup, default
 plans), every other configuration of EXTRA_CONFIGS as <prefix>_* keys: the north star's
-targets (fp16 B1/64k >= 50% of the peak with the cache flushed, fp16 B8/16k >= 80%, INT4
->= 3x fewer µs per step than fp16 at B16/32k; collected under `targets`), the reference's
+targets (fp16 B1/64k >= 50% of the peak with the cache flushed, fp16 B8/16k >= 80% - the rate
+it sustains, timed over at least 200 steps as well, since the first launch's latency weighs
+about 1.5% on 20 of its 84 us steps - and INT4 >= 3x fewer µs per step than fp16 at B16/32k;
+collected under `targets`), the reference's
 published grid points (B8/16k, B32/16k, B8/64k) and BASELINE.json's C1 (its single pass), C3,
 C4 (INT8, FP8) and C5. --no-targets skips them. roofline.kernel_us is stage 1 timed over back-to-back
 stage-1 launches; `pre_timing` lists what runs before the warmup and timed steps.
@@ -1093,11 +1095,31 @@ def config_keys(prefix, res):
     }
 
 
+SUSTAINED_STEPS = 200
+
+
+def sustained_us_per_step(config, steps=SUSTAINED_STEPS, warmup=20):
+    """Wall µs per step of `steps` back-to-back steps of `config` (default plan) after the
+    clock spin-up: the rate a decode loop sustains, with the first launch's latency (about
+    20 us from the synchronize to the first kernel's start) spread over enough steps to
+    weigh under 0.2%."""
+    B, ctx, pool, fmt_name, desc = CONFIGS[config]
+    q, k, v, bt, sl, fmt = make_inputs(B, ctx, pool, kv_format=fmt_name)
+    splits, waves, units = default_plan(config, B, bt.shape[1])
+    step = Step(q, k, v, bt, sl, splits, waves, 0, fmt, units)
+    spin_up(step)
+    wall_ms, _ = time_steps(step, steps, warmup)
+    return wall_ms * 1e3
+
+
 def north_star_targets(steps, warmup):
     """Every configuration of EXTRA_CONFIGS, timed like the headline, as extra keys of the
     JSON line, plus `targets`: the north star's three target figures with their bars.
     B1/64k's target figure is the flushed median (its 268 MB of KV barely exceed the
-    Infinity Cache); B8/16k's is the back-to-back figure, like the headline's (537 MB)."""
+    Infinity Cache). B8/16k's is the rate the step sustains back to back (537 MB; "sustains
+    >= 80%"): with fewer than SUSTAINED_STEPS timed steps, the first launch's latency
+    weighs on its 84 us steps (about 1.5% at 20 steps), so it is also timed over
+    SUSTAINED_STEPS steps (`b8_16k_*_sustained`); the same-steps figure stays beside it."""
     import torch
     out, res = {}, {}
     for prefix, config in EXTRA_CONFIGS:
@@ -1105,6 +1127,14 @@ def north_star_targets(steps, warmup):
         torch.cuda.empty_cache()
         res[prefix] = r
         out.update(config_keys(prefix, r))
+    nbytes = res["b8_16k"]["config"]["kv_bytes_per_step"]
+    sus_us = (sustained_us_per_step("B8_16K") if steps < SUSTAINED_STEPS
+              else res["b8_16k"]["us_per_step"])
+    torch.cuda.empty_cache()
+    out["b8_16k_us_per_step_sustained"] = round(sus_us, 2)
+    out["b8_16k_pct_of_peak_sustained"] = round(100 * nbytes / (sus_us * 1e-6)
+                                                / (PEAK_GBPS * 1e9), 2)
+    out["b8_16k_sustained_steps"] = max(steps, SUSTAINED_STEPS)
     out["int4_speedup"] = round(res["b16_fp16"]["us_per_step"] / res["b16_int4"]["us_per_step"],
                                 3)
     out["int4_speedup_flushed"] = round(res["b16_fp16"]["us_per_step_flushed_median"]
@@ -1112,7 +1142,9 @@ def north_star_targets(steps, warmup):
     out["targets"] = {
         "b1_64k_pct_of_peak_flushed": {"value": out["b1_64k_pct_of_peak_flushed"],
                                        "bar": ">= 50"},
-        "b8_16k_pct_of_peak": {"value": out["b8_16k_pct_of_peak"], "bar": ">= 80"},
+        "b8_16k_pct_of_peak_sustained": {"value": out["b8_16k_pct_of_peak_sustained"],
+                                         "bar": ">= 80",
+                                         "same_steps_value": out["b8_16k_pct_of_peak"]},
         "int4_speedup": {"value": out["int4_speedup"], "bar": ">= 3"},
     }
     log("targets: " + "; ".join(f"{k} {v['value']} ({v['bar']})"
