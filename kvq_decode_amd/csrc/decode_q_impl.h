@@ -1027,6 +1027,17 @@ __device__ __forceinline__ void q2_range(const DecodeParams& p, int kvh, int b, 
     const int vgs = p.vg_shift - 4;
     const QBase base = q_base<D>(p, cache_head(p, kvh));
 
+    // the chunk ranges, and the block-table entries of the pair ring's first two fills,
+    // loaded before the q staging so that their round trip overlaps its own (clamped at use)
+    const int r_hi = min(w_hi, c_full);  // fully valid chunks [w_lo, r_hi)
+    const int c_first = (w_lo & 1) && w_lo < r_hi ? w_lo + 1 : w_lo;
+    // pairs [c_first, e_hi); an empty wave or split has r_hi < w_lo and runs nothing
+    const int e_hi = c_first + (max(r_hi - c_first, 0) & ~1);
+    const int last_pair = max(e_hi - 1, 0);
+    const int pg_raw0 = chunk_pages_raw<P>(p, b, min(c_first, last_pair), last_pair, kgs, vgs);
+    const int pg_raw1 =
+        chunk_pages_raw<P>(p, b, min(c_first + P, last_pair), last_pair, kgs, vgs);
+
     extern __shared__ __attribute__((aligned(16))) float smem[];
     const int r0 = quant_lds_region0(W, G, FMT, D);
     char* kst = (char*)smem + wave * Q::TILE;
@@ -1068,20 +1079,13 @@ __device__ __forceinline__ void q2_range(const DecodeParams& p, int kvh, int b, 
                                      corr);
     };
 
-    const int r_hi = min(w_hi, c_full);  // fully valid chunks [w_lo, r_hi)
-    int c_first = w_lo;
-    if ((w_lo & 1) && w_lo < r_hi) {
-        single(w_lo, 16);
-        c_first = w_lo + 1;
-    }
-    // pairs [c_first, e_hi); an empty wave or split has r_hi < w_lo and runs nothing
-    const int e_hi = c_first + (max(r_hi - c_first, 0) & ~1);
+    if (c_first != w_lo) single(w_lo, 16);
     if (c_first < e_hi) {
         const QLaneOff lo = lane_offsets<FMT, D>(p, i16, g, 15);
         const int last = e_hi - 1;
         ChunkQ<FMT, D> ring[P];
-        int pg_cur = chunk_pages<P>(p, b, c_first, last, kgs, vgs);
-        int pg_nxt = chunk_pages<P>(p, b, c_first + P, last, kgs, vgs);
+        int pg_cur = clamp_page(p, pg_raw0);
+        int pg_nxt = clamp_page(p, pg_raw1);
         // Issued slot by slot: a slot's loads moved behind a later slot's would make the
         // ring's waits (vmcnt counts the loads issued after the awaited one) drain it.
         // a pair's K group is its first chunk's: odd slots skip the K pair load
