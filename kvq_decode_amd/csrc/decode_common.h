@@ -355,6 +355,19 @@ __device__ __forceinline__ SegGuess unit_guess(const DecodeParams& p, int u, int
     return g;
 }
 
+// Makes the kernel arguments the start of a work-unit kernel reads available in SGPRs at
+// this point. The compiler otherwise issues each argument load in the block that first
+// uses it, and the start then waits on several dependent scalar-load round trips before
+// its first memory access; loaded together they take one. (An empty asm statement with
+// SGPR inputs: it emits no instruction.)
+__device__ __forceinline__ void load_unit_args(const DecodeParams& p) {
+    asm volatile("" ::"s"(p.q), "s"(p.q_sb), "s"(p.q_sh), "s"(p.bt), "s"(p.bt_sb),
+                 "s"(p.seq_lens));
+    asm volatile("" ::"s"(p.batch), "s"(p.kv_heads), "s"(p.group), "s"(p.block_size),
+                 "s"(p.max_blocks), "s"(p.xcd_group), "s"(p.units), "s"(p.kv_rep),
+                 "s"(p.cpp_shift));
+}
+
 // Runs fn(kvh, b, seq_len, w_lo, w_hi, part_base, part_stride, pf, first) for each segment
 // of this workgroup's unit (workgroup = (kv head, unit), W waves), in batch order, with a
 // barrier between segments (they reuse the LDS of the range functions). [w_lo, w_hi) is
@@ -375,19 +388,6 @@ __device__ __forceinline__ SegGuess unit_guess(const DecodeParams& p, int u, int
 // Workgroup order: plain (kv head fastest), or with xcd_group and units a multiple of
 // kXcds, grouped so that the kv heads of one unit share an XCD (workgroup i runs on XCD
 // i % kXcds) and with it the L2 lines of the V scales, which interleave kv heads.
-// Makes the kernel arguments the start of a work-unit kernel reads available in SGPRs at
-// this point. The compiler otherwise issues each argument load in the block that first
-// uses it, and the start then waits on several dependent scalar-load round trips before
-// its first memory access; loaded together they take one. (An empty asm statement with
-// SGPR inputs: it emits no instruction.)
-__device__ __forceinline__ void load_unit_args(const DecodeParams& p) {
-    asm volatile("" ::"s"(p.q), "s"(p.q_sb), "s"(p.q_sh), "s"(p.bt), "s"(p.bt_sb),
-                 "s"(p.seq_lens));
-    asm volatile("" ::"s"(p.batch), "s"(p.kv_heads), "s"(p.group), "s"(p.block_size),
-                 "s"(p.max_blocks), "s"(p.xcd_group), "s"(p.units), "s"(p.kv_rep),
-                 "s"(p.cpp_shift));
-}
-
 template <int W, typename Pre, typename Fn>
 __device__ __forceinline__ void for_unit_segments(const DecodeParams& p, Pre&& pre, Fn&& fn) {
     load_unit_args(p);
