@@ -148,6 +148,32 @@ __device__ __forceinline__ void emit_k_row(const QuantParams& p, int kvh, int c,
                 c, code);
 }
 
+// Min / max over aligned lane groups without LDS (exact operations, so the order of the
+// combination does not change the result): within a 16-lane row by DPP - quad_perm xor 1
+// and xor 2; row_half_mirror, where each quad already holds its own result, so lane i
+// meeting lane 7 - i combines the two quads of a half; row_ror:8 - and across rows by
+// v_permlane16_swap / v_permlane32_swap (xor 16 / xor 32), whose two results are the lane's
+// own value and its partner's.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+template <int O>  // xor lane offset 1, 2, 4 (within 8-lane halves), 8, 16 or 32
+__device__ __forceinline__ void minmax_xor(float& mn, float& mx) {
+    if constexpr (O == 16 || O == 32) {
+        const auto a = O == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(mn), __float_as_uint(mn), false, false)
+                               : __builtin_amdgcn_permlane32_swap(__float_as_uint(mn), __float_as_uint(mn), false, false);
+        const auto b = O == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false)
+                               : __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+        mn = fminf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+        mx = fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+    } else {
+        constexpr int CTRL = O == 1 ? 0xB1 : O == 2 ? 0x4E : O == 4 ? 0x141 : 0x128;
+        mn = fminf(mn, dpp<CTRL>(mn));
+        mx = fmaxf(mx, dpp<CTRL>(mx));
+    }
+}
+
 // K, bulk: one wave per (kv head, group, sequence), four groups per 256-thread workgroup.
 // Lane l owns channels 8c .. 8c + 7 (c = l % PC, PC = D/8 lanes per row: 16-byte loads) of
 // rows t0 + RPI j + l / PC (RPI = 64/PC rows per load instruction). Min / max run over the
@@ -208,12 +234,10 @@ __device__ __forceinline__ void quant_k_group(const QuantParams& p, int kvh, int
     }
     // the channel's RPI row groups: lanes c, c + PC, c + 2 PC, ...
 #pragma unroll
-    for (int o = PC; o < 64; o <<= 1) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            mn[e] = fminf(mn[e], __shfl_xor(mn[e], o));
-            mx[e] = fmaxf(mx[e], __shfl_xor(mx[e], o));
-        }
+    for (int e = 0; e < 8; ++e) {
+        if constexpr (PC <= 8) minmax_xor<8>(mn[e], mx[e]);
+        if constexpr (PC <= 16) minmax_xor<16>(mn[e], mx[e]);
+        minmax_xor<32>(mn[e], mx[e]);
     }
     ScaleZero q[8];
 #pragma unroll
@@ -290,11 +314,11 @@ __device__ __forceinline__ void quant_v_rows(const QuantParams& p, int kvh, int 
             mx = fmaxf(mx, x[e]);
         }
         // min / max over the row's LPR lanes (aligned lane groups of one wave)
-#pragma unroll
-        for (int o = 1; o < LPR; o <<= 1) {
-            mn = fminf(mn, __shfl_xor(mn, o, LPR));
-            mx = fmaxf(mx, __shfl_xor(mx, o, LPR));
-        }
+        minmax_xor<1>(mn, mx);
+        minmax_xor<2>(mn, mx);
+        minmax_xor<4>(mn, mx);
+        if constexpr (LPR >= 16) minmax_xor<8>(mn, mx);
+        if constexpr (LPR >= 32) minmax_xor<16>(mn, mx);
         const ScaleZero q = make_params<FMT>(mn, mx);
         uint32_t code[8];
 #pragma unroll
